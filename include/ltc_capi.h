@@ -1,0 +1,153 @@
+/*
+ * C-ABI of the MI355X (gfx950) LTC fused ODE-solver library, libltc_hip.so.
+ *
+ * This is the drop-in boundary that replaces the reference's pybind11
+ * extension `ltc_cuda_kernels_v2` (built at ltc_cuda.py:211-217 and called
+ * only from LTCCudaForward, ltc_cuda.py:270 and :331). Plain pointers and
+ * sizes, no torch types: any host (ctypes, cgo, JNI, N-API) can bind it.
+ *
+ * Conventions
+ *  - All tensors are fp32 device pointers on the current HIP device.
+ *  - Parameters are contiguous in the reference's own layouts:
+ *      recurrent (H,H) row-major [i][j], i presynaptic (ltc.py:22-26),
+ *      sensory   (D,H) row-major [d][h] (ltc.py:27-30),
+ *      per neuron (H).
+ *  - x (B,T,D) and grad_out (B,T,H) take explicit element strides, so
+ *    strided views (e.g. x[:,:,0::2]) and expanded gradients (stride 0) are
+ *    read in place.
+ *  - Every other output is written contiguous.
+ *  - The library allocates nothing. The caller passes a device workspace of
+ *    at least ltc_*_workspace_bytes() bytes, 256-byte aligned.
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ *    Calls return as soon as the work is queued.
+ *  - Return value: 0 on success; LTC_EINVAL for bad arguments (nothing is
+ *    launched), LTC_EUNSUPPORTED for shapes outside the supported range,
+ *    LTC_EHIP when a HIP call or launch fails. ltc_last_error() then holds a
+ *    message (thread-local).
+ *  - Results are deterministic: no atomics; every reduction has a fixed order.
+ */
+#ifndef LTC_CAPI_H
+#define LTC_CAPI_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTC_ABI_VERSION 1
+
+#define LTC_OK 0
+#define LTC_EINVAL 1
+#define LTC_EUNSUPPORTED 2
+#define LTC_EHIP 3
+
+/* Largest hidden size one persistent workgroup covers (Hp*KS <= 1024). */
+#define LTC_MAX_HIDDEN 1024
+
+/* ABI version of the loaded library (LTC_ABI_VERSION at build time). */
+int ltc_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ltc_last_error(void);
+
+/* Number of visible HIP devices; 0 on a host without a GPU or driver. The
+ * Python loader uses it to decide whether the extension can serve calls
+ * (the reference probes torch.cuda.is_available(), ltc_cuda.py:142). */
+int ltc_device_count(void);
+
+/* Floats in the `saved` buffer that ltc_full_forward fills for backward:
+ * the pre-state of every unfold plus the final state, and every unfold's
+ * denominator. It replaces the reference's v_buffers_stacked (T,U,B,H) and
+ * w_num/w_den_sens_stacked (T,B,H) (csrc/ltc_kernels.cu:1207-1211). */
+long long ltc_saved_floats(int B, int T, int H, int ode_unfolds);
+
+/* Workspace sizes in bytes for one forward / backward call. */
+long long ltc_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds);
+long long ltc_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds);
+
+/*
+ * Whole forward time loop. Replaces ltc_full_forward
+ * (csrc/ltc_kernels.cu:1165-1182, bound at ltc_cuda.py:270-276).
+ *   x            (B,T,D) with element strides sxb, sxt, sxd
+ *   state        (B,H) initial state, contiguous; never written
+ *   w_pos .. vleak  the 11 boundary parameters, in the reference's argument
+ *                order (ltc_cuda.py:249-263)
+ *   out          (B,T,H) outputs
+ *   h_final      (B,H) final state
+ *   saved        ltc_saved_floats() floats, written when save_intermediates
+ *                is nonzero (training); may be NULL otherwise
+ * Unlike the reference (which swaps the roles of its transposed copies), the
+ * parameters are read in place: no transposed copies are returned.
+ */
+int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd,
+                     const float* state,
+                     const float* w_pos, const float* w_erev, const float* mu,
+                     const float* sigma,
+                     const float* sensory_mu, const float* sensory_sigma,
+                     const float* sensory_erev, const float* sensory_w_pos,
+                     const float* cm_t, const float* gleak_pos, const float* vleak,
+                     int B, int T, int D, int H, int ode_unfolds, float epsilon,
+                     int save_intermediates,
+                     float* out, float* h_final, float* saved,
+                     void* workspace, long long workspace_bytes, void* stream);
+
+/*
+ * Whole backward time loop. Replaces ltc_full_backward
+ * (csrc/ltc_kernels.cu:962-984, bound at ltc_cuda.py:331-339).
+ *   x, parameters  as given to the forward
+ *   saved          the buffer the forward filled
+ *   grad_out       (B,T,H) dL/d out with element strides sgb, sgt, sgh
+ *   grad_h_final   (B,H) dL/d h_final, contiguous, or NULL for zero
+ *                  (the reference substitutes zeros, ltc_cuda.py:326-328)
+ * Outputs, all contiguous, in Function-input order (ltc_cuda.py:342-355):
+ *   grad_x (B,T,D), grad_state (B,H), grad_w_pos, grad_w_erev, grad_mu,
+ *   grad_sigma (H,H), grad_sensory_mu, grad_sensory_sigma,
+ *   grad_sensory_erev, grad_sensory_w_pos (D,H), grad_cm_t, grad_gleak_pos,
+ *   grad_vleak (H).
+ */
+int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sxd,
+                      const float* w_pos, const float* w_erev, const float* mu,
+                      const float* sigma,
+                      const float* sensory_mu, const float* sensory_sigma,
+                      const float* sensory_erev, const float* sensory_w_pos,
+                      const float* cm_t, const float* gleak_pos, const float* vleak,
+                      const float* saved,
+                      const float* grad_out, long long sgb, long long sgt, long long sgh,
+                      const float* grad_h_final,
+                      int B, int T, int D, int H, int ode_unfolds, float epsilon,
+                      float* grad_x, float* grad_state,
+                      float* grad_w_pos, float* grad_w_erev, float* grad_mu,
+                      float* grad_sigma,
+                      float* grad_sensory_mu, float* grad_sensory_sigma,
+                      float* grad_sensory_erev, float* grad_sensory_w_pos,
+                      float* grad_cm_t, float* grad_gleak_pos, float* grad_vleak,
+                      void* workspace, long long workspace_bytes, void* stream);
+
+/*
+ * Launch plan of one call, for diagnostics and host-side bounds tests. No
+ * counterpart in the reference. Writes up to n of: Hp, Dp, NB (batch rows
+ * per ODE workgroup), KS (reduction split), RC (= Hp/KS), threads per ODE
+ * workgroup, forward LDS bytes, backward LDS bytes, NCH (recurrent gradient
+ * chunks), NRC (sensory backward row chunks), ODE workgroups. Returns the
+ * number of values written, or -1 for invalid sizes.
+ */
+#define LTC_PLAN_FIELDS 11
+int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
+
+/*
+ * Per-kernel event timing. No counterpart in the reference, whose bench
+ * times with torch.cuda.Event around whole calls (bench_ltc.py:39-96).
+ * While enabled, every kernel this library launches is bracketed by HIP
+ * events recorded on the launch stream; ltc_timing_read() waits for them and
+ * returns the summed duration and launch count of one kernel id.
+ * ltc_timing_enable() clears the accumulators.
+ */
+int ltc_timing_enable(int on);
+int ltc_timing_read(int kernel_id, double* total_ms, long long* launches);
+int ltc_kernel_count(void);
+const char* ltc_kernel_name(int kernel_id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTC_CAPI_H */

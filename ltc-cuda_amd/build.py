@@ -1,0 +1,69 @@
+"""Compile libltc_hip.so (the C-ABI library) for gfx950 with hipcc, in-tree.
+
+Usage:  python ltc-cuda_amd/build.py [--verbose]
+
+The library is linked against the HIP runtime by SONAME only (no rpath), so
+a process that has already imported torch resolves it to torch's bundled
+libamdhip64.so.7 and only one HIP runtime is ever mapped.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIB_NAME = "libltc_hip.so"
+LIB_PATH = os.path.join(HERE, LIB_NAME)
+SOURCES = ("ltc_device.hip", "ltc_capi.hip")
+ARCH = os.environ.get("LTC_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc_path() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.isfile(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def command(out: str = LIB_PATH) -> list:
+    return [
+        hipcc_path(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-mcode-object-version=5",
+        # Resolve libamdhip64.so.7 by SONAME (torch's copy once torch is loaded).
+        "-fno-rtlib-add-rpath",
+        # No packed-FP32 (v_pk_*_f32) instructions anywhere in device code.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-Wno-unused-command-line-argument",
+        "-o", out,
+        *[os.path.join(CSRC, s) for s in SOURCES],
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    tmp = LIB_PATH + ".tmp"
+    cmd = command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    msgs = [ln for ln in (proc.stdout + proc.stderr).splitlines() if noise not in ln]
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs), flush=True)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

@@ -1,0 +1,477 @@
+// C-ABI entry points of libltc_hip.so (declared in include/ltc_capi.h).
+// Validates arguments before touching the device, chooses the launch plan,
+// carves the caller's workspace and enqueues the kernels on the caller's
+// stream. Allocates no device memory.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/ltc_capi.h"
+#include "ltc_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+long long round_up(long long v, long long m) { return (v + m - 1) / m * m; }
+
+// ---------------------------------------------------------------------------
+// Launch plan
+// ---------------------------------------------------------------------------
+ltc::Plan make_plan(int B, int T, int D, int H, int U) {
+  ltc::Plan p{};
+  p.B = B;
+  p.T = T;
+  p.D = D;
+  p.H = H;
+  p.U = U;
+  p.Hp = (int)round_up(H > 0 ? H : 1, 64);
+  p.Dp = (int)round_up(D > 0 ? D : 1, 64);
+  // Rows per persistent workgroup: keep at least 256 workgroups (one per CU)
+  // while B allows, and reuse each synapse operand NB times otherwise.
+  p.NB = 1;
+  for (int nb : {16, 8, 4, 2}) {
+    if ((B + nb - 1) / nb >= 256) {
+      p.NB = nb;
+      break;
+    }
+  }
+  // Split of the reduction axis: as many waves as the thread bound allows,
+  // with LDS partials under 64 KiB and at least 4 synapses per thread. When
+  // even KS = 1 does not fit, fewer rows per workgroup.
+  auto lds_ok = [&](int nb, int k) {
+    const long long f = (long long)nb * p.Hp * 4 + (long long)k * nb * p.Hp * 8;
+    const long long b = (long long)nb * p.Hp * 8 + (long long)k * nb * p.Hp * 4;
+    return f <= 65536 && b <= 65536;
+  };
+  for (;;) {
+    // KS is a power of two <= 16, so it always divides Hp/4 (Hp is a multiple of 64).
+    const int cap = ltc::ode_max_threads(p.NB) / p.Hp;
+    int ks = 0;
+    for (int k = 16; k >= 1; k >>= 1) {
+      if (k <= cap) {
+        ks = k;
+        break;
+      }
+    }
+    while (ks > 1 && (!lds_ok(p.NB, ks) || p.Hp / ks < 4)) ks >>= 1;
+    if ((ks >= 1 && lds_ok(p.NB, ks)) || p.NB == 1) {
+      p.KS = ks < 1 ? 1 : ks;
+      break;
+    }
+    p.NB >>= 1;
+  }
+  p.RC = p.Hp / p.KS;
+  p.N = (long long)T * U * B;
+  // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
+  // unfold instances each, at most 64 partials per synapse.
+  {
+    const long long bpc = (long long)(p.Hp / 64) * (p.Hp / 32);
+    long long nch = (1024 + bpc - 1) / bpc;
+    if (nch > 64) nch = 64;
+    const long long cap = (p.N + 31) / 32;
+    if (nch > cap) nch = cap;
+    if (nch < 1) nch = 1;
+    const long long nper = (p.N + nch - 1) / nch;
+    p.NCH = (int)(nper > 0 ? (p.N + nper - 1) / nper : 1);
+    if (p.NCH < 1) p.NCH = 1;
+  }
+  // Sensory backward row chunks: same targets, at least 8 rows each.
+  {
+    const long long BT = (long long)B * T;
+    const long long bpc = (long long)(p.Dp / 64) * (p.Hp / 32);
+    long long nrc = (1024 + bpc - 1) / bpc;
+    if (nrc > 64) nrc = 64;
+    const long long cap = (BT + 7) / 8;
+    if (nrc > cap) nrc = cap;
+    if (nrc < 1) nrc = 1;
+    const long long per = (BT + nrc - 1) / nrc;
+    p.NRC = (int)(per > 0 ? (BT + per - 1) / per : 1);
+    if (p.NRC < 1) p.NRC = 1;
+  }
+  return p;
+}
+
+// Carves 256-byte aligned regions out of one workspace in a fixed order; the
+// same walk computes the total size (base == nullptr).
+struct Carver {
+  char* base;
+  long long off = 0;
+  template <class Tp>
+  Tp* take(long long count) {
+    const long long at = round_up(off, 256);
+    off = at + count * (long long)sizeof(Tp);
+    return base ? reinterpret_cast<Tp*>(base + at) : nullptr;
+  }
+};
+
+struct FwdWs {
+  ltc::Prepped pp;
+  float* sn;
+  float* sd;
+};
+
+FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
+  FwdWs w{};
+  w.pp.recF = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
+  w.pp.neuron = c.take<float>(3LL * p.Hp);
+  w.sn = c.take<float>((long long)p.B * p.T * p.Hp);
+  w.sd = c.take<float>((long long)p.B * p.T * p.Hp);
+  return w;
+}
+
+struct BwdWs {
+  ltc::Prepped pp;
+  float2* absave;
+  float* dsn;
+  float* dsd;
+  float* npart;
+  float* rpart;
+  float* spart;
+  float* dxpart;
+};
+
+BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
+  BwdWs w{};
+  w.pp.recF = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.recB = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
+  w.pp.neuron = c.take<float>(3LL * p.Hp);
+  w.absave = c.take<float2>(p.N * p.Hp);
+  w.dsn = c.take<float>((long long)p.B * p.T * p.Hp);
+  w.dsd = c.take<float>((long long)p.B * p.T * p.Hp);
+  w.npart = c.take<float>((long long)p.B * 3 * p.Hp);
+  w.rpart = c.take<float>((long long)p.NCH * 4 * p.Hp * p.Hp);
+  w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
+  w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
+  return w;
+}
+
+long long saved_floats(const ltc::Plan& p) {
+  // vsave: T*U+1 slots of (B,Hp); densave: T*U slots of (B,Hp).
+  return ((long long)p.T * p.U + 1) * p.B * p.Hp + (long long)p.T * p.U * p.B * p.Hp;
+}
+
+int check_dims(int B, int T, int D, int H, int U) {
+  if (B < 0 || T < 0 || D < 1 || H < 1)
+    return fail(LTC_EINVAL, "dimensions must satisfy B >= 0, T >= 0, D >= 1, H >= 1");
+  if (U < 1) return fail(LTC_EINVAL, "ode_unfolds must be >= 1");
+  if (H > LTC_MAX_HIDDEN)
+    return fail(LTC_EUNSUPPORTED, "hidden size H = " + std::to_string(H) + " exceeds " +
+                                      std::to_string(LTC_MAX_HIDDEN));
+  if ((long long)B * T * (D > H ? D : H) > (1LL << 40))
+    return fail(LTC_EUNSUPPORTED, "problem too large");
+  return LTC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Event timing
+// ---------------------------------------------------------------------------
+const char* const kNames[ltc::K_COUNT] = {"ltc_prep",     "ltc_sens_fwd", "ltc_ode_fwd",
+                                          "ltc_ode_bwd",  "ltc_rec_grad", "ltc_sens_bwd",
+                                          "ltc_finalize"};
+
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  struct Rec {
+    int id;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> pending;
+  std::vector<hipEvent_t> pool;
+  double total_ms[ltc::K_COUNT] = {};
+  long long count[ltc::K_COUNT] = {};
+
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+  void drain() {
+    for (auto& r : pending) {
+      float ms = 0.f;
+      if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+        total_ms[r.id] += ms;
+        count[r.id] += 1;
+      }
+      pool.push_back(r.a);
+      pool.push_back(r.b);
+    }
+    pending.clear();
+  }
+};
+
+Timing& timing() {
+  static Timing* t = new Timing();  // never destroyed: events may outlive static teardown
+  return *t;
+}
+
+// Runs one launch, bracketed by events when timing is enabled.
+template <class F>
+hipError_t timed(int id, hipStream_t s, F&& launch) {
+  Timing& tm = timing();
+  if (!tm.on) return launch();
+  hipEvent_t a = nullptr, b = nullptr;
+  {
+    std::lock_guard<std::mutex> g(tm.mu);
+    a = tm.get();
+    b = tm.get();
+  }
+  if (a) (void)hipEventRecord(a, s);
+  const hipError_t err = launch();
+  if (b) (void)hipEventRecord(b, s);
+  if (a && b) {
+    std::lock_guard<std::mutex> g(tm.mu);
+    tm.pending.push_back({id, a, b});
+  }
+  return err;
+}
+
+int hip_fail(const char* what, hipError_t e) {
+  return fail(LTC_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace
+
+extern "C" {
+
+int ltc_abi_version(void) { return LTC_ABI_VERSION; }
+
+const char* ltc_last_error(void) { return g_err.c_str(); }
+
+int ltc_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+long long ltc_saved_floats(int B, int T, int H, int ode_unfolds) {
+  if (B < 0 || T < 0 || H < 1 || ode_unfolds < 1) return -1;
+  return saved_floats(make_plan(B, T, 1, H, ode_unfolds));
+}
+
+long long ltc_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_fwd(p, c);
+  return round_up(c.off, 256);
+}
+
+long long ltc_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_bwd(p, c);
+  return round_up(c.off, 256);
+}
+
+int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd,
+                     const float* state, const float* w_pos, const float* w_erev,
+                     const float* mu, const float* sigma, const float* sensory_mu,
+                     const float* sensory_sigma, const float* sensory_erev,
+                     const float* sensory_w_pos, const float* cm_t, const float* gleak_pos,
+                     const float* vleak, int B, int T, int D, int H, int ode_unfolds,
+                     float epsilon, int save_intermediates, float* out, float* h_final,
+                     float* saved, void* workspace, long long workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_dims(B, T, D, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (!w_pos || !w_erev || !mu || !sigma || !sensory_mu || !sensory_sigma || !sensory_erev ||
+      !sensory_w_pos || !cm_t || !gleak_pos || !vleak)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (B > 0 && (!state || !h_final)) return fail(LTC_EINVAL, "state/h_final pointer is NULL");
+  if ((long long)B * T > 0 && (!x || !out)) return fail(LTC_EINVAL, "x/out pointer is NULL");
+  if (save_intermediates && !saved) return fail(LTC_EINVAL, "saved pointer is NULL");
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_fwd(p, need);
+  if (workspace_bytes < need.off || (need.off > 0 && !workspace))
+    return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
+  if (B == 0) return LTC_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (T == 0) {
+    // No steps: the final state is the initial state.
+    hipError_t e = hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
+                                  hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
+    return LTC_OK;
+  }
+
+  Carver c{static_cast<char*>(workspace)};
+  const FwdWs w = carve_fwd(p, c);
+  const ltc::RawParams rp{w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma, sensory_erev,
+                          sensory_w_pos, cm_t, gleak_pos, vleak};
+  const ltc::Strides3 xs{sxb, sxt, sxd};
+  float* vsave = save_intermediates ? saved : nullptr;
+  float* densave = save_intermediates ? saved + ((long long)T * ode_unfolds + 1) * B * p.Hp : nullptr;
+
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep(p, rp, w.pp, false, s); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = timed(ltc::K_SENS_FWD, s, [&] { return ltc::launch_sens_fwd(p, x, xs, w.pp, w.sn, w.sd, s); });
+  if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  e = timed(ltc::K_ODE_FWD, s, [&] {
+    return ltc::launch_ode_fwd(p, w.pp, w.sn, w.sd, state, epsilon, out, h_final, vsave, densave, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  return LTC_OK;
+}
+
+int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sxd,
+                      const float* w_pos, const float* w_erev, const float* mu,
+                      const float* sigma, const float* sensory_mu, const float* sensory_sigma,
+                      const float* sensory_erev, const float* sensory_w_pos, const float* cm_t,
+                      const float* gleak_pos, const float* vleak, const float* saved,
+                      const float* grad_out, long long sgb, long long sgt, long long sgh,
+                      const float* grad_h_final, int B, int T, int D, int H, int ode_unfolds,
+                      float epsilon, float* grad_x, float* grad_state, float* grad_w_pos,
+                      float* grad_w_erev, float* grad_mu, float* grad_sigma,
+                      float* grad_sensory_mu, float* grad_sensory_sigma,
+                      float* grad_sensory_erev, float* grad_sensory_w_pos, float* grad_cm_t,
+                      float* grad_gleak_pos, float* grad_vleak, void* workspace,
+                      long long workspace_bytes, void* stream) {
+  g_err.clear();
+  (void)epsilon;  // the saved denominators already include it
+  int rc = check_dims(B, T, D, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (!w_pos || !w_erev || !mu || !sigma || !sensory_mu || !sensory_sigma || !sensory_erev ||
+      !sensory_w_pos || !cm_t || !gleak_pos || !vleak)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (!grad_w_pos || !grad_w_erev || !grad_mu || !grad_sigma || !grad_sensory_mu ||
+      !grad_sensory_sigma || !grad_sensory_erev || !grad_sensory_w_pos || !grad_cm_t ||
+      !grad_gleak_pos || !grad_vleak)
+    return fail(LTC_EINVAL, "gradient output pointer is NULL");
+  if (B > 0 && !grad_state) return fail(LTC_EINVAL, "grad_state pointer is NULL");
+  if ((long long)B * T > 0 && (!x || !grad_out || !grad_x || !saved))
+    return fail(LTC_EINVAL, "x/grad_out/grad_x/saved pointer is NULL");
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_bwd(p, need);
+  if (workspace_bytes < need.off || (need.off > 0 && !workspace))
+    return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+
+  if ((long long)B * T == 0) {
+    // No unfolds: parameter gradients are zero and dL/dh0 = dL/dh_final.
+    float* zs[] = {grad_w_pos, grad_w_erev, grad_mu, grad_sigma};
+    for (float* z : zs) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zd[] = {grad_sensory_mu, grad_sensory_sigma, grad_sensory_erev, grad_sensory_w_pos};
+    for (float* z : zd) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zh[] = {grad_cm_t, grad_gleak_pos, grad_vleak};
+    for (float* z : zh) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    if (B > 0) {
+      hipError_t e = grad_h_final
+                         ? hipMemcpyAsync(grad_state, grad_h_final, (size_t)B * H * sizeof(float),
+                                          hipMemcpyDeviceToDevice, s)
+                         : hipMemsetAsync(grad_state, 0, (size_t)B * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("grad_state copy", e);
+    }
+    return LTC_OK;
+  }
+
+  Carver c{static_cast<char*>(workspace)};
+  const BwdWs w = carve_bwd(p, c);
+  const ltc::RawParams rp{w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma, sensory_erev,
+                          sensory_w_pos, cm_t, gleak_pos, vleak};
+  const ltc::Strides3 xs{sxb, sxt, sxd};
+  const ltc::Strides3 gs{sgb, sgt, sgh};
+  const float* vsave = saved;
+  const float* densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
+  const ltc::GradOut go{grad_x, grad_w_pos, grad_w_erev, grad_mu, grad_sigma, grad_sensory_mu,
+                        grad_sensory_sigma, grad_sensory_erev, grad_sensory_w_pos, grad_cm_t,
+                        grad_gleak_pos, grad_vleak};
+
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep(p, rp, w.pp, true, s); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = timed(ltc::K_ODE_BWD, s, [&] {
+    return ltc::launch_ode_bwd(p, w.pp, vsave, densave, grad_out, gs, grad_h_final, w.absave,
+                               w.dsn, w.dsd, w.npart, grad_state, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+  e = timed(ltc::K_REC_GRAD, s,
+            [&] { return ltc::launch_rec_grad(p, w.pp, vsave, w.absave, w.rpart, s); });
+  if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  e = timed(ltc::K_SENS_BWD, s, [&] {
+    return ltc::launch_sens_bwd(p, x, xs, w.pp, w.dsn, w.dsd, w.spart, w.dxpart, s);
+  });
+  if (e != hipSuccess) return hip_fail("sensory backward launch", e);
+  e = timed(ltc::K_FINALIZE, s, [&] {
+    return ltc::launch_finalize(p, rp, w.rpart, w.spart, w.dxpart, w.npart, go, s);
+  });
+  if (e != hipSuccess) return hip_fail("finalize launch", e);
+  return LTC_OK;
+}
+
+int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || !out || n < 0) return -1;
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  const long long v[LTC_PLAN_FIELDS] = {
+      p.Hp, p.Dp, p.NB, p.KS, p.RC, (long long)p.Hp * p.KS,
+      (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8,
+      (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4,
+      p.NCH, p.NRC, (B + p.NB - 1) / p.NB};
+  const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
+  for (int i = 0; i < m; ++i) out[i] = v[i];
+  return m;
+}
+
+int ltc_timing_enable(int on) {
+  Timing& tm = timing();
+  std::lock_guard<std::mutex> g(tm.mu);
+  tm.drain();
+  tm.on = on != 0;
+  for (int i = 0; i < ltc::K_COUNT; ++i) {
+    tm.total_ms[i] = 0.0;
+    tm.count[i] = 0;
+  }
+  return LTC_OK;
+}
+
+int ltc_timing_read(int kernel_id, double* total_ms, long long* launches) {
+  if (kernel_id < 0 || kernel_id >= ltc::K_COUNT || !total_ms || !launches)
+    return fail(LTC_EINVAL, "bad kernel id or NULL output");
+  Timing& tm = timing();
+  std::lock_guard<std::mutex> g(tm.mu);
+  tm.drain();
+  *total_ms = tm.total_ms[kernel_id];
+  *launches = tm.count[kernel_id];
+  return LTC_OK;
+}
+
+int ltc_kernel_count(void) { return ltc::K_COUNT; }
+
+const char* ltc_kernel_name(int kernel_id) {
+  if (kernel_id < 0 || kernel_id >= ltc::K_COUNT) return "";
+  return kNames[kernel_id];
+}
+
+}  // extern "C"

@@ -1,0 +1,820 @@
+// gfx950 kernels for the LTC fused ODE-solver path.
+//
+// Math (restated from ltc.py:42-63; gradients as csrc/ltc_kernels.cu:627-667
+// and :323-338 compute them):
+//   sensory  sn[b,t,h] = sum_d Ws*sig(Ss*(x-Ms))*Es,  sd[b,t,h] = sum_d Ws*sig(...)
+//   unfold   a_ij = sig(S_ij*(v_i - M_ij))
+//            n_j = sum_i a_ij*WE_ij + sn_j,  q_j = sum_i a_ij*WP_ij + sd_j
+//            v_j <- (C_j*v_j + G_j*L_j + n_j) / (C_j + G_j + q_j + eps)
+//
+// Layout choices (all buffers in HBM, fp32):
+//  * Lanes of a wave run over the OUTPUT neuron and each thread loops over a
+//    slice of the reduction axis. Row-major [i][j] parameters are then read
+//    as one contiguous 1 KiB float4 line per wave, with no transpose for the
+//    forward and no cross-lane reduction inside the synapse loop.
+//  * The four per-synapse operands travel as one float4 {S', c', WE, WP}
+//    with S' = -S*log2(e) and c' = S*M*log2(e), so the gate is
+//    rcp(1 + exp2(fma(S', v, c'))): one FMA, one v_exp_f32, one add and one
+//    v_rcp_f32 per synapse.
+//  * The sensory term depends on x only, so it is computed for every (b,t)
+//    in one parallel pass before the sequential unfold loop.
+//  * The unfold loop runs in one persistent launch: a workgroup owns NB batch
+//    rows for all T*U unfolds, with the state in LDS and, when they fit,
+//    each thread's synapse operands in registers for the whole launch.
+//  * Backward: a reverse-time chain kernel produces dL/dv for every unfold
+//    and saves alpha/beta; parameter gradients are then reduced over
+//    (t,k,b) by separate kernels into partial buffers that a finalize kernel
+//    sums in a fixed order. No atomics anywhere, so every result is bitwise
+//    reproducible run to run.
+#include "ltc_internal.h"
+
+namespace ltc {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegLn2 = -0.69314718055994531f;
+
+// sigmoid(z) for zp = -z*log2(e). v_exp_f32 saturates to +inf for large zp
+// and rcp(inf) = 0, while exp2 of a large negative zp is 0 and rcp(1) = 1, so
+// both saturated limits are exact and a*(1-a) is 0 there (never inf/inf).
+__device__ __forceinline__ float gate(float zp) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zp));
+}
+
+// Workgroup barrier that orders LDS only. Global loads issued before it stay
+// in flight (no vmcnt(0) wait), which lets the next unfold's operands stream
+// in while the workgroup synchronises.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---------------------------------------------------------------------------
+// Parameter images (one launch, flat index space over three segments).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int H, int D,
+                                                   int Hp, int Dp, int bwd) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long nrec = (long long)Hp * Hp;
+  const long long nsens = (long long)Dp * Hp;
+  if (tid < nrec) {
+    const int i = (int)(tid / Hp), j = (int)(tid - (long long)i * Hp);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < H && j < H) {
+      const long long e = (long long)i * H + j;
+      const float S = rp.sigma[e], M = rp.mu[e];
+      v = make_float4(-S * kLog2e, S * M * kLog2e, rp.w_erev[e], rp.w_pos[e]);
+    }
+    pp.recF[tid] = v;
+    if (bwd) pp.recB[(long long)j * Hp + i] = v;
+    return;
+  }
+  tid -= nrec;
+  if (tid < nsens) {
+    const int d = (int)(tid / Hp), h = (int)(tid - (long long)d * Hp);
+    float4 f = make_float4(0.f, 0.f, 0.f, 0.f), g = f;
+    if (d < D && h < H) {
+      const long long e = (long long)d * H + h;
+      const float Ss = rp.s_sigma[e], Ms = rp.s_mu[e], Es = rp.s_erev[e], Ws = rp.s_wpos[e];
+      f = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * Es, Ws);
+      g = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Es, Ws * Ss);
+    }
+    if (bwd)
+      pp.sensB[(long long)h * Dp + d] = g;
+    else
+      pp.sensF[tid] = f;
+    return;
+  }
+  tid -= nsens;
+  if (tid < 3LL * Hp) {
+    const int q = (int)(tid / Hp), j = (int)(tid - (long long)q * Hp);
+    const float* src = q == 0 ? rp.cm : (q == 1 ? rp.gleak : rp.vleak);
+    pp.neuron[tid] = j < H ? src[j] : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sensory forward for all (b,t) rows at once.
+// grid (Hp/64, ceil(BT / (4*RPW))), block 256: lane -> h, wave -> RPW rows.
+// Each float4 operand read from HBM/L2 is reused for RPW rows in registers;
+// x is staged through LDS 64 inputs at a time and read as a broadcast.
+// ---------------------------------------------------------------------------
+template <int RPW>
+__global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__ x, Strides3 xs,
+                                                       int T, int D, int BT, int Hp,
+                                                       const float4* __restrict__ sensF,
+                                                       float* __restrict__ sn,
+                                                       float* __restrict__ sd) {
+  constexpr int ROWS = 4 * RPW;
+  constexpr int XLD = ROWS + 4;  // keeps each staged row 16-byte aligned
+  __shared__ __align__(16) float xsh[64 * XLD];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane;
+  const int row0 = blockIdx.y * ROWS;
+  float an[RPW], ad[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
+
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    for (int e = threadIdx.x; e < 64 * ROWS; e += 256) {
+      const int r = e >> 6, dd = e & 63;
+      const int row = row0 + r, d = d0 + dd;
+      float v = 0.f;
+      if (row < BT && d < D) {
+        const int b = row / T, t = row - b * T;
+        v = x[b * xs.b + t * xs.t + d * xs.c];
+      }
+      xsh[dd * XLD + r] = v;
+    }
+    __syncthreads();
+    const int dn = min(64, D - d0);
+    const float4* pcol = sensF + (long long)d0 * Hp + h;
+#pragma unroll 4
+    for (int dd = 0; dd < dn; ++dd) {
+      const float4 p = pcol[(long long)dd * Hp];
+      const float* xr = xsh + dd * XLD + w * RPW;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const float a = gate(fmaf(p.x, xr[r], p.y));
+        an[r] = fmaf(a, p.z, an[r]);
+        ad[r] = fmaf(a, p.w, ad[r]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int row = row0 + w * RPW + r;
+    if (row < BT) {
+      sn[(long long)row * Hp + h] = an[r];
+      sd[(long long)row * Hp + h] = ad[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent forward unfold loop.
+// One workgroup owns NB batch rows for all T*U unfolds. blockDim = Hp*KS:
+// thread (o = tid % Hp, ks = tid / Hp) accumulates the partial n_o, q_o over
+// presynaptic i in [ks*RC, ks*RC + RC) for every row; partials meet in LDS
+// and thread (o, ks) finishes rows b = ks, ks+KS, ... of column o.
+// RCP > 0: the RC = RCP float4 operands of the thread live in registers.
+// ---------------------------------------------------------------------------
+struct FwdK {
+  const float4* recF;
+  const float* neuron;
+  const float* sn;
+  const float* sd;
+  const float* state0;
+  float* out;
+  float* hfin;
+  float* vsave;
+  float* densave;
+  int B, T, H, Hp, U, KS, RC;
+  float eps;
+};
+
+template <int NB>
+__device__ __forceinline__ void fwd_synapse(const float4 p, const float* vs, int Hp, int r,
+                                            float* na, float* qa) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float a = gate(fmaf(p.x, vs[b * Hp + r], p.y));
+    na[b] = fmaf(a, p.z, na[b]);
+    qa[b] = fmaf(a, p.w, qa[b]);
+  }
+}
+
+template <int NB, int RCP>
+__global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
+  extern __shared__ float4 lds4[];
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
+  const int RC = RCP > 0 ? RCP : k.RC;
+  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp]
+  float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][Hp]
+  const int tid = threadIdx.x;
+  const int ks = tid / Hp, o = tid - ks * Hp;
+  const int b0 = blockIdx.x * NB;
+  const int r0 = ks * RC;
+
+  const float C = k.neuron[o], G = k.neuron[Hp + o], L = k.neuron[2 * Hp + o];
+  const float GL = G * L, CG = C + G;
+
+  float4 preg[RCP > 0 ? RCP : 1];
+  if constexpr (RCP > 0) {
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * Hp + o];
+  }
+
+  for (int e = tid; e < NB * Hp; e += blockDim.x) {
+    const int b = e / Hp, j = e - b * Hp;
+    vs[e] = (b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j] : 0.f;
+  }
+  lds_barrier();
+
+  for (int t = 0; t < T; ++t) {
+    float snr[NB], sdr[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      const int b = ks + m * KS;
+      snr[m] = sdr[m] = 0.f;
+      if (b < NB && b0 + b < B) {
+        const long long e = ((long long)(b0 + b) * T + t) * Hp + o;
+        snr[m] = k.sn[e];
+        sdr[m] = k.sd[e];
+      }
+    }
+    for (int u = 0; u < U; ++u) {
+      float na[NB], qa[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) na[b] = qa[b] = 0.f;
+      if constexpr (RCP > 0) {
+#pragma unroll
+        for (int rr = 0; rr < RCP; ++rr) fwd_synapse<NB>(preg[rr], vs, Hp, r0 + rr, na, qa);
+      } else {
+        const float4* pc = k.recF + (long long)r0 * Hp + o;
+#pragma unroll 4
+        for (int rr = 0; rr < RC; ++rr) fwd_synapse<NB>(pc[(long long)rr * Hp], vs, Hp, r0 + rr, na, qa);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
+      lds_barrier();
+#pragma unroll
+      for (int m = 0; m < NB; ++m) {
+        const int b = ks + m * KS;
+        if (b < NB) {
+          float n = 0.f, q = 0.f;
+          for (int s = 0; s < KS; ++s) {
+            const float2 rv = red[(s * NB + b) * Hp + o];
+            n += rv.x;
+            q += rv.y;
+          }
+          const float vold = vs[b * Hp + o];
+          const float den = CG + (q + sdr[m]) + k.eps;
+          const float num = C * vold + GL + (n + snr[m]);
+          const float vnew = o < H ? num / den : 0.f;
+          const bool live = b0 + b < B;
+          if (k.vsave != nullptr && live) {
+            const long long e = ((long long)(t * U + u) * B + b0 + b) * Hp + o;
+            k.vsave[e] = vold;
+            k.densave[e] = den;
+          }
+          vs[b * Hp + o] = vnew;
+          if (u == U - 1 && live && o < H) k.out[((long long)(b0 + b) * T + t) * H + o] = vnew;
+        }
+      }
+      lds_barrier();
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < NB; ++m) {
+    const int b = ks + m * KS;
+    if (b < NB && b0 + b < B) {
+      const float v = vs[b * Hp + o];
+      if (o < H) k.hfin[(long long)(b0 + b) * H + o] = v;
+      if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0 + b) * Hp + o] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent reverse-time chain: dL/dv for every unfold.
+// Same thread layout as the forward with the roles swapped: o is the
+// presynaptic neuron i whose gradient is being formed and the thread loops
+// over postsynaptic j in [ks*RC, ks*RC + RC), reading the transposed image
+// recB[j][i]. alpha_j, beta_j of each unfold are broadcast through LDS.
+// ---------------------------------------------------------------------------
+struct BwdK {
+  const float4* recB;
+  const float* neuron;
+  const float* vsave;
+  const float* densave;
+  const float* gout;
+  Strides3 gs;
+  const float* ghfin;
+  float2* absave;
+  float* dsn;
+  float* dsd;
+  float* npart;
+  float* gstate;
+  int B, T, H, Hp, U, KS, RC;
+};
+
+template <int NB>
+__device__ __forceinline__ void bwd_synapse(const float4 p, const float2* ab, int Hp, int r,
+                                            const float* vi, float* acc) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float2 c = ab[b * Hp + r];
+    const float a = gate(fmaf(p.x, vi[b], p.y));
+    const float a2 = fmaf(-a, a, a);
+    const float hh = fmaf(c.x, p.z, c.y * p.w);
+    acc[b] = fmaf(hh * a2, p.x, acc[b]);
+  }
+}
+
+template <int NB, int RCP>
+__global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
+  extern __shared__ float4 lds4[];
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
+  const int RC = RCP > 0 ? RCP : k.RC;
+  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
+  float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][Hp]
+  const int tid = threadIdx.x;
+  const int ks = tid / Hp, o = tid - ks * Hp;
+  const int b0 = blockIdx.x * NB;
+  const int r0 = ks * RC;
+  const long long BHp = (long long)B * Hp;
+  const float C = k.neuron[o];
+
+  float4 preg[RCP > 0 ? RCP : 1];
+  if constexpr (RCP > 0) {
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + o];
+  }
+
+  float g[NB], pC[NB], pGv[NB], pA[NB];
+#pragma unroll
+  for (int m = 0; m < NB; ++m) {
+    const int b = ks + m * KS;
+    g[m] = 0.f;
+    pC[m] = pGv[m] = pA[m] = 0.f;
+    if (k.ghfin != nullptr && b < NB && b0 + b < B && o < H) g[m] = k.ghfin[(long long)(b0 + b) * H + o];
+  }
+
+  for (int t = T - 1; t >= 0; --t) {
+    float accA[NB], accB[NB];
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      const int b = ks + m * KS;
+      accA[m] = accB[m] = 0.f;
+      if (b < NB && b0 + b < B && o < H)
+        g[m] += k.gout[(b0 + b) * k.gs.b + t * k.gs.t + o * k.gs.c];
+    }
+    for (int u = U - 1; u >= 0; --u) {
+      const long long n = (long long)t * U + u;
+      float vi[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) vi[b] = b0 + b < B ? k.vsave[(n * B + b0 + b) * Hp + o] : 0.f;
+      float gdir[NB];
+#pragma unroll
+      for (int m = 0; m < NB; ++m) {
+        const int b = ks + m * KS;
+        gdir[m] = 0.f;
+        if (b < NB) {
+          float al = 0.f, be = 0.f;
+          const bool live = b0 + b < B;
+          if (live && o < H) {
+            const long long e = (n * B + b0 + b) * Hp + o;
+            const float den = k.densave[e];
+            const float vk = k.vsave[e];
+            const float vk1 = k.vsave[e + BHp];
+            const float rden = 1.0f / den;
+            al = g[m] * rden;
+            be = -g[m] * vk1 * rden;
+            accA[m] += al;
+            accB[m] += be;
+            pC[m] += al * (vk - vk1);
+            pGv[m] += al * vk1;
+            pA[m] += al;
+            gdir[m] = al * C;
+          }
+          ab[b * Hp + o] = make_float2(al, be);
+          if (live) k.absave[(n * B + b0 + b) * Hp + o] = make_float2(al, be);
+        }
+      }
+      lds_barrier();
+      float acc[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+      if constexpr (RCP > 0) {
+#pragma unroll
+        for (int rr = 0; rr < RCP; ++rr) bwd_synapse<NB>(preg[rr], ab, Hp, r0 + rr, vi, acc);
+      } else {
+        const float4* pc = k.recB + (long long)r0 * Hp + o;
+#pragma unroll 4
+        for (int rr = 0; rr < RC; ++rr) bwd_synapse<NB>(pc[(long long)rr * Hp], ab, Hp, r0 + rr, vi, acc);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = acc[b];
+      lds_barrier();
+#pragma unroll
+      for (int m = 0; m < NB; ++m) {
+        const int b = ks + m * KS;
+        if (b < NB) {
+          float s = 0.f;
+          for (int q = 0; q < KS; ++q) s += red[(q * NB + b) * Hp + o];
+          g[m] = o < H ? fmaf(kNegLn2, s, gdir[m]) : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < NB; ++m) {
+      const int b = ks + m * KS;
+      if (b < NB && b0 + b < B) {
+        const long long e = ((long long)(b0 + b) * T + t) * Hp + o;
+        k.dsn[e] = accA[m];
+        k.dsd[e] = accB[m];
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < NB; ++m) {
+    const int b = ks + m * KS;
+    if (b < NB && b0 + b < B) {
+      if (o < H) k.gstate[(long long)(b0 + b) * H + o] = g[m];
+      float* np = k.npart + (long long)(b0 + b) * 3 * Hp + o;
+      np[0] = pC[m];
+      np[Hp] = pGv[m];
+      np[2 * Hp] = pA[m];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Recurrent parameter gradients, reduced over n = (t,k,b).
+// grid (Hp/64, Hp/32, NCH), block 256: lane -> j, wave w -> 8 presynaptic i.
+// Per synapse and n:  a = gate, a2 = a(1-a), h = alpha*WE + beta*WP,
+//   sWE += alpha*a, sWP += beta*a, sD += h*a2, sDv += h*a2*v_i
+// and the finalize kernel forms dM = -S*sD and dS = sDv - M*sD.
+// ---------------------------------------------------------------------------
+constexpr int RG_NT = 32;
+
+struct RecGK {
+  const float4* recF;
+  const float* vsave;
+  const float2* absave;
+  float* rpart;
+  int Hp;
+  long long N, nper;
+};
+
+__global__ __launch_bounds__(256) void rec_grad_kernel(RecGK k) {
+  __shared__ __align__(16) float vsh[RG_NT][32];
+  __shared__ __align__(16) float2 absh[RG_NT][64];
+  const int Hp = k.Hp;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int jb = blockIdx.x * 64, ib = blockIdx.y * 32;
+  const int j = jb + lane, i0 = ib + w * 8;
+  float4 p[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ++ii) p[ii] = k.recF[(long long)(i0 + ii) * Hp + j];
+  float sWE[8], sWP[8], sD[8], sDv[8];
+#pragma unroll
+  for (int ii = 0; ii < 8; ++ii) sWE[ii] = sWP[ii] = sD[ii] = sDv[ii] = 0.f;
+
+  const long long nb = (long long)blockIdx.z * k.nper;
+  const long long ne = min(k.N, nb + k.nper);
+  for (long long n0 = nb; n0 < ne; n0 += RG_NT) {
+    for (int e = threadIdx.x; e < RG_NT * 32; e += 256) {
+      const int nn = e >> 5, ii = e & 31;
+      const long long n = n0 + nn;
+      vsh[nn][ii] = n < ne ? k.vsave[n * Hp + ib + ii] : 0.f;
+    }
+    for (int e = threadIdx.x; e < RG_NT * 64; e += 256) {
+      const int nn = e >> 6, jj = e & 63;
+      const long long n = n0 + nn;
+      absh[nn][jj] = n < ne ? k.absave[n * Hp + jb + jj] : make_float2(0.f, 0.f);
+    }
+    __syncthreads();
+    const int cnt = (int)min((long long)RG_NT, ne - n0);
+    for (int nn = 0; nn < cnt; ++nn) {
+      const float2 c = absh[nn][lane];
+      const float4 va = *reinterpret_cast<const float4*>(&vsh[nn][w * 8]);
+      const float4 vb = *reinterpret_cast<const float4*>(&vsh[nn][w * 8 + 4]);
+      const float v[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+      for (int ii = 0; ii < 8; ++ii) {
+        const float a = gate(fmaf(p[ii].x, v[ii], p[ii].y));
+        const float a2 = fmaf(-a, a, a);
+        sWE[ii] = fmaf(c.x, a, sWE[ii]);
+        sWP[ii] = fmaf(c.y, a, sWP[ii]);
+        const float dl = fmaf(c.x, p[ii].z, c.y * p[ii].w) * a2;
+        sD[ii] += dl;
+        sDv[ii] = fmaf(dl, v[ii], sDv[ii]);
+      }
+    }
+    __syncthreads();
+  }
+  const long long HH = (long long)Hp * Hp;
+  float* out = k.rpart + (long long)blockIdx.z * 4 * HH;
+#pragma unroll
+  for (int ii = 0; ii < 8; ++ii) {
+    const long long e = (long long)(i0 + ii) * Hp + j;
+    out[e] = sWE[ii];
+    out[HH + e] = sWP[ii];
+    out[2 * HH + e] = sD[ii];
+    out[3 * HH + e] = sDv[ii];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sensory backward over all (b,t) rows.
+// grid (Dp/64, Hp/32, NRC), block 256: lane -> d, wave w -> 8 neurons h.
+// With A = dL/dsn, Bq = dL/dsd, gamma = A*Es + Bq, a2 = a(1-a):
+//   s1 += gamma*a, s2 += A*a, s3 += gamma*a2, s4 += gamma*a2*x,
+//   dx_d += gamma*a2*Ws*Ss   (summed over h; waves meet in LDS, h-blocks in
+//   the finalize kernel).
+// Finalize: dWs = s1, dEs = Ws*s2, dMs = -Ss*Ws*s3, dSs = Ws*(s4 - Ms*s3).
+// ---------------------------------------------------------------------------
+constexpr int SB_RT = 32;
+
+struct SensBK {
+  const float* x;
+  Strides3 xs;
+  const float4* sensB;
+  const float* dsn;
+  const float* dsd;
+  float* spart;
+  float* dxpart;
+  int T, D, Dp, Hp, BT, rows_per;
+};
+
+__global__ __launch_bounds__(256) void sens_bwd_kernel(SensBK k) {
+  __shared__ __align__(16) float2 absh[SB_RT][32];
+  __shared__ float xsh[SB_RT][64];
+  __shared__ float dxr[4][SB_RT][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int db = blockIdx.x * 64, hb = blockIdx.y;
+  const int d = db + lane, h0 = hb * 32 + w * 8;
+  const int Dp = k.Dp, Hp = k.Hp;
+  float4 q[8];
+#pragma unroll
+  for (int hh = 0; hh < 8; ++hh) q[hh] = k.sensB[(long long)(h0 + hh) * Dp + d];
+  float s1[8], s2[8], s3[8], s4[8];
+#pragma unroll
+  for (int hh = 0; hh < 8; ++hh) s1[hh] = s2[hh] = s3[hh] = s4[hh] = 0.f;
+
+  const int rb = blockIdx.z * k.rows_per;
+  const int re = min(k.BT, rb + k.rows_per);
+  for (int r0 = rb; r0 < re; r0 += SB_RT) {
+    const int cnt = min(SB_RT, re - r0);
+    for (int e = threadIdx.x; e < SB_RT * 32; e += 256) {
+      const int rr = e >> 5, hh = e & 31;
+      const int row = r0 + rr;
+      float2 v = make_float2(0.f, 0.f);
+      if (rr < cnt) {
+        const long long ix = (long long)row * Hp + hb * 32 + hh;
+        v = make_float2(k.dsn[ix], k.dsd[ix]);
+      }
+      absh[rr][hh] = v;
+    }
+    for (int e = threadIdx.x; e < SB_RT * 64; e += 256) {
+      const int rr = e >> 6, dd = e & 63;
+      const int row = r0 + rr, dg = db + dd;
+      float v = 0.f;
+      if (rr < cnt && dg < k.D) {
+        const int b = row / k.T, t = row - b * k.T;
+        v = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      }
+      xsh[rr][dd] = v;
+    }
+    __syncthreads();
+    for (int rr = 0; rr < cnt; ++rr) {
+      const float xv = xsh[rr][lane];
+      float dxp = 0.f;
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh) {
+        const float2 c = absh[rr][w * 8 + hh];
+        const float a = gate(fmaf(q[hh].x, xv, q[hh].y));
+        const float a2 = fmaf(-a, a, a);
+        const float gm = fmaf(c.x, q[hh].z, c.y);
+        s1[hh] = fmaf(gm, a, s1[hh]);
+        s2[hh] = fmaf(c.x, a, s2[hh]);
+        const float ga2 = gm * a2;
+        s3[hh] += ga2;
+        s4[hh] = fmaf(ga2, xv, s4[hh]);
+        dxp = fmaf(ga2, q[hh].w, dxp);
+      }
+      dxr[w][rr][lane] = dxp;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < cnt * 64; e += 256) {
+      const int rr = e >> 6, dd = e & 63;
+      const float s = dxr[0][rr][dd] + dxr[1][rr][dd] + dxr[2][rr][dd] + dxr[3][rr][dd];
+      k.dxpart[((long long)hb * k.BT + r0 + rr) * Dp + db + dd] = s;
+    }
+    __syncthreads();
+  }
+  const long long DH = (long long)Dp * Hp;
+  float* out = k.spart + (long long)blockIdx.z * 4 * DH;
+#pragma unroll
+  for (int hh = 0; hh < 8; ++hh) {
+    const long long e = (long long)(h0 + hh) * Dp + d;
+    out[e] = s1[hh];
+    out[DH + e] = s2[hh];
+    out[2 * DH + e] = s3[hh];
+    out[3 * DH + e] = s4[hh];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Finalize: fixed-order sums of every partial buffer, then the closed forms.
+// Flat index space: (H*H recurrent) + (D*H sensory) + (H neurons) + (BT*D x).
+// ---------------------------------------------------------------------------
+struct FinK {
+  RawParams rp;
+  const float* rpart;
+  const float* spart;
+  const float* dxpart;
+  const float* npart;
+  GradOut g;
+  int B, D, H, Hp, Dp, NCH, NRC, HB, BT;
+};
+
+__global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
+  const long long nrec = (long long)H * H, nsens = (long long)D * H;
+  if (tid < nrec) {
+    const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
+    const long long HH = (long long)Hp * Hp;
+    const float* src = k.rpart + (long long)i * Hp + j;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    for (int z = 0; z < k.NCH; ++z) {
+      const float* pz = src + (long long)z * 4 * HH;
+      s0 += pz[0];
+      s1 += pz[HH];
+      s2 += pz[2 * HH];
+      s3 += pz[3 * HH];
+    }
+    k.g.w_erev[tid] = s0;
+    k.g.w_pos[tid] = s1;
+    k.g.mu[tid] = -k.rp.sigma[tid] * s2;
+    k.g.sigma[tid] = s3 - k.rp.mu[tid] * s2;
+    return;
+  }
+  tid -= nrec;
+  if (tid < nsens) {
+    // h-major walk so the partial reads are contiguous in d
+    const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
+    const long long DH = (long long)Dp * Hp;
+    const float* src = k.spart + (long long)h * Dp + d;
+    float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+    for (int z = 0; z < k.NRC; ++z) {
+      const float* pz = src + (long long)z * 4 * DH;
+      s1 += pz[0];
+      s2 += pz[DH];
+      s3 += pz[2 * DH];
+      s4 += pz[3 * DH];
+    }
+    const long long e = (long long)d * H + h;
+    const float Ws = k.rp.s_wpos[e], Ss = k.rp.s_sigma[e], Ms = k.rp.s_mu[e];
+    k.g.s_wpos[e] = s1;
+    k.g.s_erev[e] = Ws * s2;
+    k.g.s_mu[e] = -Ss * Ws * s3;
+    k.g.s_sigma[e] = Ws * (s4 - Ms * s3);
+    return;
+  }
+  tid -= nsens;
+  if (tid < H) {
+    const int j = (int)tid;
+    float c = 0.f, gv = 0.f, ga = 0.f;
+    for (int b = 0; b < k.B; ++b) {
+      const float* np = k.npart + (long long)b * 3 * Hp + j;
+      c += np[0];
+      gv += np[Hp];
+      ga += np[2 * Hp];
+    }
+    k.g.cm[j] = c;
+    k.g.gleak[j] = k.rp.vleak[j] * ga - gv;
+    k.g.vleak[j] = k.rp.gleak[j] * ga;
+    return;
+  }
+  tid -= H;
+  if (tid < (long long)k.BT * D) {
+    const long long row = tid / D;
+    const int d = (int)(tid - row * D);
+    float s = 0.f;
+    for (int hb = 0; hb < k.HB; ++hb) s += k.dxpart[((long long)hb * k.BT + row) * Dp + d];
+    k.g.x[tid] = s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Template dispatch helpers.
+// ---------------------------------------------------------------------------
+size_t fwd_lds_bytes(const Plan& p) {
+  return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * p.Hp * 8;
+}
+size_t bwd_lds_bytes(const Plan& p) {
+  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KS * p.NB * p.Hp * 4;
+}
+
+template <int NB>
+hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
+  const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
+  const size_t lds = fwd_lds_bytes(p);
+  const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
+  switch (rcp) {
+    case 4: hipLaunchKernelGGL((ode_fwd_kernel<NB, 4>), grid, block, lds, s, a); break;
+    case 8: hipLaunchKernelGGL((ode_fwd_kernel<NB, 8>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((ode_fwd_kernel<NB, 16>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((ode_fwd_kernel<NB, 0>), grid, block, lds, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+template <int NB>
+hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
+  const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
+  const size_t lds = bwd_lds_bytes(p);
+  const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
+  switch (rcp) {
+    case 4: hipLaunchKernelGGL((ode_bwd_kernel<NB, 4>), grid, block, lds, s, a); break;
+    case 8: hipLaunchKernelGGL((ode_bwd_kernel<NB, 8>), grid, block, lds, s, a); break;
+    case 16: hipLaunchKernelGGL((ode_bwd_kernel<NB, 16>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((ode_bwd_kernel<NB, 0>), grid, block, lds, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
+                       hipStream_t s) {
+  const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  hipLaunchKernelGGL(prep_kernel, dim3(blocks), dim3(256), 0, s, rp, pp, p.H, p.D, p.Hp, p.Dp,
+                     bwd ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                           float* sn, float* sd, hipStream_t s) {
+  const int BT = p.B * p.T;
+  const int hb = p.Hp / 64;
+  int rpw = 8;
+  while (rpw > 1 && (long long)hb * ((BT + 4 * rpw - 1) / (4 * rpw)) < 1024) rpw >>= 1;
+  const dim3 block(256);
+  const dim3 grid(hb, (BT + 4 * rpw - 1) / (4 * rpw));
+  switch (rpw) {
+    case 8: hipLaunchKernelGGL(sens_fwd_kernel<8>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
+    case 4: hipLaunchKernelGGL(sens_fwd_kernel<4>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
+    case 2: hipLaunchKernelGGL(sens_fwd_kernel<2>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
+    default: hipLaunchKernelGGL(sens_fwd_kernel<1>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
+                          const float* state0, float eps, float* out, float* hfin,
+                          float* vsave, float* densave, hipStream_t s) {
+  FwdK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave,
+         p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, eps};
+  switch (p.NB) {
+    case 16: return fwd_by_rcp<16>(p, a, s);
+    case 8: return fwd_by_rcp<8>(p, a, s);
+    case 4: return fwd_by_rcp<4>(p, a, s);
+    case 2: return fwd_by_rcp<2>(p, a, s);
+    default: return fwd_by_rcp<1>(p, a, s);
+  }
+}
+
+hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
+                          const float* densave, const float* gout, Strides3 gs,
+                          const float* ghfin, float2* absave, float* dsn, float* dsd,
+                          float* npart, float* gstate, hipStream_t s) {
+  BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
+         p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC};
+  switch (p.NB) {
+    case 16: return bwd_by_rcp<16>(p, a, s);
+    case 8: return bwd_by_rcp<8>(p, a, s);
+    case 4: return bwd_by_rcp<4>(p, a, s);
+    case 2: return bwd_by_rcp<2>(p, a, s);
+    default: return bwd_by_rcp<1>(p, a, s);
+  }
+}
+
+hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
+                           const float2* absave, float* rpart, hipStream_t s) {
+  const long long nper = (p.N + p.NCH - 1) / p.NCH;
+  RecGK a{pp.recF, vsave, absave, rpart, p.Hp, p.N, nper};
+  hipLaunchKernelGGL(rec_grad_kernel, dim3(p.Hp / 64, p.Hp / 32, p.NCH), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                           const float* dsn, const float* dsd, float* spart, float* dxpart,
+                           hipStream_t s) {
+  const int BT = p.B * p.T;
+  const int rows_per = (BT + p.NRC - 1) / p.NRC;
+  SensBK a{x, xs, pp.sensB, dsn, dsd, spart, dxpart, p.T, p.D, p.Dp, p.Hp, BT, rows_per};
+  hipLaunchKernelGGL(sens_bwd_kernel, dim3(p.Dp / 64, p.Hp / 32, p.NRC), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
+                           const float* spart, const float* dxpart, const float* npart,
+                           const GradOut& g, hipStream_t s) {
+  const int BT = p.B * p.T;
+  FinK a{rp, rpart, spart, dxpart, npart, g, p.B, p.D, p.H, p.Hp, p.Dp, p.NCH, p.NRC,
+         p.Hp / 32, BT};
+  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + (long long)BT * p.D;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  hipLaunchKernelGGL(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace ltc

@@ -1,0 +1,107 @@
+// Internal interface between the C-ABI layer (ltc_capi.hip) and the gfx950
+// kernels (ltc_device.hip). Not installed; the public surface is
+// include/ltc_capi.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ltc {
+
+// Threads per workgroup of the persistent ODE kernels for NB batch rows per
+// workgroup. More rows per thread means more live registers, so fewer
+// threads; the same bound is the kernels' __launch_bounds__.
+constexpr int ode_max_threads(int nb) { return nb <= 2 ? 1024 : (nb <= 4 ? 512 : 256); }
+
+// Kernel ids for the optional event-timing facility.
+enum KernelId : int {
+  K_PREP = 0,
+  K_SENS_FWD,
+  K_ODE_FWD,
+  K_ODE_BWD,
+  K_REC_GRAD,
+  K_SENS_BWD,
+  K_FINALIZE,
+  K_COUNT
+};
+
+// Shapes and launch choices shared by every kernel of one call.
+struct Plan {
+  int B, T, D, H, U;
+  int Hp, Dp;      // H and D rounded up to 64 (one wave of lanes per 64 columns)
+  int NB;          // batch rows per workgroup in the persistent ODE kernels
+  int KS;          // split of the reduction axis across waves of one workgroup
+  int RC;          // reduction chunk per thread = Hp / KS
+  int NCH;         // n-chunks of the recurrent parameter-gradient reduction
+  int NRC;         // row-chunks of the sensory backward reduction
+  long long N;     // T * U * B unfold instances
+};
+
+// Derived, zero-padded parameter images built once per call by the prep kernel.
+//   recF[i][j] = {-S*log2e, S*M*log2e, WE, WP} of synapse (i -> j), [Hp][Hp]
+//   recB[j][i] = the same float4, transposed, [Hp][Hp]
+//   sensF[d][h] = {-Ss*log2e, Ss*Ms*log2e, Ws*Es, Ws}, [Dp][Hp]
+//   sensB[h][d] = {-Ss*log2e, Ss*Ms*log2e, Es, Ws*Ss}, [Hp][Dp]
+//   neuron = C[Hp], G[Hp], L[Hp]
+struct Prepped {
+  float4* recF;
+  float4* recB;
+  float4* sensF;
+  float4* sensB;
+  float* neuron;
+};
+
+struct RawParams {
+  const float* w_pos;
+  const float* w_erev;
+  const float* mu;
+  const float* sigma;
+  const float* s_mu;
+  const float* s_sigma;
+  const float* s_erev;
+  const float* s_wpos;
+  const float* cm;
+  const float* gleak;
+  const float* vleak;
+};
+
+struct Strides3 {
+  long long b, t, c;
+};
+
+hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
+                       hipStream_t s);
+hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                           float* sn, float* sd, hipStream_t s);
+hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
+                          const float* state0, float eps, float* out, float* hfin,
+                          float* vsave, float* densave, hipStream_t s);
+hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
+                          const float* densave, const float* gout, Strides3 gs,
+                          const float* ghfin, float2* absave, float* dsn, float* dsd,
+                          float* npart, float* gstate, hipStream_t s);
+hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
+                           const float2* absave, float* rpart, hipStream_t s);
+hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                           const float* dsn, const float* dsd, float* spart, float* dxpart,
+                           hipStream_t s);
+struct GradOut {
+  float* x;        // (B,T,D) contiguous
+  float* w_pos;    // (H,H)
+  float* w_erev;
+  float* mu;
+  float* sigma;
+  float* s_mu;     // (D,H)
+  float* s_sigma;
+  float* s_erev;
+  float* s_wpos;
+  float* cm;       // (H)
+  float* gleak;
+  float* vleak;
+};
+hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
+                           const float* spart, const float* dxpart, const float* npart,
+                           const GradOut& g, hipStream_t s);
+
+}  // namespace ltc

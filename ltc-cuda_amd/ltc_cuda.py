@@ -1,0 +1,366 @@
+"""MI355X HIP backend for the LTC fused ODE solver (drop-in for the reference ltc_cuda.py).
+
+The reference builds a pybind11 CUDA extension at import time and exposes
+`_HAS_CUDA_KERNELS`, `_cuda_module`, `LTCCudaForward` and `ltc_cuda_forward`
+(ltc_cuda.py:23-24, 241-388). This module keeps those names and signatures.
+Behind them sits `libltc_hip.so`, a C-ABI library of hand-written gfx950
+kernels (include/ltc_capi.h), bound here with ctypes. ctypes releases the
+GIL during each call, and every call only enqueues work on the current torch
+stream.
+
+Differences from the reference, all deliberate:
+  * `_cuda_module.ltc_full_forward/backward` keep the reference's argument
+    lists and return lists of tensors, but the saved-for-backward set is one
+    opaque `saved` tensor (unfold states and denominators) instead of the
+    transposed parameter copies and sensory stacks (ltc_cuda.py:281-299).
+  * Inputs are validated (device, dtype, shape) and a failing launch raises
+    RuntimeError with the library's message; the reference checks nothing.
+  * The library is prebuilt in-tree (`python ltc-cuda_amd/build.py`); a
+    missing or unloadable library leaves `_HAS_CUDA_KERNELS = False` with the
+    reason in `_LOAD_ERROR`, and `ltc.py` then raises for CUDA inputs instead
+    of silently switching paths.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+
+import torch
+
+logger = logging.getLogger(__name__)
+
+_HAS_CUDA_KERNELS = False
+_cuda_module = None
+_LOAD_ERROR: str | None = None
+
+LIB_NAME = "libltc_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+_f32p = ctypes.c_void_p
+_i64 = ctypes.c_longlong
+_int = ctypes.c_int
+_flt = ctypes.c_float
+
+
+class CApi:
+    """ctypes view of include/ltc_capi.h."""
+
+    SYMBOLS = (
+        "ltc_abi_version", "ltc_last_error", "ltc_device_count", "ltc_saved_floats",
+        "ltc_fwd_workspace_bytes", "ltc_bwd_workspace_bytes", "ltc_full_forward",
+        "ltc_full_backward", "ltc_launch_plan", "ltc_timing_enable", "ltc_timing_read",
+        "ltc_kernel_count", "ltc_kernel_name",
+    )
+    PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
+                   "NRC", "ode_workgroups")
+
+    def __init__(self, path: str = LIB_PATH):
+        self.path = path
+        lib = ctypes.CDLL(path)
+        self.lib = lib
+        lib.ltc_abi_version.restype = _int
+        lib.ltc_abi_version.argtypes = []
+        lib.ltc_last_error.restype = ctypes.c_char_p
+        lib.ltc_last_error.argtypes = []
+        lib.ltc_device_count.restype = _int
+        lib.ltc_device_count.argtypes = []
+        lib.ltc_saved_floats.restype = _i64
+        lib.ltc_saved_floats.argtypes = [_int, _int, _int, _int]
+        for name in ("ltc_fwd_workspace_bytes", "ltc_bwd_workspace_bytes"):
+            fn = getattr(lib, name)
+            fn.restype = _i64
+            fn.argtypes = [_int, _int, _int, _int, _int]
+        lib.ltc_full_forward.restype = _int
+        lib.ltc_full_forward.argtypes = (
+            [_f32p, _i64, _i64, _i64, _f32p] + [_f32p] * 11
+            + [_int, _int, _int, _int, _int, _flt, _int]
+            + [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.c_void_p])
+        lib.ltc_full_backward.restype = _int
+        lib.ltc_full_backward.argtypes = (
+            [_f32p, _i64, _i64, _i64] + [_f32p] * 11 + [_f32p]
+            + [_f32p, _i64, _i64, _i64, _f32p]
+            + [_int, _int, _int, _int, _int, _flt]
+            + [_f32p] * 13 + [_f32p, _i64, ctypes.c_void_p])
+        lib.ltc_launch_plan.restype = _int
+        lib.ltc_launch_plan.argtypes = [_int, _int, _int, _int, _int,
+                                        ctypes.POINTER(ctypes.c_longlong), _int]
+        lib.ltc_timing_enable.restype = _int
+        lib.ltc_timing_enable.argtypes = [_int]
+        lib.ltc_timing_read.restype = _int
+        lib.ltc_timing_read.argtypes = [_int, ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_longlong)]
+        lib.ltc_kernel_count.restype = _int
+        lib.ltc_kernel_count.argtypes = []
+        lib.ltc_kernel_name.restype = ctypes.c_char_p
+        lib.ltc_kernel_name.argtypes = [_int]
+
+    def last_error(self) -> str:
+        return self.lib.ltc_last_error().decode(errors="replace")
+
+    def check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            raise RuntimeError(f"{what} failed (code {rc}): {self.last_error()}")
+
+    def plan(self, B: int, T: int, D: int, H: int, U: int) -> dict:
+        """Launch plan the library would use for these sizes."""
+        n = len(self.PLAN_FIELDS)
+        buf = (ctypes.c_longlong * n)()
+        got = self.lib.ltc_launch_plan(B, T, D, H, U, buf, n)
+        if got < 0:
+            raise ValueError(f"invalid LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        return dict(zip(self.PLAN_FIELDS, list(buf)[:got]))
+
+    # -- per-kernel event timing -------------------------------------------------
+    def timing_enable(self, on: bool) -> None:
+        self.check(self.lib.ltc_timing_enable(1 if on else 0), "ltc_timing_enable")
+
+    def timing_read(self) -> dict:
+        out = {}
+        for k in range(self.lib.ltc_kernel_count()):
+            ms = ctypes.c_double(0.0)
+            n = ctypes.c_longlong(0)
+            self.check(self.lib.ltc_timing_read(k, ctypes.byref(ms), ctypes.byref(n)),
+                       "ltc_timing_read")
+            out[self.lib.ltc_kernel_name(k).decode()] = (ms.value, n.value)
+        return out
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    ws = torch.empty(max(int(nbytes), 256) + 256, dtype=torch.uint8, device=device)
+    return ws
+
+
+def _aligned(ws: torch.Tensor) -> int:
+    p = ws.data_ptr()
+    return (p + 255) & ~255
+
+
+class _HipModule:
+    """Stands in for the reference's pybind module (`_cuda_module`).
+
+    Same entry-point names and argument lists as csrc/ltc_kernels.cu:1165-1182
+    and :962-984, minus the transposed copies, plus one `saved` tensor.
+    """
+
+    def __init__(self, capi: CApi):
+        self.capi = capi
+
+    @staticmethod
+    def _check_inputs(x_seq, state, params, H, D):
+        dev = x_seq.device
+        if x_seq.dim() != 3:
+            raise ValueError(f"x_seq must be (B, T, D), got {tuple(x_seq.shape)}")
+        if state.dim() != 2 or state.shape[0] != x_seq.shape[0]:
+            raise ValueError(f"state must be (B, H), got {tuple(state.shape)}")
+        shapes = [(H, H)] * 4 + [(D, H)] * 4 + [(H,)] * 3
+        for t, shp in zip(params, shapes):
+            if tuple(t.shape) != shp:
+                raise ValueError(f"parameter shape {tuple(t.shape)} != expected {shp}")
+        for t in (x_seq, state, *params):
+            if t.device != dev or not t.is_cuda:
+                raise ValueError("all LTC tensors must be on the same CUDA (HIP) device")
+            if t.dtype != torch.float32:
+                raise TypeError(f"LTC HIP kernels are fp32-only, got {t.dtype}")
+
+    def ltc_full_forward(self, x_seq, state, w_pos, w_erev, mu, sigma,
+                         sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+                         cm_t, gleak_pos, vleak, ode_unfolds, epsilon, save_intermediates):
+        B, T, D = x_seq.shape
+        H = state.shape[1]
+        params = (w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma, sensory_erev,
+                  sensory_w_pos, cm_t, gleak_pos, vleak)
+        self._check_inputs(x_seq, state, params, H, D)
+        dev = x_seq.device
+        params = [p.contiguous() for p in params]
+        state_c = state.contiguous()
+        lib = self.capi.lib
+        U = int(ode_unfolds)
+        out = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+        h = torch.empty(B, H, device=dev, dtype=torch.float32)
+        saved = None
+        if save_intermediates:
+            n = lib.ltc_saved_floats(B, T, H, U)
+            if n < 0:
+                raise ValueError(f"bad sizes for ltc_saved_floats: B={B} T={T} H={H} U={U}")
+            saved = torch.empty(max(int(n), 1), device=dev, dtype=torch.float32)
+        need = lib.ltc_fwd_workspace_bytes(B, T, D, H, U)
+        if need < 0:
+            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            sx = x_seq.stride()
+            rc = lib.ltc_full_forward(
+                _ptr(x_seq), sx[0], sx[1], sx[2], _ptr(state_c),
+                *[_ptr(p) for p in params],
+                B, T, D, H, U, float(epsilon), 1 if save_intermediates else 0,
+                _ptr(out), _ptr(h), _ptr(saved), _aligned(ws), int(need),
+                _stream_handle(dev))
+        self.capi.check(rc, "ltc_full_forward")
+        return [out, h] if saved is None else [out, h, saved]
+
+    def ltc_full_backward(self, x_seq, state, w_pos, w_erev, mu, sigma,
+                          sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+                          cm_t, gleak_pos, vleak, saved, grad_outputs, grad_final_state,
+                          ode_unfolds, epsilon, has_grad_state):
+        B, T, D = x_seq.shape
+        H = state.shape[1]
+        params = (w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma, sensory_erev,
+                  sensory_w_pos, cm_t, gleak_pos, vleak)
+        self._check_inputs(x_seq, state, params, H, D)
+        dev = x_seq.device
+        params = [p.contiguous() for p in params]
+        lib = self.capi.lib
+        U = int(ode_unfolds)
+        if tuple(grad_outputs.shape) != (B, T, H):
+            raise ValueError(f"grad_outputs must be (B, T, H), got {tuple(grad_outputs.shape)}")
+        go = grad_outputs
+        if go.dtype != torch.float32 or go.device != dev:
+            go = go.to(device=dev, dtype=torch.float32)
+        ghf = None
+        if has_grad_state and grad_final_state is not None:
+            ghf = grad_final_state.to(device=dev, dtype=torch.float32).contiguous()
+        f32 = dict(device=dev, dtype=torch.float32)
+        grads = [torch.empty(B, T, D, **f32), torch.empty(B, H, **f32)]
+        grads += [torch.empty(H, H, **f32) for _ in range(4)]
+        grads += [torch.empty(D, H, **f32) for _ in range(4)]
+        grads += [torch.empty(H, **f32) for _ in range(3)]
+        need = lib.ltc_bwd_workspace_bytes(B, T, D, H, U)
+        if need < 0:
+            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            sx = x_seq.stride()
+            sg = go.stride()
+            rc = lib.ltc_full_backward(
+                _ptr(x_seq), sx[0], sx[1], sx[2],
+                *[_ptr(p) for p in params], _ptr(saved),
+                _ptr(go), sg[0], sg[1], sg[2], _ptr(ghf),
+                B, T, D, H, U, float(epsilon),
+                *[_ptr(g) for g in grads], _aligned(ws), int(need), _stream_handle(dev))
+        self.capi.check(rc, "ltc_full_backward")
+        return grads
+
+
+def load_capi(path: str = LIB_PATH) -> CApi:
+    """Load the C-ABI library and check its ABI version (no device needed)."""
+    capi = CApi(path)
+    ver = capi.lib.ltc_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"{path}: ABI version {ver}, expected {ABI_VERSION}")
+    return capi
+
+
+def _try_load_hip_kernels() -> bool:
+    """Load libltc_hip.so when a HIP device is present (ltc_cuda.py:138-234).
+
+    Never compiles at import time: the library is built in-tree beforehand.
+    """
+    global _HAS_CUDA_KERNELS, _cuda_module, _LOAD_ERROR
+    _HAS_CUDA_KERNELS = False
+    _cuda_module = None
+    if not torch.cuda.is_available():
+        _LOAD_ERROR = "no HIP device visible to torch"
+        return False
+    if not os.path.isfile(LIB_PATH):
+        _LOAD_ERROR = (f"{LIB_PATH} not found; build it with "
+                       f"`python {os.path.join(os.path.dirname(LIB_PATH), 'build.py')}`")
+        logger.warning("LTC HIP kernels unavailable: %s", _LOAD_ERROR)
+        return False
+    try:
+        capi = load_capi(LIB_PATH)
+        if capi.lib.ltc_device_count() < 1:
+            raise RuntimeError("libltc_hip.so sees no HIP device")
+    except (OSError, RuntimeError) as exc:
+        _LOAD_ERROR = f"failed to load {LIB_PATH}: {exc}"
+        logger.warning("LTC HIP kernels unavailable: %s", _LOAD_ERROR)
+        return False
+    _cuda_module = _HipModule(capi)
+    _HAS_CUDA_KERNELS = True
+    _LOAD_ERROR = None
+    logger.info("Loaded LTC HIP kernels from %s", LIB_PATH)
+    return True
+
+
+# Name kept for callers of the reference loader.
+_try_load_cuda_kernels = _try_load_hip_kernels
+
+_try_load_hip_kernels()
+
+
+def require_kernels():
+    """Return the loaded backend or raise with the reason it is missing."""
+    if not _HAS_CUDA_KERNELS or _cuda_module is None:
+        raise RuntimeError(f"LTC HIP extension is not loaded: {_LOAD_ERROR}")
+    return _cuda_module
+
+
+class LTCCudaForward(torch.autograd.Function):
+    """Autograd Function over the fused HIP forward/backward (ltc_cuda.py:241-359).
+
+    forward inputs and backward gradients keep the reference order:
+    x_seq, state, w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma,
+    sensory_erev, sensory_w_pos, cm_t, gleak_pos, vleak, then None for
+    ode_unfolds, epsilon and needs_grad.
+    """
+
+    @staticmethod
+    def forward(ctx, x_seq, state, w_pos, w_erev, mu, sigma,
+                sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+                cm_t, gleak_pos, vleak, ode_unfolds, epsilon, needs_grad):
+        mod = require_kernels()
+        result = mod.ltc_full_forward(
+            x_seq, state, w_pos, w_erev, mu, sigma,
+            sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+            cm_t, gleak_pos, vleak, ode_unfolds, epsilon, needs_grad)
+        outputs, current_state = result[0], result[1]
+        if needs_grad:
+            ctx.save_for_backward(x_seq, state, w_pos, w_erev, mu, sigma,
+                                  sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+                                  cm_t, gleak_pos, vleak, result[2])
+        ctx.ode_unfolds = ode_unfolds
+        ctx.epsilon = epsilon
+        return outputs, current_state
+
+    @staticmethod
+    def backward(ctx, grad_outputs, grad_state):
+        saved = ctx.saved_tensors
+        if not saved:
+            raise RuntimeError("LTCCudaForward.backward called on a forward run without grad")
+        (x_seq, state, w_pos, w_erev, mu, sigma, sensory_mu, sensory_sigma, sensory_erev,
+         sensory_w_pos, cm_t, gleak_pos, vleak, buf) = saved
+        B, T, _ = x_seq.shape
+        H = state.shape[1]
+        if grad_outputs is None:
+            grad_outputs = torch.zeros(B, T, H, device=x_seq.device, dtype=x_seq.dtype)
+        has_grad_state = grad_state is not None
+        grads = require_kernels().ltc_full_backward(
+            x_seq, state, w_pos, w_erev, mu, sigma,
+            sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+            cm_t, gleak_pos, vleak, buf, grad_outputs, grad_state,
+            ctx.ode_unfolds, ctx.epsilon, has_grad_state)
+        return (*grads, None, None, None)
+
+
+def ltc_cuda_forward(x_seq, state, w_pos, w_erev, mu, sigma,
+                     sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+                     cm_t, gleak_pos, vleak, ode_unfolds, epsilon):
+    """Entry point of the fused path (ltc_cuda.py:362-388).
+
+    Grad mode is read here, outside Function.forward where it is always off.
+    """
+    needs_grad = torch.is_grad_enabled()
+    return LTCCudaForward.apply(
+        x_seq, state, w_pos, w_erev, mu, sigma,
+        sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
+        cm_t, gleak_pos, vleak, ode_unfolds, epsilon, needs_grad)

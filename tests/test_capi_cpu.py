@@ -1,0 +1,143 @@
+"""C-ABI library checks that need no GPU: it loads, exports what the header
+declares, reports sizes, and rejects bad arguments before touching a device."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (loads torch's HIP runtime first, as in production)
+
+import ltc_cuda
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ltc_capi.h")
+
+pytestmark = pytest.mark.skipif(not os.path.isfile(ltc_cuda.LIB_PATH),
+                                reason="libltc_hip.so not built (python ltc-cuda_amd/build.py)")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_ ]+\**\s*\**(ltc_\w+)\s*\(", text,
+                                 flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def capi():
+    return ltc_cuda.load_capi(ltc_cuda.LIB_PATH)
+
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for must in ("ltc_full_forward", "ltc_full_backward", "ltc_fwd_workspace_bytes",
+                 "ltc_bwd_workspace_bytes", "ltc_saved_floats", "ltc_last_error",
+                 "ltc_abi_version", "ltc_device_count"):
+        assert must in names
+    assert set(names) == set(ltc_cuda.CApi.SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol(capi):
+    for name in _declared_functions():
+        assert hasattr(capi.lib, name), name
+        assert ctypes.cast(getattr(capi.lib, name), ctypes.c_void_p).value
+
+
+def test_abi_version(capi):
+    assert capi.lib.ltc_abi_version() == ltc_cuda.ABI_VERSION
+
+
+def test_sizes(capi):
+    lib = capi.lib
+    # saved = (T*U + 1) * B * Hp + T*U*B*Hp floats, Hp = H rounded up to 64
+    assert lib.ltc_saved_floats(24, 8, 64, 6) == (8 * 6 + 1) * 24 * 64 + 8 * 6 * 24 * 64
+    assert lib.ltc_saved_floats(2, 3, 65, 1) == (3 + 1) * 2 * 128 + 3 * 2 * 128
+    a = lib.ltc_fwd_workspace_bytes(24, 8, 128, 64, 6)
+    b = lib.ltc_fwd_workspace_bytes(48, 8, 128, 64, 6)
+    assert 0 < a < b and a % 256 == 0
+    assert lib.ltc_bwd_workspace_bytes(24, 8, 128, 64, 6) > 0
+    assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 0, 6) == -1
+    assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 2000, 6) == -1
+    assert lib.ltc_bwd_workspace_bytes(1, 1, 1, 8, 0) == -1
+
+
+def _fwd_call(capi, **over):
+    args = dict(x=1, s=(0, 0, 0), state=1, params=[1] * 11, B=2, T=3, D=4, H=5, U=6,
+                eps=1e-8, save=0, out=1, h=1, saved=None, ws=256, wsb=1 << 30, stream=None)
+    args.update(over)
+    return capi.lib.ltc_full_forward(
+        args["x"], *args["s"], args["state"], *args["params"], args["B"], args["T"],
+        args["D"], args["H"], args["U"], args["eps"], args["save"], args["out"], args["h"],
+        args["saved"], args["ws"], args["wsb"], args["stream"])
+
+
+def test_forward_rejects_bad_arguments_before_launch(capi):
+    # Fake non-NULL addresses: every case must fail validation, so nothing runs.
+    assert _fwd_call(capi, H=0) == 1 and "H >= 1" in capi.last_error()
+    assert _fwd_call(capi, U=0) == 1 and "ode_unfolds" in capi.last_error()
+    assert _fwd_call(capi, H=1025) == 2 and "exceeds" in capi.last_error()
+    assert _fwd_call(capi, params=[1] * 10 + [None]) == 1
+    assert _fwd_call(capi, save=1, saved=None) == 1 and "saved" in capi.last_error()
+    assert _fwd_call(capi, wsb=16) == 1 and "workspace too small" in capi.last_error()
+    assert _fwd_call(capi, ws=256 + 8) == 1 and "aligned" in capi.last_error()
+    assert _fwd_call(capi, x=None) == 1
+
+
+def test_backward_rejects_bad_arguments_before_launch(capi):
+    lib = capi.lib
+    p = [1] * 11
+    g = [1] * 13
+    rc = lib.ltc_full_backward(1, 0, 0, 0, *p, 1, 1, 0, 0, 0, None, 2, 3, 4, 5, 0, 1e-8,
+                               *g, 256, 1 << 30, None)
+    assert rc == 1 and "ode_unfolds" in capi.last_error()
+    rc = lib.ltc_full_backward(1, 0, 0, 0, *p, None, 1, 0, 0, 0, None, 2, 3, 4, 5, 6, 1e-8,
+                               *g, 256, 1 << 30, None)
+    assert rc == 1 and "NULL" in capi.last_error()
+    rc = lib.ltc_full_backward(1, 0, 0, 0, *p, 1, 1, 0, 0, 0, None, 2, 3, 4, 5, 6, 1e-8,
+                               *g, 256, 100, None)
+    assert rc == 1 and "workspace" in capi.last_error()
+
+
+def test_timing_surface(capi):
+    n = capi.lib.ltc_kernel_count()
+    names = [capi.lib.ltc_kernel_name(k).decode() for k in range(n)]
+    assert "ltc_ode_fwd" in names and "ltc_ode_bwd" in names
+    assert capi.lib.ltc_kernel_name(n) == b""
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the GPU-less host")
+def test_no_device_reported_without_gpu(capi):
+    assert capi.lib.ltc_device_count() == 0
+    assert not ltc_cuda._HAS_CUDA_KERNELS
+    assert ltc_cuda._LOAD_ERROR
+
+
+def _max_threads(nb):
+    # Mirror of ode_max_threads() in ltc-cuda_amd/csrc/ltc_internal.h.
+    return 1024 if nb <= 2 else (512 if nb <= 4 else 256)
+
+
+SHAPES = [(B, T, D, H, U) for B in (1, 2, 24, 255, 256, 257, 511, 1024, 4096, 5000)
+          for (D, H) in ((1, 1), (5, 4), (128, 64), (32, 65), (128, 128), (7, 192), (256, 256),
+                         (512, 512), (64, 1000), (3, 1024))
+          for (T, U) in ((8, 6), (1, 1))]
+
+
+@pytest.mark.parametrize("shape", SHAPES + [(24, 8, 128, 64, 6), (4096, 4, 64, 64, 6),
+                                                  (256, 64, 256, 256, 6), (128, 32, 512, 512, 6),
+                                                  (32, 16, 128, 128, 6)])
+def test_launch_plan_fits_the_hardware_limits(capi, shape):
+    """Every launch the plan makes fits the kernels' compiled assumptions."""
+    B, T, D, H, U = shape
+    p = capi.plan(B, T, D, H, U)
+    assert p["Hp"] % 64 == 0 and p["Hp"] >= H and p["Hp"] - H < 64
+    assert p["Dp"] % 64 == 0 and p["Dp"] >= D and p["Dp"] - D < 64
+    assert p["NB"] in (1, 2, 4, 8, 16)
+    assert p["KS"] >= 1 and p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 4 == 0
+    assert p["threads"] == p["Hp"] * p["KS"] <= _max_threads(p["NB"])
+    assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
+    assert 1 <= p["NCH"] <= 64 and 1 <= p["NRC"] <= 64
+    assert p["ode_workgroups"] * p["NB"] >= B > (p["ode_workgroups"] - 1) * p["NB"] or B == 0
