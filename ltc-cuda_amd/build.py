@@ -49,6 +49,23 @@ def command(out: str = LIB_PATH) -> list:
     ]
 
 
+PROBE_SRC = os.path.join(HERE, "probes", "issue_rate.cpp")
+PROBE_BIN = os.path.join(HERE, "probes", "issue_rate")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """Standalone issue-rate probe (FMA / exp / rcp throughput) used for the roofline."""
+    cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument", "-o", PROBE_BIN, PROBE_SRC]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed on the issue-rate probe:\n" + proc.stderr)
+    return PROBE_BIN
+
+
 def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     cmd = command(tmp)
@@ -62,6 +79,7 @@ def build(verbose: bool = False) -> str:
     if verbose and msgs:
         print("\n".join(msgs), flush=True)
     os.replace(tmp, LIB_PATH)
+    build_probe(verbose)
     return LIB_PATH
 
 
