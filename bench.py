@@ -261,6 +261,27 @@ def measure_large(name, c, capi):
     return rec
 
 
+COPY_BYTES = 64 << 20
+
+
+def profile_pass(name):
+    """Known-size copy, then a few steps of one config (run under rocprofv3 --pmc)."""
+    src = torch.ones(COPY_BYTES // 4, device="cuda:0")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    c = C1 if name == "C1" else LARGE[name]
+    m, x, target = make_inputs(c, "cuda:0")
+    for _ in range(3):
+        if c["loss"] is None:
+            with torch.no_grad():
+                m(x)
+        else:
+            step(m, x, target)
+    torch.cuda.synchronize()
+    print(f"profile pass {name} done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -268,6 +289,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-large", action="store_true")
+    ap.add_argument("--profile-pass", choices=["C1", "C3", "C4", "C5"], default=None,
+                    help="for rocprofv3 --pmc: a 64 MiB device copy (calibrates the byte "
+                         "counters), then 3 steps of the named config; prints nothing else")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -281,6 +305,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
     capi = ltc_cuda.require_kernels().capi
+    if args.profile_pass:
+        profile_pass(args.profile_pass)
+        return
     c = C1
     m, x, target = make_inputs(c, "cuda:0")
 

@@ -127,10 +127,12 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
  * counterpart in the reference. Writes up to n of: Hp, Dp, NB (batch rows
  * per ODE workgroup), KS (reduction split), RC (= Hp/KS), threads per ODE
  * workgroup, forward LDS bytes, backward LDS bytes, NCH (recurrent gradient
- * chunks), NRC (sensory backward row chunks), ODE workgroups. Returns the
- * number of values written, or -1 for invalid sizes.
+ * chunks, or one per workgroup when fused), NRC (sensory backward row
+ * chunks), ODE workgroups, and 1 when the recurrent parameter gradients are
+ * accumulated inside the chain kernel. Returns the number of values written,
+ * or -1 for invalid sizes.
  */
-#define LTC_PLAN_FIELDS 11
+#define LTC_PLAN_FIELDS 12
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

@@ -52,8 +52,11 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
     return f <= 65536 && b <= 65536;
   };
   for (;;) {
-    // KS is a power of two <= 16, so it always divides Hp/4 (Hp is a multiple of 64).
+    // KS is a power of two <= 16, so it always divides Hp/4 (Hp is a multiple
+    // of 64). With NB >= 4 rows, KS >= 4 keeps the rows each thread finishes
+    // within ode_owned_rows(NB).
     const int cap = ltc::ode_max_threads(p.NB) / p.Hp;
+    const int ks_min = p.NB >= 4 ? 4 : 1;
     int ks = 0;
     for (int k = 16; k >= 1; k >>= 1) {
       if (k <= cap) {
@@ -61,8 +64,8 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
         break;
       }
     }
-    while (ks > 1 && (!lds_ok(p.NB, ks) || p.Hp / ks < 4)) ks >>= 1;
-    if ((ks >= 1 && lds_ok(p.NB, ks)) || p.NB == 1) {
+    while (ks > ks_min && (!lds_ok(p.NB, ks) || p.Hp / ks < 4)) ks >>= 1;
+    if ((ks >= ks_min && lds_ok(p.NB, ks) && p.Hp / ks >= 4) || p.NB == 1) {
       p.KS = ks < 1 ? 1 : ks;
       break;
     }
@@ -70,9 +73,16 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
   }
   p.RC = p.Hp / p.KS;
   p.N = (long long)T * U * B;
+  // When each thread's synapse operands fit in registers (RC in {4, 8, 16}),
+  // the chain kernel also accumulates the recurrent parameter gradients and
+  // writes one partial per workgroup.
+  p.FUSE = ltc::ode_fuse_ok(p.NB, p.RC);
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
-  {
+  if (p.FUSE) {
+    p.NCH = (B + p.NB - 1) / p.NB;
+    if (p.NCH < 1) p.NCH = 1;
+  } else {
     const long long bpc = (long long)(p.Hp / 64) * (p.Hp / 32);
     long long nch = (1024 + bpc - 1) / bpc;
     if (nch > 64) nch = 64;
@@ -145,7 +155,7 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   w.pp.recB = c.take<float4>((long long)p.Hp * p.Hp);
   w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
   w.pp.neuron = c.take<float>(3LL * p.Hp);
-  w.absave = c.take<float2>(p.N * p.Hp);
+  w.absave = p.FUSE ? nullptr : c.take<float2>(p.N * p.Hp);
   w.dsn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.dsd = c.take<float>((long long)p.B * p.T * p.Hp);
   w.npart = c.take<float>((long long)p.B * 3 * p.Hp);
@@ -414,12 +424,14 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
   if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_ODE_BWD, s, [&] {
     return ltc::launch_ode_bwd(p, w.pp, vsave, densave, grad_out, gs, grad_h_final, w.absave,
-                               w.dsn, w.dsd, w.npart, grad_state, s);
+                               w.dsn, w.dsd, w.npart, grad_state, w.rpart, s);
   });
   if (e != hipSuccess) return hip_fail("ODE backward launch", e);
-  e = timed(ltc::K_REC_GRAD, s,
-            [&] { return ltc::launch_rec_grad(p, w.pp, vsave, w.absave, w.rpart, s); });
-  if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  if (!p.FUSE) {
+    e = timed(ltc::K_REC_GRAD, s,
+              [&] { return ltc::launch_rec_grad(p, w.pp, vsave, w.absave, w.rpart, s); });
+    if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  }
   e = timed(ltc::K_SENS_BWD, s, [&] {
     return ltc::launch_sens_bwd(p, x, xs, w.pp, w.dsn, w.dsd, w.spart, w.dxpart, s);
   });
@@ -438,7 +450,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.Hp, p.Dp, p.NB, p.KS, p.RC, (long long)p.Hp * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8,
       (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4,
-      p.NCH, p.NRC, (B + p.NB - 1) / p.NB};
+      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -96,22 +96,29 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
 
 // ---------------------------------------------------------------------------
 // Sensory forward for all (b,t) rows at once.
-// grid (Hp/64, ceil(BT / (4*RPW))), block 256: lane -> h, wave -> RPW rows.
-// Each float4 operand read from HBM/L2 is reused for RPW rows in registers;
-// x is staged through LDS 64 inputs at a time and read as a broadcast.
+// Block 256 = 4 waves, lane -> h (64 neurons per workgroup). Each float4
+// operand read from L2 is reused for RPW rows held in registers; x is staged
+// through LDS 64 inputs at a time and read as a broadcast.
+//   DS = 1: the 4 waves own 4 groups of RPW rows (4*RPW rows per workgroup)
+//           and each walks all of D (large B*T: operands shared through L1);
+//   DS = 4: the 4 waves split D into quarters over the same RPW rows and meet
+//           in LDS (small B*T: 4x shorter dependent load chains per thread).
+// grid (Hp/64, ceil(BT / rows_per_workgroup)).
 // ---------------------------------------------------------------------------
-template <int RPW>
+template <int RPW, int DS>
 __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__ x, Strides3 xs,
                                                        int T, int D, int BT, int Hp,
                                                        const float4* __restrict__ sensF,
                                                        float* __restrict__ sn,
                                                        float* __restrict__ sd) {
-  constexpr int ROWS = 4 * RPW;
-  constexpr int XLD = ROWS + 4;  // keeps each staged row 16-byte aligned
+  constexpr int ROWS = (DS == 1 ? 4 : 1) * RPW;
+  constexpr int XLD = ROWS + 4;  // padded staged row, 16-byte aligned
   __shared__ __align__(16) float xsh[64 * XLD];
+  __shared__ float2 part[DS == 1 ? 1 : 3][RPW][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int h = blockIdx.x * 64 + lane;
   const int row0 = blockIdx.y * ROWS;
+  const int rw = DS == 1 ? w * RPW : 0;  // first staged row of this wave
   float an[RPW], ad[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
@@ -129,11 +136,13 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
     }
     __syncthreads();
     const int dn = min(64, D - d0);
+    const int dlo = DS == 1 ? 0 : w * (64 / DS);
+    const int dhi = DS == 1 ? dn : min(dn, dlo + 64 / DS);
     const float4* pcol = sensF + (long long)d0 * Hp + h;
 #pragma unroll 4
-    for (int dd = 0; dd < dn; ++dd) {
+    for (int dd = dlo; dd < dhi; ++dd) {
       const float4 p = pcol[(long long)dd * Hp];
-      const float* xr = xsh + dd * XLD + w * RPW;
+      const float* xr = xsh + dd * XLD + rw;
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
         const float a = gate(fmaf(p.x, xr[r], p.y));
@@ -143,9 +152,26 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
     }
     __syncthreads();
   }
+  if constexpr (DS != 1) {
+    if (w > 0) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) part[w - 1][r][lane] = make_float2(an[r], ad[r]);
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const float2 v = part[q][r][lane];
+        an[r] += v.x;
+        ad[r] += v.y;
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    const int row = row0 + w * RPW + r;
+    const int row = row0 + rw + r;
     if (row < BT) {
       sn[(long long)row * Hp + h] = an[r];
       sd[(long long)row * Hp + h] = ad[r];
@@ -188,6 +214,7 @@ __device__ __forceinline__ void fwd_synapse(const float4 p, const float* vs, int
 
 template <int NB, int RCP>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
+  constexpr int MO = ode_owned_rows(NB);
   extern __shared__ float4 lds4[];
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
   const int RC = RCP > 0 ? RCP : k.RC;
@@ -213,18 +240,23 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   }
   lds_barrier();
 
-  for (int t = 0; t < T; ++t) {
-    float snr[NB], sdr[NB];
+  // Sensory sums of step t are requested one step ahead (software pipeline).
+  float snr[MO], sdr[MO], snn[MO], sdn[MO];
+  auto load_sens = [&](int t, float (&sn_)[MO], float (&sd_)[MO]) {
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
+    for (int m = 0; m < MO; ++m) {
       const int b = ks + m * KS;
-      snr[m] = sdr[m] = 0.f;
+      sn_[m] = sd_[m] = 0.f;
       if (b < NB && b0 + b < B) {
         const long long e = ((long long)(b0 + b) * T + t) * Hp + o;
-        snr[m] = k.sn[e];
-        sdr[m] = k.sd[e];
+        sn_[m] = k.sn[e];
+        sd_[m] = k.sd[e];
       }
     }
+  };
+  if (T > 0) load_sens(0, snr, sdr);
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) load_sens(t + 1, snn, sdn);
     for (int u = 0; u < U; ++u) {
       float na[NB], qa[NB];
 #pragma unroll
@@ -241,7 +273,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
       lds_barrier();
 #pragma unroll
-      for (int m = 0; m < NB; ++m) {
+      for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
           float n = 0.f, q = 0.f;
@@ -266,9 +298,16 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       }
       lds_barrier();
     }
+    if (t + 1 < T) {
+#pragma unroll
+      for (int m = 0; m < MO; ++m) {
+        snr[m] = snn[m];
+        sdr[m] = sdn[m];
+      }
+    }
   }
 #pragma unroll
-  for (int m = 0; m < NB; ++m) {
+  for (int m = 0; m < MO; ++m) {
     const int b = ks + m * KS;
     if (b < NB && b0 + b < B) {
       const float v = vs[b * Hp + o];
@@ -293,29 +332,78 @@ struct BwdK {
   const float* gout;
   Strides3 gs;
   const float* ghfin;
-  float2* absave;
+  float2* absave;   // alpha/beta per unfold, for rec_grad_kernel (unused when fused)
   float* dsn;
   float* dsd;
   float* npart;
   float* gstate;
+  float* rpart;     // per-workgroup recurrent partials [grid][4][Hp][Hp] (fused only)
   int B, T, H, Hp, U, KS, RC;
 };
 
-template <int NB>
+// One synapse (i = o, j = r) of the chain for every row of the tile. With
+// FUSE the parameter-gradient sums of this synapse ride along in gacc:
+// {sum alpha*a, sum beta*a, sum delta, sum delta*v_i}.
+template <int NB, bool FUSE>
 __device__ __forceinline__ void bwd_synapse(const float4 p, const float2* ab, int Hp, int r,
-                                            const float* vi, float* acc) {
+                                            const float* vi, float* acc, float4& gacc) {
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const float2 c = ab[b * Hp + r];
     const float a = gate(fmaf(p.x, vi[b], p.y));
     const float a2 = fmaf(-a, a, a);
-    const float hh = fmaf(c.x, p.z, c.y * p.w);
-    acc[b] = fmaf(hh * a2, p.x, acc[b]);
+    const float dl = fmaf(c.x, p.z, c.y * p.w) * a2;
+    acc[b] = fmaf(dl, p.x, acc[b]);
+    if constexpr (FUSE) {
+      gacc.x = fmaf(c.x, a, gacc.x);
+      gacc.y = fmaf(c.y, a, gacc.y);
+      gacc.z += dl;
+      gacc.w = fmaf(dl, vi[b], gacc.w);
+    }
   }
 }
 
-template <int NB, int RCP>
+// Operands of unfold n for the synapse phase (all rows, column o) and for the
+// rows this thread finishes (den, v^k, v^{k+1}).
+template <int NB, int MO>
+__device__ __forceinline__ void bwd_load_unfold(const BwdK& k, long long n, int b0, int ks, int o,
+                                                float (&vi)[NB], float (&den)[MO],
+                                                float (&vk)[MO], float (&vk1)[MO]) {
+  const long long BHp = (long long)k.B * k.Hp;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) vi[b] = b0 + b < k.B ? k.vsave[(n * k.B + b0 + b) * k.Hp + o] : 0.f;
+#pragma unroll
+  for (int m = 0; m < MO; ++m) {
+    const int b = ks + m * k.KS;
+    den[m] = 1.f;
+    vk[m] = vk1[m] = 0.f;
+    if (b < NB && b0 + b < k.B && o < k.H) {
+      const long long e = (n * k.B + b0 + b) * k.Hp + o;
+      den[m] = k.densave[e];
+      vk[m] = k.vsave[e];
+      vk1[m] = k.vsave[e + BHp];
+    }
+  }
+}
+
+template <int NB, int MO>
+__device__ __forceinline__ void bwd_load_gout(const BwdK& k, int t, int b0, int ks, int o,
+                                              float (&go)[MO]) {
+#pragma unroll
+  for (int m = 0; m < MO; ++m) {
+    const int b = ks + m * k.KS;
+    go[m] = 0.f;
+    if (b < NB && b0 + b < k.B && o < k.H) go[m] = k.gout[(b0 + b) * k.gs.b + t * k.gs.t + o * k.gs.c];
+  }
+}
+
+// FUSE (register-resident operands only): each operand also carries its
+// gradient accumulators, which removes the separate parameter-gradient pass
+// and its second gate evaluation.
+template <int NB, int RCP, bool FUSE>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
+  static_assert(!FUSE || RCP > 0, "fused gradients need register-resident operands");
+  constexpr int MO = ode_owned_rows(NB);
   extern __shared__ float4 lds4[];
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
   const int RC = RCP > 0 ? RCP : k.RC;
@@ -325,82 +413,99 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   const int ks = tid / Hp, o = tid - ks * Hp;
   const int b0 = blockIdx.x * NB;
   const int r0 = ks * RC;
-  const long long BHp = (long long)B * Hp;
   const float C = k.neuron[o];
 
   float4 preg[RCP > 0 ? RCP : 1];
+  float4 gacc[FUSE ? RCP : 1];
   if constexpr (RCP > 0) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + o];
   }
-
-  float g[NB], pC[NB], pGv[NB], pA[NB];
+  if constexpr (FUSE) {
 #pragma unroll
-  for (int m = 0; m < NB; ++m) {
+    for (int rr = 0; rr < RCP; ++rr) gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+
+  float g[MO], pC[MO], pGv[MO], pA[MO];
+#pragma unroll
+  for (int m = 0; m < MO; ++m) {
     const int b = ks + m * KS;
     g[m] = 0.f;
     pC[m] = pGv[m] = pA[m] = 0.f;
     if (k.ghfin != nullptr && b < NB && b0 + b < B && o < H) g[m] = k.ghfin[(long long)(b0 + b) * H + o];
   }
+  if (T == 0) return;
+
+  // Software pipeline: the operands of the next unfold (and the next step's
+  // output gradient) are requested one unfold ahead; LDS-only barriers keep
+  // those loads in flight.
+  float cvi[NB], cden[MO], cvk[MO], cvk1[MO];
+  float nvi[NB], nden[MO], nvk[MO], nvk1[MO];
+  float gcur[MO], gnext[MO];
+#pragma unroll
+  for (int m = 0; m < MO; ++m) gnext[m] = 0.f;
+  bwd_load_unfold<NB, MO>(k, (long long)T * U - 1, b0, ks, o, cvi, cden, cvk, cvk1);
+  bwd_load_gout<NB, MO>(k, T - 1, b0, ks, o, gcur);
 
   for (int t = T - 1; t >= 0; --t) {
-    float accA[NB], accB[NB];
+    if (t > 0) bwd_load_gout<NB, MO>(k, t - 1, b0, ks, o, gnext);
+    float accA[MO], accB[MO];
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
-      const int b = ks + m * KS;
+    for (int m = 0; m < MO; ++m) {
       accA[m] = accB[m] = 0.f;
-      if (b < NB && b0 + b < B && o < H)
-        g[m] += k.gout[(b0 + b) * k.gs.b + t * k.gs.t + o * k.gs.c];
+      g[m] += gcur[m];
     }
     for (int u = U - 1; u >= 0; --u) {
       const long long n = (long long)t * U + u;
-      float vi[NB];
+      if (n > 0) bwd_load_unfold<NB, MO>(k, n - 1, b0, ks, o, nvi, nden, nvk, nvk1);
+      float gdir[MO];
 #pragma unroll
-      for (int b = 0; b < NB; ++b) vi[b] = b0 + b < B ? k.vsave[(n * B + b0 + b) * Hp + o] : 0.f;
-      float gdir[NB];
-#pragma unroll
-      for (int m = 0; m < NB; ++m) {
+      for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         gdir[m] = 0.f;
         if (b < NB) {
           float al = 0.f, be = 0.f;
           const bool live = b0 + b < B;
           if (live && o < H) {
-            const long long e = (n * B + b0 + b) * Hp + o;
-            const float den = k.densave[e];
-            const float vk = k.vsave[e];
-            const float vk1 = k.vsave[e + BHp];
-            const float rden = 1.0f / den;
+            const float rden = 1.0f / cden[m];
             al = g[m] * rden;
-            be = -g[m] * vk1 * rden;
+            be = -g[m] * cvk1[m] * rden;
             accA[m] += al;
             accB[m] += be;
-            pC[m] += al * (vk - vk1);
-            pGv[m] += al * vk1;
+            pC[m] += al * (cvk[m] - cvk1[m]);
+            pGv[m] += al * cvk1[m];
             pA[m] += al;
             gdir[m] = al * C;
           }
           ab[b * Hp + o] = make_float2(al, be);
-          if (live) k.absave[(n * B + b0 + b) * Hp + o] = make_float2(al, be);
+          if (!FUSE && live) k.absave[(n * B + b0 + b) * Hp + o] = make_float2(al, be);
         }
       }
       lds_barrier();
       float acc[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-      if constexpr (RCP > 0) {
+      if constexpr (FUSE) {
 #pragma unroll
-        for (int rr = 0; rr < RCP; ++rr) bwd_synapse<NB>(preg[rr], ab, Hp, r0 + rr, vi, acc);
+        for (int rr = 0; rr < RCP; ++rr)
+          bwd_synapse<NB, true>(preg[rr], ab, Hp, r0 + rr, cvi, acc, gacc[rr]);
+      } else if constexpr (RCP > 0) {
+        float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int rr = 0; rr < RCP; ++rr)
+          bwd_synapse<NB, false>(preg[rr], ab, Hp, r0 + rr, cvi, acc, unused);
       } else {
+        float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
         const float4* pc = k.recB + (long long)r0 * Hp + o;
 #pragma unroll 4
-        for (int rr = 0; rr < RC; ++rr) bwd_synapse<NB>(pc[(long long)rr * Hp], ab, Hp, r0 + rr, vi, acc);
+        for (int rr = 0; rr < RC; ++rr)
+          bwd_synapse<NB, false>(pc[(long long)rr * Hp], ab, Hp, r0 + rr, cvi, acc, unused);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = acc[b];
       lds_barrier();
 #pragma unroll
-      for (int m = 0; m < NB; ++m) {
+      for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
           float s = 0.f;
@@ -408,19 +513,30 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
           g[m] = o < H ? fmaf(kNegLn2, s, gdir[m]) : 0.f;
         }
       }
+      if (n > 0) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) cvi[b] = nvi[b];
+#pragma unroll
+        for (int m = 0; m < MO; ++m) {
+          cden[m] = nden[m];
+          cvk[m] = nvk[m];
+          cvk1[m] = nvk1[m];
+        }
+      }
     }
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
+    for (int m = 0; m < MO; ++m) {
       const int b = ks + m * KS;
       if (b < NB && b0 + b < B) {
         const long long e = ((long long)(b0 + b) * T + t) * Hp + o;
         k.dsn[e] = accA[m];
         k.dsd[e] = accB[m];
       }
+      gcur[m] = gnext[m];
     }
   }
 #pragma unroll
-  for (int m = 0; m < NB; ++m) {
+  for (int m = 0; m < MO; ++m) {
     const int b = ks + m * KS;
     if (b < NB && b0 + b < B) {
       if (o < H) k.gstate[(long long)(b0 + b) * H + o] = g[m];
@@ -428,6 +544,19 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
       np[0] = pC[m];
       np[Hp] = pGv[m];
       np[2 * Hp] = pA[m];
+    }
+  }
+  if constexpr (FUSE) {
+    // This workgroup's share of the recurrent parameter gradients, synapse
+    // (i = o, j = r0 + rr), layout [workgroup][4][i][j] as rec_grad_kernel's.
+    const long long HH = (long long)Hp * Hp;
+    float* out = k.rpart + (long long)blockIdx.x * 4 * HH + (long long)o * Hp + r0;
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      out[rr] = gacc[rr].x;
+      out[HH + rr] = gacc[rr].y;
+      out[2 * HH + rr] = gacc[rr].z;
+      out[3 * HH + rr] = gacc[rr].w;
     }
   }
 }
@@ -632,6 +761,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const long long HH = (long long)Hp * Hp;
     const float* src = k.rpart + (long long)i * Hp + j;
     float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll 8
     for (int z = 0; z < k.NCH; ++z) {
       const float* pz = src + (long long)z * 4 * HH;
       s0 += pz[0];
@@ -652,6 +782,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const long long DH = (long long)Dp * Hp;
     const float* src = k.spart + (long long)h * Dp + d;
     float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+#pragma unroll 8
     for (int z = 0; z < k.NRC; ++z) {
       const float* pz = src + (long long)z * 4 * DH;
       s1 += pz[0];
@@ -671,6 +802,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
   if (tid < H) {
     const int j = (int)tid;
     float c = 0.f, gv = 0.f, ga = 0.f;
+#pragma unroll 8
     for (int b = 0; b < k.B; ++b) {
       const float* np = k.npart + (long long)b * 3 * Hp + j;
       c += np[0];
@@ -687,6 +819,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const long long row = tid / D;
     const int d = (int)(tid - row * D);
     float s = 0.f;
+#pragma unroll 4
     for (int hb = 0; hb < k.HB; ++hb) s += k.dxpart[((long long)hb * k.BT + row) * Dp + d];
     k.g.x[tid] = s;
   }
@@ -721,12 +854,24 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
   const size_t lds = bwd_lds_bytes(p);
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
-  switch (rcp) {
-    case 4: hipLaunchKernelGGL((ode_bwd_kernel<NB, 4>), grid, block, lds, s, a); break;
-    case 8: hipLaunchKernelGGL((ode_bwd_kernel<NB, 8>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((ode_bwd_kernel<NB, 16>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((ode_bwd_kernel<NB, 0>), grid, block, lds, s, a); break;
+#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
+  if (p.FUSE) {
+    // Only the spill-free pairs of ode_fuse_ok() are instantiated.
+    if constexpr (ode_fuse_ok(NB, 8)) {
+      if (rcp == 8) LTC_BWD(8, true);
+    }
+    if constexpr (ode_fuse_ok(NB, 4)) {
+      if (rcp == 4) LTC_BWD(4, true);
+    }
+  } else {
+    switch (rcp) {
+      case 4: LTC_BWD(4, false); break;
+      case 8: LTC_BWD(8, false); break;
+      case 16: LTC_BWD(16, false); break;
+      default: LTC_BWD(0, false); break;
+    }
   }
+#undef LTC_BWD
   return hipGetLastError();
 }
 
@@ -745,16 +890,32 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
                            float* sn, float* sd, hipStream_t s) {
   const int BT = p.B * p.T;
   const int hb = p.Hp / 64;
-  int rpw = 8;
-  while (rpw > 1 && (long long)hb * ((BT + 4 * rpw - 1) / (4 * rpw)) < 1024) rpw >>= 1;
   const dim3 block(256);
-  const dim3 grid(hb, (BT + 4 * rpw - 1) / (4 * rpw));
-  switch (rpw) {
-    case 8: hipLaunchKernelGGL(sens_fwd_kernel<8>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
-    case 4: hipLaunchKernelGGL(sens_fwd_kernel<4>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
-    case 2: hipLaunchKernelGGL(sens_fwd_kernel<2>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
-    default: hipLaunchKernelGGL(sens_fwd_kernel<1>, grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd); break;
+  // Many rows: 4 row groups per workgroup sharing operands through L1.
+  // Few rows: split D over the waves instead, so each thread's chain of
+  // dependent operand loads is 4x shorter.
+  const bool split_d = (long long)hb * ((BT + 3) / 4) < 512;
+  int rpw = 8;
+  const int rows_of = split_d ? 1 : 4;
+  while (rpw > 1 && (long long)hb * ((BT + rows_of * rpw - 1) / (rows_of * rpw)) < 1024) rpw >>= 1;
+  const dim3 grid(hb, (BT + rows_of * rpw - 1) / (rows_of * rpw));
+#define LTC_SENS(R, DSV) hipLaunchKernelGGL((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd)
+  if (split_d) {
+    switch (rpw) {
+      case 8: LTC_SENS(8, 4); break;
+      case 4: LTC_SENS(4, 4); break;
+      case 2: LTC_SENS(2, 4); break;
+      default: LTC_SENS(1, 4); break;
+    }
+  } else {
+    switch (rpw) {
+      case 8: LTC_SENS(8, 1); break;
+      case 4: LTC_SENS(4, 1); break;
+      case 2: LTC_SENS(2, 1); break;
+      default: LTC_SENS(1, 1); break;
+    }
   }
+#undef LTC_SENS
   return hipGetLastError();
 }
 
@@ -775,9 +936,9 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
 hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           const float* densave, const float* gout, Strides3 gs,
                           const float* ghfin, float2* absave, float* dsn, float* dsd,
-                          float* npart, float* gstate, hipStream_t s) {
+                          float* npart, float* gstate, float* rpart, hipStream_t s) {
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
-         p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC};
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC};
   switch (p.NB) {
     case 16: return bwd_by_rcp<16>(p, a, s);
     case 8: return bwd_by_rcp<8>(p, a, s);

@@ -14,6 +14,19 @@ namespace ltc {
 // threads; the same bound is the kernels' __launch_bounds__.
 constexpr int ode_max_threads(int nb) { return nb <= 2 ? 1024 : (nb <= 4 ? 512 : 256); }
 
+// Rows each thread finishes per unfold (the compile-time size of its per-row
+// registers). The launch plan keeps ceil(NB / KS) within it: KS >= 4 when NB >= 4.
+constexpr int ode_owned_rows(int nb) { return nb <= 2 ? nb : nb / 4; }
+
+// (NB, RC) pairs whose chain kernel can also keep the four recurrent
+// gradient accumulators of every register-resident operand without spilling
+// at the register budget __launch_bounds__(ode_max_threads(NB)) leaves
+// (checked against the compiled code objects: zero scratch).
+constexpr bool ode_fuse_ok(int nb, int rc) {
+  return (nb == 1 && rc == 4) || (nb == 4 && (rc == 4 || rc == 8)) ||
+         (nb == 8 && (rc == 4 || rc == 8)) || (nb == 16 && rc == 4);
+}
+
 // Kernel ids for the optional event-timing facility.
 enum KernelId : int {
   K_PREP = 0,
@@ -33,7 +46,8 @@ struct Plan {
   int NB;          // batch rows per workgroup in the persistent ODE kernels
   int KS;          // split of the reduction axis across waves of one workgroup
   int RC;          // reduction chunk per thread = Hp / KS
-  int NCH;         // n-chunks of the recurrent parameter-gradient reduction
+  bool FUSE;       // recurrent parameter gradients accumulated inside the chain kernel
+  int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances
 };
@@ -80,7 +94,7 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
 hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           const float* densave, const float* gout, Strides3 gs,
                           const float* ghfin, float2* absave, float* dsn, float* dsd,
-                          float* npart, float* gstate, hipStream_t s);
+                          float* npart, float* gstate, float* rpart, hipStream_t s);
 hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
                            const float2* absave, float* rpart, hipStream_t s);
 hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,

@@ -55,7 +55,7 @@ class CApi:
         "ltc_kernel_count", "ltc_kernel_name",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
-                   "NRC", "ode_workgroups")
+                   "NRC", "ode_workgroups", "fuse")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path

@@ -138,6 +138,15 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     assert p["NB"] in (1, 2, 4, 8, 16)
     assert p["KS"] >= 1 and p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 4 == 0
     assert p["threads"] == p["Hp"] * p["KS"] <= _max_threads(p["NB"])
+    # rows finished per thread fit the kernel's compile-time per-row registers
+    owned = p["NB"] if p["NB"] <= 2 else p["NB"] // 4
+    assert -(-p["NB"] // p["KS"]) <= owned
     assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
-    assert 1 <= p["NCH"] <= 64 and 1 <= p["NRC"] <= 64
+    assert 1 <= p["NRC"] <= 64
+    if p["fuse"]:
+        # one partial per chain workgroup; operands and accumulators in registers
+        assert p["RC"] in (4, 8, 16) and p["NCH"] == p["ode_workgroups"]
+        assert (p["NB"], p["RC"]) in ((1, 4), (4, 4), (4, 8), (8, 4), (8, 8), (16, 4))
+    else:
+        assert 1 <= p["NCH"] <= 64
     assert p["ode_workgroups"] * p["NB"] >= B > (p["ode_workgroups"] - 1) * p["NB"] or B == 0
