@@ -159,13 +159,15 @@ def roofline(c, ktimes, traffic=None):
     return r
 
 
-def issue_fraction(c, t_ms, which):
-    """Mix-aware VALU bound: minimum lane-slots per synapse over measured time.
+R_TRANS = 2.0  # measured on gfx950: v_exp_f32 / v_rcp_f32 cost 2 lane-slots (probes/issue_rate)
 
-    Forward 4 FMA-class + 2 transcendental, backward 12 + 2; transcendentals
-    cost r = 4 lane-slots (quarter rate).
+
+def issue_fraction(c, t_ms, which, r=R_TRANS):
+    """Mix-aware VALU bound over measured time.
+
+    Minimum lane-slots per synapse: forward 4 FMA-class + 2 transcendental,
+    backward 12 + 2; a transcendental costs r lane-slots.
     """
-    r = 4.0
     per = {"fwd": 4 + 2 * r, "fwdbwd": 16 + 4 * r}[which]
     return n_syn(c) * per / LANE_SLOTS_PER_S / (t_ms * 1e-3)
 
@@ -253,6 +255,7 @@ def measure_large(name, c, capi):
     ksum = sum(v[0] * v[1] for v in kt.values())
     rec["kernel_ms_sum"] = round(ksum, 4)
     rec["issue_frac_kernels"] = round(issue_fraction(c, ksum, which), 4)
+    rec["issue_frac_kernels_r4"] = round(issue_fraction(c, ksum, which, 4.0), 4)
     rec["flop_frac_kernels"] = round(
         n_syn(c) * (10 if which == "fwd" else 32) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
     del m, x, target
@@ -348,6 +351,7 @@ def main():
         "kernel_ms_sum": round(ksum, 5),
         "issue_frac_step": round(issue_fraction(c, ms, "fwdbwd"), 5),
         "issue_frac_kernels": round(issue_fraction(c, ksum, "fwdbwd"), 5),
+        "issue_frac_kernels_r4": round(issue_fraction(c, ksum, "fwdbwd", 4.0), 5),
         "roofline": roofline(c, kt, load_traffic("C1")),
         "vs_reference_gtx1080_published": round(REF_GTX1080_MS / ms, 3),
     }

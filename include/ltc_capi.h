@@ -123,16 +123,75 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
                       void* workspace, long long workspace_bytes, void* stream);
 
 /*
+ * Module-level path: the whole TrueLiquidTimeConstant.forward
+ * (reference ltc.py:249-326) and its backward in one call each. The caller
+ * passes the module's leaves instead of the boundary tensors, and the
+ * library computes the pre-transforms of ltc.py:259-283 itself:
+ *   xa = LayerNorm(x; ln_weight, ln_bias, ln_eps) * input_w + input_b
+ *   w_pos = softplus(w) * mask, w_erev = w_pos * erev,
+ *   cm_t = softplus(cm) / (dt / ode_unfolds), gleak_pos = softplus(gleak),
+ *   sensory_w_pos = softplus(sensory_w) * sensory_mask
+ * (softplus with torch's threshold 20). The backward returns gradients
+ * with respect to the leaves. No counterpart in the reference, whose
+ * module runs these steps as separate PyTorch ops around the fused call
+ * (ltc.py:259-307). D <= 1024; larger inputs use ltc_full_forward.
+ * `saved` holds ltc_module_saved_floats() floats: the boundary's saved
+ * buffer followed by the normalised input and its row statistics.
+ */
+long long ltc_module_saved_floats(int B, int T, int D, int H, int ode_unfolds);
+long long ltc_module_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds);
+long long ltc_module_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds);
+
+int ltc_module_forward(const float* x, long long sxb, long long sxt, long long sxd,
+                       const float* state,
+                       const float* w, const float* erev, const float* mask,
+                       const float* mu, const float* sigma,
+                       const float* sensory_w, const float* sensory_erev,
+                       const float* sensory_mask, const float* sensory_mu,
+                       const float* sensory_sigma,
+                       const float* gleak, const float* vleak, const float* cm,
+                       const float* input_w, const float* input_b,
+                       const float* ln_weight, const float* ln_bias,
+                       int B, int T, int D, int H, int ode_unfolds, float dt, float epsilon,
+                       float ln_eps, int save_intermediates,
+                       float* out, float* h_final, float* saved,
+                       void* workspace, long long workspace_bytes, void* stream);
+
+int ltc_module_backward(const float* x, long long sxb, long long sxt, long long sxd,
+                        const float* w, const float* erev, const float* mask,
+                        const float* mu, const float* sigma,
+                        const float* sensory_w, const float* sensory_erev,
+                        const float* sensory_mask, const float* sensory_mu,
+                        const float* sensory_sigma,
+                        const float* gleak, const float* vleak, const float* cm,
+                        const float* input_w, const float* input_b,
+                        const float* ln_weight, const float* ln_bias,
+                        const float* saved,
+                        const float* grad_out, long long sgb, long long sgt, long long sgh,
+                        const float* grad_h_final,
+                        int B, int T, int D, int H, int ode_unfolds, float dt, float epsilon,
+                        float ln_eps,
+                        float* grad_x, float* grad_state,
+                        float* grad_w, float* grad_erev, float* grad_mu, float* grad_sigma,
+                        float* grad_sensory_w, float* grad_sensory_erev,
+                        float* grad_sensory_mu, float* grad_sensory_sigma,
+                        float* grad_gleak, float* grad_vleak, float* grad_cm,
+                        float* grad_input_w, float* grad_input_b,
+                        float* grad_ln_weight, float* grad_ln_bias,
+                        void* workspace, long long workspace_bytes, void* stream);
+
+/*
  * Launch plan of one call, for diagnostics and host-side bounds tests. No
  * counterpart in the reference. Writes up to n of: Hp, Dp, NB (batch rows
  * per ODE workgroup), KS (reduction split), RC (= Hp/KS), threads per ODE
  * workgroup, forward LDS bytes, backward LDS bytes, NCH (recurrent gradient
  * chunks, or one per workgroup when fused), NRC (sensory backward row
- * chunks), ODE workgroups, and 1 when the recurrent parameter gradients are
- * accumulated inside the chain kernel. Returns the number of values written,
- * or -1 for invalid sizes.
+ * chunks), ODE workgroups, 1 when the recurrent parameter gradients are
+ * accumulated inside the chain kernel, and 1 when the chain kernel stages
+ * each time step's saved states in LDS. Returns the number of values
+ * written, or -1 for invalid sizes.
  */
-#define LTC_PLAN_FIELDS 12
+#define LTC_PLAN_FIELDS 13
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

@@ -77,6 +77,14 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
   // the chain kernel also accumulates the recurrent parameter gradients and
   // writes one partial per workgroup.
   p.FUSE = ltc::ode_fuse_ok(p.NB, p.RC);
+  // Step staging for the chain kernel: two step buffers of (2U+1)*NB*Hp
+  // floats next to its other LDS arrays, at most 8 staged floats per thread.
+  {
+    const long long slots = (2LL * U + 1) * p.NB * p.Hp;
+    const long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4;
+    p.STAGE = ltc::ode_stage_ok(p.NB) && base + 2 * slots * 4 <= 65536 &&
+              slots <= 8LL * p.Hp * p.KS;
+  }
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
   if (p.FUSE) {
@@ -165,9 +173,31 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   return w;
 }
 
+// Module-path extras: the normalised input and its row statistics live in the
+// saved buffer when training (the backward reads them), else in the workspace.
+struct LnWs {
+  float* xa;
+  float* stats;
+};
+
+LnWs carve_ln(const ltc::Plan& p, Carver& c) {
+  LnWs w{};
+  w.xa = c.take<float>((long long)p.B * p.T * p.D);
+  w.stats = c.take<float>(2LL * p.B * p.T);
+  return w;
+}
+
 long long saved_floats(const ltc::Plan& p) {
   // vsave: T*U+1 slots of (B,Hp); densave: T*U slots of (B,Hp).
   return ((long long)p.T * p.U + 1) * p.B * p.Hp + (long long)p.T * p.U * p.B * p.Hp;
+}
+
+long long module_saved_floats(const ltc::Plan& p) {
+  // boundary saved buffer, then xa and stats at 64-float (256-byte) alignment
+  Carver c{nullptr};
+  c.take<float>(saved_floats(p));
+  carve_ln(p, c);
+  return (c.off + 3) / 4;
 }
 
 int check_dims(int B, int T, int D, int H, int U) {
@@ -187,7 +217,7 @@ int check_dims(int B, int T, int D, int H, int U) {
 // ---------------------------------------------------------------------------
 const char* const kNames[ltc::K_COUNT] = {"ltc_prep",     "ltc_sens_fwd", "ltc_ode_fwd",
                                           "ltc_ode_bwd",  "ltc_rec_grad", "ltc_sens_bwd",
-                                          "ltc_finalize"};
+                                          "ltc_ln_bwd",   "ltc_finalize"};
 
 struct Timing {
   std::mutex mu;
@@ -443,14 +473,233 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
   return LTC_OK;
 }
 
+long long ltc_module_saved_floats(int B, int T, int D, int H, int ode_unfolds) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || D > ltc::kModuleMaxD) return -1;
+  return module_saved_floats(make_plan(B, T, D, H, ode_unfolds));
+}
+
+long long ltc_module_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || D > ltc::kModuleMaxD) return -1;
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_fwd(p, c);
+  carve_ln(p, c);  // used when nothing is saved (inference)
+  return round_up(c.off, 256);
+}
+
+long long ltc_module_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds) {
+  if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || D > ltc::kModuleMaxD) return -1;
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_bwd(p, c);
+  c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  return round_up(c.off, 256);
+}
+
+namespace {
+
+int check_leaves(const ltc::LeafParams& lp) {
+  if (!lp.w || !lp.erev || !lp.mask || !lp.mu || !lp.sigma || !lp.s_w || !lp.s_erev ||
+      !lp.s_mask || !lp.s_mu || !lp.s_sigma || !lp.gleak || !lp.vleak || !lp.cm ||
+      !lp.input_w || !lp.input_b || !lp.ln_w || !lp.ln_b)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (!(lp.dtU > 0.f)) return fail(LTC_EINVAL, "dt / ode_unfolds must be positive");
+  return LTC_OK;
+}
+
+}  // namespace
+
+int ltc_module_forward(const float* x, long long sxb, long long sxt, long long sxd,
+                       const float* state, const float* w, const float* erev, const float* mask,
+                       const float* mu, const float* sigma, const float* sensory_w,
+                       const float* sensory_erev, const float* sensory_mask,
+                       const float* sensory_mu, const float* sensory_sigma, const float* gleak,
+                       const float* vleak, const float* cm, const float* input_w,
+                       const float* input_b, const float* ln_weight, const float* ln_bias,
+                       int B, int T, int D, int H, int ode_unfolds, float dt, float epsilon,
+                       float ln_eps, int save_intermediates, float* out, float* h_final,
+                       float* saved, void* workspace, long long workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_dims(B, T, D, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (D > ltc::kModuleMaxD)
+    return fail(LTC_EUNSUPPORTED, "module path handles D <= " + std::to_string(ltc::kModuleMaxD));
+  const ltc::LeafParams lp{w, erev, mask, mu, sigma, sensory_w, sensory_erev, sensory_mask,
+                           sensory_mu, sensory_sigma, gleak, vleak, cm, input_w, input_b,
+                           ln_weight, ln_bias, (float)((double)dt / ode_unfolds), ln_eps};
+  rc = check_leaves(lp);
+  if (rc != LTC_OK) return rc;
+  if (B > 0 && (!state || !h_final)) return fail(LTC_EINVAL, "state/h_final pointer is NULL");
+  if ((long long)B * T > 0 && (!x || !out)) return fail(LTC_EINVAL, "x/out pointer is NULL");
+  if (save_intermediates && !saved) return fail(LTC_EINVAL, "saved pointer is NULL");
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_fwd(p, need);
+  carve_ln(p, need);
+  if (workspace_bytes < need.off || (need.off > 0 && !workspace))
+    return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
+  if (B == 0) return LTC_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (T == 0) {
+    hipError_t e = hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
+                                  hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
+    return LTC_OK;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  const FwdWs wfw = carve_fwd(p, c);
+  LnWs lw = carve_ln(p, c);
+  float* vsave = nullptr;
+  float* densave = nullptr;
+  if (save_intermediates) {
+    vsave = saved;
+    densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
+    Carver sc{reinterpret_cast<char*>(saved)};
+    sc.take<float>(saved_floats(p));
+    lw = carve_ln(p, sc);
+  }
+  const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
+  const ltc::Strides3 xas{(long long)T * D, D, 1};
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, wfw.pp, false, &ln, s); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = timed(ltc::K_SENS_FWD, s,
+            [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, wfw.pp, wfw.sn, wfw.sd, s); });
+  if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  e = timed(ltc::K_ODE_FWD, s, [&] {
+    return ltc::launch_ode_fwd(p, wfw.pp, wfw.sn, wfw.sd, state, epsilon, out, h_final, vsave,
+                               densave, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  return LTC_OK;
+}
+
+int ltc_module_backward(const float* x, long long sxb, long long sxt, long long sxd,
+                        const float* w, const float* erev, const float* mask, const float* mu,
+                        const float* sigma, const float* sensory_w, const float* sensory_erev,
+                        const float* sensory_mask, const float* sensory_mu,
+                        const float* sensory_sigma, const float* gleak, const float* vleak,
+                        const float* cm, const float* input_w, const float* input_b,
+                        const float* ln_weight, const float* ln_bias, const float* saved,
+                        const float* grad_out, long long sgb, long long sgt, long long sgh,
+                        const float* grad_h_final, int B, int T, int D, int H, int ode_unfolds,
+                        float dt, float epsilon, float ln_eps, float* grad_x, float* grad_state,
+                        float* grad_w, float* grad_erev, float* grad_mu, float* grad_sigma,
+                        float* grad_sensory_w, float* grad_sensory_erev, float* grad_sensory_mu,
+                        float* grad_sensory_sigma, float* grad_gleak, float* grad_vleak,
+                        float* grad_cm, float* grad_input_w, float* grad_input_b,
+                        float* grad_ln_weight, float* grad_ln_bias, void* workspace,
+                        long long workspace_bytes, void* stream) {
+  g_err.clear();
+  (void)epsilon;  // the saved denominators already include it
+  int rc = check_dims(B, T, D, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (D > ltc::kModuleMaxD)
+    return fail(LTC_EUNSUPPORTED, "module path handles D <= " + std::to_string(ltc::kModuleMaxD));
+  const ltc::LeafParams lp{w, erev, mask, mu, sigma, sensory_w, sensory_erev, sensory_mask,
+                           sensory_mu, sensory_sigma, gleak, vleak, cm, input_w, input_b,
+                           ln_weight, ln_bias, (float)((double)dt / ode_unfolds), ln_eps};
+  rc = check_leaves(lp);
+  if (rc != LTC_OK) return rc;
+  const ltc::LeafGrads lg{grad_x, grad_w, grad_erev, grad_mu, grad_sigma, grad_sensory_w,
+                          grad_sensory_erev, grad_sensory_mu, grad_sensory_sigma, grad_gleak,
+                          grad_vleak, grad_cm, grad_input_w, grad_input_b, grad_ln_weight,
+                          grad_ln_bias};
+  if (!lg.w || !lg.erev || !lg.mu || !lg.sigma || !lg.s_w || !lg.s_erev || !lg.s_mu ||
+      !lg.s_sigma || !lg.gleak || !lg.vleak || !lg.cm || !lg.input_w || !lg.input_b ||
+      !lg.ln_w || !lg.ln_b)
+    return fail(LTC_EINVAL, "gradient output pointer is NULL");
+  if (B > 0 && !grad_state) return fail(LTC_EINVAL, "grad_state pointer is NULL");
+  if ((long long)B * T > 0 && (!x || !grad_out || !grad_x || !saved))
+    return fail(LTC_EINVAL, "x/grad_out/grad_x/saved pointer is NULL");
+  const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_bwd(p, need);
+  need.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  if (workspace_bytes < need.off || (need.off > 0 && !workspace))
+    return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if ((long long)B * T == 0) {
+    float* zs[] = {grad_w, grad_erev, grad_mu, grad_sigma};
+    for (float* z : zs) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zd[] = {grad_sensory_w, grad_sensory_erev, grad_sensory_mu, grad_sensory_sigma};
+    for (float* z : zd) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zh[] = {grad_gleak, grad_vleak, grad_cm};
+    for (float* z : zh) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zx[] = {grad_input_w, grad_input_b, grad_ln_weight, grad_ln_bias};
+    for (float* z : zx) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    if (B > 0) {
+      hipError_t e = grad_h_final
+                         ? hipMemcpyAsync(grad_state, grad_h_final, (size_t)B * H * sizeof(float),
+                                          hipMemcpyDeviceToDevice, s)
+                         : hipMemsetAsync(grad_state, 0, (size_t)B * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("grad_state copy", e);
+    }
+    return LTC_OK;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  const BwdWs wb = carve_bwd(p, c);
+  float* lnpart = c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  Carver sc{const_cast<char*>(reinterpret_cast<const char*>(saved))};
+  sc.take<float>(saved_floats(p));
+  const LnWs lw = carve_ln(p, sc);
+  const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
+  const ltc::Strides3 xas{(long long)T * D, D, 1};
+  const ltc::Strides3 gs{sgb, sgt, sgh};
+  const float* vsave = saved;
+  const float* densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, wb.pp, true, nullptr, s); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = timed(ltc::K_ODE_BWD, s, [&] {
+    return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.absave,
+                               wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+  if (!p.FUSE) {
+    e = timed(ltc::K_REC_GRAD, s,
+              [&] { return ltc::launch_rec_grad(p, wb.pp, vsave, wb.absave, wb.rpart, s); });
+    if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  }
+  e = timed(ltc::K_SENS_BWD, s, [&] {
+    return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s);
+  });
+  if (e != hipSuccess) return hip_fail("sensory backward launch", e);
+  e = timed(ltc::K_LN_BWD, s,
+            [&] { return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s); });
+  if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
+  e = timed(ltc::K_FINALIZE, s, [&] {
+    return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, lg, s);
+  });
+  if (e != hipSuccess) return hip_fail("finalize launch", e);
+  return LTC_OK;
+}
+
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n) {
   if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || !out || n < 0) return -1;
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, (long long)p.Hp * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8,
-      (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4,
-      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0};
+      (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4 +
+          (p.STAGE ? 2 * (2LL * ode_unfolds + 1) * p.NB * p.Hp * 4 : 0),
+      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0, p.STAGE ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -341,6 +341,10 @@ struct BwdK {
   int B, T, H, Hp, U, KS, RC;
 };
 
+constexpr int kStageRegs = 8;  // staged floats per thread and step (plan keeps (2U+1)*NB*Hp within)
+
+__device__ __forceinline__ int b0_of(const BwdK&, int nb) { return blockIdx.x * nb; }
+
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
 // FUSE the parameter-gradient sums of this synapse ride along in gacc:
 // {sum alpha*a, sum beta*a, sum delta, sum delta*v_i}.
@@ -400,7 +404,12 @@ __device__ __forceinline__ void bwd_load_gout(const BwdK& k, int t, int b0, int 
 // FUSE (register-resident operands only): each operand also carries its
 // gradient accumulators, which removes the separate parameter-gradient pass
 // and its second gate evaluation.
-template <int NB, int RCP, bool FUSE>
+// STAGE: the saved states and denominators of a whole time step (all U
+// unfolds, the tile's NB rows) are copied into an LDS double buffer one step
+// ahead: the loads are issued at the start of a step and written to LDS at
+// its end, so every unfold reads its operands from LDS and pays no global
+// load latency. Used when two step buffers fit next to the other LDS arrays.
+template <int NB, int RCP, bool FUSE, bool STAGE>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   static_assert(!FUSE || RCP > 0, "fused gradients need register-resident operands");
   constexpr int MO = ode_owned_rows(NB);
@@ -409,6 +418,36 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   const int RC = RCP > 0 ? RCP : k.RC;
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][Hp]
+  float* stg = red + KS * NB * Hp;                      // [2][2U+1][NB][Hp] when STAGE
+  const int SL = (2 * U + 1) * NB * Hp;                 // floats per step buffer
+  const int NBHp = NB * Hp;
+  float sreg[STAGE ? kStageRegs : 1];
+  // Step t's slots: v^0..v^U (U+1 slots) then den^0..den^{U-1}; rows past B
+  // read as v = 0, den = 1.
+  auto stage_issue = [&](int t) {
+#pragma unroll
+    for (int q = 0; q < kStageRegs; ++q) {
+      const int e = threadIdx.x + q * blockDim.x;
+      float v = 0.f;
+      if (e < SL) {
+        const int slot = e / NBHp, w = e - slot * NBHp;
+        if (b0_of(k, NB) + w / Hp < B) {
+          v = slot <= U ? k.vsave[(((long long)t * U + slot) * B + b0_of(k, NB)) * Hp + w]
+                        : k.densave[(((long long)t * U + slot - U - 1) * B + b0_of(k, NB)) * Hp + w];
+        } else if (slot > U) {
+          v = 1.f;
+        }
+      }
+      sreg[q] = v;
+    }
+  };
+  auto stage_commit = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < kStageRegs; ++q) {
+      const int e = threadIdx.x + q * blockDim.x;
+      if (e < SL) stg[buf * SL + e] = sreg[q];
+    }
+  };
   const int tid = threadIdx.x;
   const int ks = tid / Hp, o = tid - ks * Hp;
   const int b0 = blockIdx.x * NB;
@@ -436,19 +475,28 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   }
   if (T == 0) return;
 
-  // Software pipeline: the operands of the next unfold (and the next step's
-  // output gradient) are requested one unfold ahead; LDS-only barriers keep
-  // those loads in flight.
+  // Operands of the current unfold; without STAGE they are software-pipelined
+  // one unfold ahead from global memory, with STAGE they come from LDS.
   float cvi[NB], cden[MO], cvk[MO], cvk1[MO];
   float nvi[NB], nden[MO], nvk[MO], nvk1[MO];
   float gcur[MO], gnext[MO];
 #pragma unroll
   for (int m = 0; m < MO; ++m) gnext[m] = 0.f;
-  bwd_load_unfold<NB, MO>(k, (long long)T * U - 1, b0, ks, o, cvi, cden, cvk, cvk1);
+  int cur = 0;
+  if constexpr (STAGE) {
+    stage_issue(T - 1);
+    stage_commit(0);
+    lds_barrier();
+  } else {
+    bwd_load_unfold<NB, MO>(k, (long long)T * U - 1, b0, ks, o, cvi, cden, cvk, cvk1);
+  }
   bwd_load_gout<NB, MO>(k, T - 1, b0, ks, o, gcur);
 
   for (int t = T - 1; t >= 0; --t) {
-    if (t > 0) bwd_load_gout<NB, MO>(k, t - 1, b0, ks, o, gnext);
+    if (t > 0) {
+      bwd_load_gout<NB, MO>(k, t - 1, b0, ks, o, gnext);
+      if constexpr (STAGE) stage_issue(t - 1);
+    }
     float accA[MO], accB[MO];
 #pragma unroll
     for (int m = 0; m < MO; ++m) {
@@ -457,7 +505,22 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
     }
     for (int u = U - 1; u >= 0; --u) {
       const long long n = (long long)t * U + u;
-      if (n > 0) bwd_load_unfold<NB, MO>(k, n - 1, b0, ks, o, nvi, nden, nvk, nvk1);
+      if constexpr (STAGE) {
+        const float* sb = stg + cur * SL;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) cvi[b] = sb[(u * NB + b) * Hp + o];
+#pragma unroll
+        for (int m = 0; m < MO; ++m) {
+          const int b = ks + m * KS;
+          if (b < NB) {
+            cvk[m] = sb[(u * NB + b) * Hp + o];
+            cvk1[m] = sb[((u + 1) * NB + b) * Hp + o];
+            cden[m] = sb[((U + 1 + u) * NB + b) * Hp + o];
+          }
+        }
+      } else {
+        if (n > 0) bwd_load_unfold<NB, MO>(k, n - 1, b0, ks, o, nvi, nden, nvk, nvk1);
+      }
       float gdir[MO];
 #pragma unroll
       for (int m = 0; m < MO; ++m) {
@@ -513,15 +576,24 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
           g[m] = o < H ? fmaf(kNegLn2, s, gdir[m]) : 0.f;
         }
       }
-      if (n > 0) {
+      if constexpr (!STAGE) {
+        if (n > 0) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) cvi[b] = nvi[b];
+          for (int b = 0; b < NB; ++b) cvi[b] = nvi[b];
 #pragma unroll
-        for (int m = 0; m < MO; ++m) {
-          cden[m] = nden[m];
-          cvk[m] = nvk[m];
-          cvk1[m] = nvk1[m];
+          for (int m = 0; m < MO; ++m) {
+            cden[m] = nden[m];
+            cvk[m] = nvk[m];
+            cvk1[m] = nvk1[m];
+          }
         }
+      }
+    }
+    if constexpr (STAGE) {
+      if (t > 0) {
+        stage_commit(cur ^ 1);
+        lds_barrier();
+        cur ^= 1;
       }
     }
 #pragma unroll
@@ -752,6 +824,21 @@ struct FinK {
   int B, D, H, Hp, Dp, NCH, NRC, HB, BT;
 };
 
+// Sum of n strided partials with 8 loads in flight per round.
+__device__ __forceinline__ float sum_partials(const float* p, long long stride, int n) {
+  float acc = 0.f;
+  int z = 0;
+  for (; z + 8 <= n; z += 8) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = p[(long long)(z + i) * stride];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += v[i];
+  }
+  for (; z < n; ++z) acc += p[(long long)z * stride];
+  return acc;
+}
+
 __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
@@ -760,15 +847,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
     const long long HH = (long long)Hp * Hp;
     const float* src = k.rpart + (long long)i * Hp + j;
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll 8
-    for (int z = 0; z < k.NCH; ++z) {
-      const float* pz = src + (long long)z * 4 * HH;
-      s0 += pz[0];
-      s1 += pz[HH];
-      s2 += pz[2 * HH];
-      s3 += pz[3 * HH];
-    }
+    const float s0 = sum_partials(src, 4 * HH, k.NCH);
+    const float s1 = sum_partials(src + HH, 4 * HH, k.NCH);
+    const float s2 = sum_partials(src + 2 * HH, 4 * HH, k.NCH);
+    const float s3 = sum_partials(src + 3 * HH, 4 * HH, k.NCH);
     k.g.w_erev[tid] = s0;
     k.g.w_pos[tid] = s1;
     k.g.mu[tid] = -k.rp.sigma[tid] * s2;
@@ -781,15 +863,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
     const long long DH = (long long)Dp * Hp;
     const float* src = k.spart + (long long)h * Dp + d;
-    float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
-#pragma unroll 8
-    for (int z = 0; z < k.NRC; ++z) {
-      const float* pz = src + (long long)z * 4 * DH;
-      s1 += pz[0];
-      s2 += pz[DH];
-      s3 += pz[2 * DH];
-      s4 += pz[3 * DH];
-    }
+    const float s1 = sum_partials(src, 4 * DH, k.NRC);
+    const float s2 = sum_partials(src + DH, 4 * DH, k.NRC);
+    const float s3 = sum_partials(src + 2 * DH, 4 * DH, k.NRC);
+    const float s4 = sum_partials(src + 3 * DH, 4 * DH, k.NRC);
     const long long e = (long long)d * H + h;
     const float Ws = k.rp.s_wpos[e], Ss = k.rp.s_sigma[e], Ms = k.rp.s_mu[e];
     k.g.s_wpos[e] = s1;
@@ -801,14 +878,10 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
   tid -= nsens;
   if (tid < H) {
     const int j = (int)tid;
-    float c = 0.f, gv = 0.f, ga = 0.f;
-#pragma unroll 8
-    for (int b = 0; b < k.B; ++b) {
-      const float* np = k.npart + (long long)b * 3 * Hp + j;
-      c += np[0];
-      gv += np[Hp];
-      ga += np[2 * Hp];
-    }
+    const float* src = k.npart + j;
+    const float c = sum_partials(src, 3LL * Hp, k.B);
+    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
+    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
     k.g.cm[j] = c;
     k.g.gleak[j] = k.rp.vleak[j] * ga - gv;
     k.g.vleak[j] = k.rp.gleak[j] * ga;
@@ -818,10 +891,284 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
   if (tid < (long long)k.BT * D) {
     const long long row = tid / D;
     const int d = (int)(tid - row * D);
-    float s = 0.f;
-#pragma unroll 4
-    for (int hb = 0; hb < k.HB; ++hb) s += k.dxpart[((long long)hb * k.BT + row) * Dp + d];
-    k.g.x[tid] = s;
+    k.g.x[tid] = sum_partials(k.dxpart + row * Dp + d, (long long)k.BT * Dp, k.HB);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Module path: pre-transforms and LayerNorm inside the library.
+// ---------------------------------------------------------------------------
+
+// torch's softplus (beta 1, threshold 20) and its derivative z/(z+1), z = e^x.
+__device__ __forceinline__ float softplus_t(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float softplus_grad(float x) {
+  if (x > 20.f) return 1.f;
+  const float z = expf(x);
+  return z / (z + 1.f);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+constexpr int kLnPerLane = kModuleMaxD / 64;  // row values each lane keeps
+
+// Parameter images from the leaves (same flat segments as prep_kernel), plus
+// LayerNorm + affine of the (b,t) rows in trailing blocks of the same launch:
+// one wave per row, the row held in registers (D <= kModuleMaxD), two-pass
+// mean/variance, xa = ((x - mean)*rstd*ln_w + ln_b)*input_w + input_b.
+__global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
+                                                        int Hp, int Dp, int bwd, int nprep_blocks,
+                                                        LnBuf ln, int T, int BT) {
+  if ((int)blockIdx.x >= nprep_blocks) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int row = ((int)blockIdx.x - nprep_blocks) * 4 + w;
+    if (row >= BT) return;
+    const int b = row / T, t = row - b * T;
+    const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
+    float xv[kLnPerLane];
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < kLnPerLane; ++c) {
+      const int d = lane + 64 * c;
+      xv[c] = d < D ? xr[d * ln.xs.c] : 0.f;
+      sum += xv[c];
+    }
+    const float mean = wave_sum(sum) / (float)D;
+    float sq = 0.f;
+#pragma unroll
+    for (int c = 0; c < kLnPerLane; ++c) {
+      const int d = lane + 64 * c;
+      const float dv = d < D ? xv[c] - mean : 0.f;
+      sq = fmaf(dv, dv, sq);
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)D + lp.ln_eps);
+    float* xo = ln.xa + (long long)row * D;
+#pragma unroll
+    for (int c = 0; c < kLnPerLane; ++c) {
+      const int d = lane + 64 * c;
+      if (d < D) {
+        const float xn = (xv[c] - mean) * rstd * lp.ln_w[d] + lp.ln_b[d];
+        xo[d] = xn * lp.input_w[d] + lp.input_b[d];
+      }
+    }
+    if (lane == 0) {
+      ln.stats[2LL * row] = mean;
+      ln.stats[2LL * row + 1] = rstd;
+    }
+    return;
+  }
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long nrec = (long long)Hp * Hp;
+  const long long nsens = (long long)Dp * Hp;
+  if (tid < nrec) {
+    const int i = (int)(tid / Hp), j = (int)(tid - (long long)i * Hp);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < H && j < H) {
+      const long long e = (long long)i * H + j;
+      const float S = lp.sigma[e], M = lp.mu[e];
+      const float wp = softplus_t(lp.w[e]) * lp.mask[e];
+      v = make_float4(-S * kLog2e, S * M * kLog2e, wp * lp.erev[e], wp);
+    }
+    pp.recF[tid] = v;
+    if (bwd) pp.recB[(long long)j * Hp + i] = v;
+    return;
+  }
+  tid -= nrec;
+  if (tid < nsens) {
+    const int d = (int)(tid / Hp), h = (int)(tid - (long long)d * Hp);
+    float4 f = make_float4(0.f, 0.f, 0.f, 0.f), g = f;
+    if (d < D && h < H) {
+      const long long e = (long long)d * H + h;
+      const float Ss = lp.s_sigma[e], Ms = lp.s_mu[e], Es = lp.s_erev[e];
+      const float Ws = softplus_t(lp.s_w[e]) * lp.s_mask[e];
+      f = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * Es, Ws);
+      g = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Es, Ws * Ss);
+    }
+    if (bwd)
+      pp.sensB[(long long)h * Dp + d] = g;
+    else
+      pp.sensF[tid] = f;
+    return;
+  }
+  tid -= nsens;
+  if (tid < 3LL * Hp) {
+    const int q = (int)(tid / Hp), j = (int)(tid - (long long)q * Hp);
+    float v = 0.f;
+    if (j < H) {
+      if (q == 0) v = softplus_t(lp.cm[j]) / lp.dtU;
+      else if (q == 1) v = softplus_t(lp.gleak[j]);
+      else v = lp.vleak[j];
+    }
+    pp.neuron[tid] = v;
+  }
+}
+
+// LayerNorm + affine backward. Block 256 = 4 waves, kLnRows rows per block,
+// each wave takes rows w, w+4, ... With gxa = dL/dxa (sum of the h-block
+// partials), xh = (x - mean)*rstd, gxn = gxa*input_w, gxh = gxn*ln_w:
+//   dx = rstd*(gxh - mean_d(gxh) - xh*mean_d(gxh*xh))
+// and the column sums dinput_w = sum gxa*xn, dinput_b = sum gxa,
+// dln_w = sum gxn*xh, dln_b = sum gxn are accumulated per lane, combined over
+// the 4 waves in LDS in a fixed order and written as one partial per block.
+constexpr int kLnRows = 16;
+
+__global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, const float* dxpart,
+                                                     float* gx, float* lnpart, int T, int D,
+                                                     int Dp, int BT, int HB) {
+  __shared__ float col[4][kModuleMaxD];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float cw[kLnPerLane], cb[kLnPerLane], cl[kLnPerLane], cbl[kLnPerLane];
+  float iw[kLnPerLane], lw[kLnPerLane], lb[kLnPerLane];
+#pragma unroll
+  for (int c = 0; c < kLnPerLane; ++c) {
+    const int d = lane + 64 * c;
+    cw[c] = cb[c] = cl[c] = cbl[c] = 0.f;
+    iw[c] = d < D ? lp.input_w[d] : 0.f;
+    lw[c] = d < D ? lp.ln_w[d] : 0.f;
+    lb[c] = d < D ? lp.ln_b[d] : 0.f;
+  }
+  const long long hstride = (long long)BT * Dp;
+  for (int i = 0; i < kLnRows / 4; ++i) {
+    const int row = blockIdx.x * kLnRows + w + 4 * i;
+    if (row >= BT) break;
+    const int b = row / T, t = row - b * T;
+    const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
+    const float mean = ln.stats[2LL * row], rstd = ln.stats[2LL * row + 1];
+    float xh[kLnPerLane], gxh[kLnPerLane];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int c = 0; c < kLnPerLane; ++c) {
+      const int d = lane + 64 * c;
+      xh[c] = gxh[c] = 0.f;
+      if (d < D) {
+        float gxa = 0.f;
+        const float* pp = dxpart + (long long)row * Dp + d;
+        for (int hb = 0; hb < HB; ++hb) gxa += pp[hb * hstride];
+        xh[c] = (xr[d * ln.xs.c] - mean) * rstd;
+        const float xn = xh[c] * lw[c] + lb[c];
+        const float gxn = gxa * iw[c];
+        gxh[c] = gxn * lw[c];
+        cw[c] = fmaf(gxa, xn, cw[c]);
+        cb[c] += gxa;
+        cl[c] = fmaf(gxn, xh[c], cl[c]);
+        cbl[c] += gxn;
+        s1 += gxh[c];
+        s2 = fmaf(gxh[c], xh[c], s2);
+      }
+    }
+    const float m1 = wave_sum(s1) / (float)D, m2 = wave_sum(s2) / (float)D;
+    float* go = gx + (long long)row * D;
+#pragma unroll
+    for (int c = 0; c < kLnPerLane; ++c) {
+      const int d = lane + 64 * c;
+      if (d < D) go[d] = rstd * (gxh[c] - m1 - xh[c] * m2);
+    }
+  }
+  // Fixed-order combine of the 4 waves' column sums.
+  for (int wv = 0; wv < 4; ++wv) {
+    if (w == wv) {
+#pragma unroll
+      for (int c = 0; c < kLnPerLane; ++c) {
+        const int d = lane + 64 * c;
+        if (d < D) {
+          if (wv == 0) {
+            col[0][d] = cw[c];
+            col[1][d] = cb[c];
+            col[2][d] = cl[c];
+            col[3][d] = cbl[c];
+          } else {
+            col[0][d] += cw[c];
+            col[1][d] += cb[c];
+            col[2][d] += cl[c];
+            col[3][d] += cbl[c];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  float* out = lnpart + (long long)blockIdx.x * 4 * Dp;
+  for (int e = threadIdx.x; e < 4 * D; e += 256) {
+    const int q = e / D, d = e - q * D;
+    out[(long long)q * Dp + d] = col[q][d];
+  }
+}
+
+// Finalize of the module path: partial sums as finalize_kernel, then the
+// chain rule through the pre-transforms to the module's leaves.
+struct FinLeafK {
+  LeafParams lp;
+  const float* rpart;
+  const float* spart;
+  const float* npart;
+  const float* lnpart;
+  LeafGrads g;
+  int B, D, H, Hp, Dp, NCH, NRC, NLN;
+};
+
+__global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
+  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
+  const long long nrec = (long long)H * H, nsens = (long long)D * H;
+  if (tid < nrec) {
+    const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
+    const long long HH = (long long)Hp * Hp;
+    const float* src = k.rpart + (long long)i * Hp + j;
+    const float dwe = sum_partials(src, 4 * HH, k.NCH);
+    const float dwp = sum_partials(src + HH, 4 * HH, k.NCH);
+    const float sd = sum_partials(src + 2 * HH, 4 * HH, k.NCH);
+    const float sdv = sum_partials(src + 3 * HH, 4 * HH, k.NCH);
+    const float wv = k.lp.w[tid], mk = k.lp.mask[tid], ev = k.lp.erev[tid];
+    const float wpos = softplus_t(wv) * mk;
+    // w_pos feeds the synapse directly and through w_erev = w_pos * erev.
+    k.g.w[tid] = (dwp + dwe * ev) * mk * softplus_grad(wv);
+    k.g.erev[tid] = dwe * wpos;
+    k.g.mu[tid] = -k.lp.sigma[tid] * sd;
+    k.g.sigma[tid] = sdv - k.lp.mu[tid] * sd;
+    return;
+  }
+  tid -= nrec;
+  if (tid < nsens) {
+    const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
+    const long long DH = (long long)Dp * Hp;
+    const float* src = k.spart + (long long)h * Dp + d;
+    const float s1 = sum_partials(src, 4 * DH, k.NRC);
+    const float s2 = sum_partials(src + DH, 4 * DH, k.NRC);
+    const float s3 = sum_partials(src + 2 * DH, 4 * DH, k.NRC);
+    const float s4 = sum_partials(src + 3 * DH, 4 * DH, k.NRC);
+    const long long e = (long long)d * H + h;
+    const float sw = k.lp.s_w[e], mk = k.lp.s_mask[e];
+    const float Ws = softplus_t(sw) * mk, Ss = k.lp.s_sigma[e], Ms = k.lp.s_mu[e];
+    k.g.s_w[e] = s1 * mk * softplus_grad(sw);
+    k.g.s_erev[e] = Ws * s2;
+    k.g.s_mu[e] = -Ss * Ws * s3;
+    k.g.s_sigma[e] = Ws * (s4 - Ms * s3);
+    return;
+  }
+  tid -= nsens;
+  if (tid < H) {
+    const int j = (int)tid;
+    const float* src = k.npart + j;
+    const float c = sum_partials(src, 3LL * Hp, k.B);
+    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
+    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
+    const float gl = k.lp.gleak[j];
+    k.g.cm[j] = c / k.lp.dtU * softplus_grad(k.lp.cm[j]);
+    k.g.gleak[j] = (k.lp.vleak[j] * ga - gv) * softplus_grad(gl);
+    k.g.vleak[j] = softplus_t(gl) * ga;
+    return;
+  }
+  tid -= H;
+  if (tid < D) {
+    const int d = (int)tid;
+    const float* src = k.lnpart + d;
+    k.g.input_w[d] = sum_partials(src, 4LL * Dp, k.NLN);
+    k.g.input_b[d] = sum_partials(src + Dp, 4LL * Dp, k.NLN);
+    k.g.ln_w[d] = sum_partials(src + 2 * Dp, 4LL * Dp, k.NLN);
+    k.g.ln_b[d] = sum_partials(src + 3 * Dp, 4LL * Dp, k.NLN);
   }
 }
 
@@ -832,7 +1179,8 @@ size_t fwd_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * p.Hp * 8;
 }
 size_t bwd_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KS * p.NB * p.Hp * 4;
+  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KS * p.NB * p.Hp * 4 +
+         (p.STAGE ? (size_t)2 * (2 * p.U + 1) * p.NB * p.Hp * 4 : 0);
 }
 
 template <int NB>
@@ -849,12 +1197,12 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int NB>
-hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
+template <int NB, bool STAGE>
+hipError_t bwd_by_rcp_stage(const Plan& p, const BwdK& a, hipStream_t s) {
   const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
   const size_t lds = bwd_lds_bytes(p);
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
-#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
+#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F, STAGE>), grid, block, lds, s, a)
   if (p.FUSE) {
     // Only the spill-free pairs of ode_fuse_ok() are instantiated.
     if constexpr (ode_fuse_ok(NB, 8)) {
@@ -873,6 +1221,14 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   }
 #undef LTC_BWD
   return hipGetLastError();
+}
+
+template <int NB>
+hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
+  if constexpr (ode_stage_ok(NB)) {
+    if (p.STAGE) return bwd_by_rcp_stage<NB, true>(p, a, s);
+  }
+  return bwd_by_rcp_stage<NB, false>(p, a, s);
 }
 
 }  // namespace
@@ -975,6 +1331,38 @@ hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpar
   const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + (long long)BT * p.D;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, bool bwd,
+                            const LnBuf* ln, hipStream_t s) {
+  const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
+  const int nprep = (int)((total + 255) / 256);
+  const int BT = p.B * p.T;
+  const int nln = ln ? (BT + 3) / 4 : 0;
+  LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
+  hipLaunchKernelGGL(prep_leaf_kernel, dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, p.D,
+                     p.Hp, p.Dp, bwd ? 1 : 0, nprep, lb, p.T, BT);
+  return hipGetLastError();
+}
+
+int ln_bwd_blocks(const Plan& p) { return (p.B * p.T + kLnRows - 1) / kLnRows; }
+
+hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
+                         const float* dxpart, float* gx, float* lnpart, hipStream_t s) {
+  hipLaunchKernelGGL(ln_bwd_kernel, dim3(ln_bwd_blocks(p)), dim3(256), 0, s, lp, ln, dxpart, gx,
+                     lnpart, p.T, p.D, p.Dp, p.B * p.T, p.Hp / 32);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
+                                const float* spart, const float* npart, const float* lnpart,
+                                const LeafGrads& g, hipStream_t s) {
+  FinLeafK a{lp, rpart, spart, npart, lnpart, g, p.B, p.D, p.H, p.Hp, p.Dp, p.NCH, p.NRC,
+             ln_bwd_blocks(p)};
+  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

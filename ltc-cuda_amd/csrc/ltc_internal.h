@@ -18,6 +18,9 @@ constexpr int ode_max_threads(int nb) { return nb <= 2 ? 1024 : (nb <= 4 ? 512 :
 // registers). The launch plan keeps ceil(NB / KS) within it: KS >= 4 when NB >= 4.
 constexpr int ode_owned_rows(int nb) { return nb <= 2 ? nb : nb / 4; }
 
+// Batch tiles whose chain kernel may stage a whole time step in LDS.
+constexpr bool ode_stage_ok(int nb) { return nb <= 4; }
+
 // (NB, RC) pairs whose chain kernel can also keep the four recurrent
 // gradient accumulators of every register-resident operand without spilling
 // at the register budget __launch_bounds__(ode_max_threads(NB)) leaves
@@ -35,6 +38,7 @@ enum KernelId : int {
   K_ODE_BWD,
   K_REC_GRAD,
   K_SENS_BWD,
+  K_LN_BWD,
   K_FINALIZE,
   K_COUNT
 };
@@ -47,6 +51,7 @@ struct Plan {
   int KS;          // split of the reduction axis across waves of one workgroup
   int RC;          // reduction chunk per thread = Hp / KS
   bool FUSE;       // recurrent parameter gradients accumulated inside the chain kernel
+  bool STAGE;      // chain kernel stages each step's saved states in LDS
   int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances
@@ -84,8 +89,51 @@ struct Strides3 {
   long long b, t, c;
 };
 
+// Module-level leaves (reference ltc.py:150-186) for the fused module path:
+// the pre-transforms of ltc.py:259-283 are then computed inside the kernels.
+//   w_pos = softplus(w)*mask, w_erev = w_pos*erev, cm_t = softplus(cm)/dtU,
+//   gleak_pos = softplus(gleak), sensory_w_pos = softplus(s_w)*s_mask,
+//   xa = LayerNorm(x; ln_w, ln_b, ln_eps)*input_w + input_b.
+struct LeafParams {
+  const float* w;
+  const float* erev;
+  const float* mask;
+  const float* mu;
+  const float* sigma;
+  const float* s_w;
+  const float* s_erev;
+  const float* s_mask;
+  const float* s_mu;
+  const float* s_sigma;
+  const float* gleak;
+  const float* vleak;
+  const float* cm;
+  const float* input_w;
+  const float* input_b;
+  const float* ln_w;
+  const float* ln_b;
+  float dtU;     // dt / ode_unfolds, as the fp32 scalar torch divides by
+  float ln_eps;
+};
+
+// LayerNorm + affine of the module path: per (b,t) row, xa written contiguous
+// [B*T][D] and (mean, rstd) in stats [B*T][2].
+struct LnBuf {
+  const float* x;  // raw input, strided
+  Strides3 xs;
+  float* xa;
+  float* stats;
+};
+
+// Largest input width the module path handles (LayerNorm rows in registers).
+constexpr int kModuleMaxD = 1024;
+
 hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
                        hipStream_t s);
+// Module path: images from the leaves; with ln != nullptr the same launch
+// also normalises every (b,t) row of x.
+hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, bool bwd,
+                            const LnBuf* ln, hipStream_t s);
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
@@ -117,5 +165,33 @@ struct GradOut {
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
                            const GradOut& g, hipStream_t s);
+
+// Module path backward.
+struct LeafGrads {
+  float* x;  // (B,T,D) raw-input gradient, contiguous
+  float* w;
+  float* erev;
+  float* mu;
+  float* sigma;
+  float* s_w;
+  float* s_erev;
+  float* s_mu;
+  float* s_sigma;
+  float* gleak;
+  float* vleak;
+  float* cm;
+  float* input_w;
+  float* input_b;
+  float* ln_w;
+  float* ln_b;
+};
+// LayerNorm/affine backward per row, from the h-block partials of dL/dxa;
+// writes dL/dx and per-block column partials lnpart[nblk][4][Dp].
+int ln_bwd_blocks(const Plan& p);
+hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
+                         const float* dxpart, float* gx, float* lnpart, hipStream_t s);
+hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
+                                const float* spart, const float* npart, const float* lnpart,
+                                const LeafGrads& g, hipStream_t s);
 
 }  // namespace ltc

@@ -10,7 +10,11 @@ a seed builds the same tensors), the eval-mode transform cache, the
 `TemporalLTC` alias.
 
 Dispatch. fp32 tensors on a HIP device go to the fused kernels in
-libltc_hip.so through `ltc_cuda.ltc_cuda_forward`. If that library is not
+libltc_hip.so. In training mode the whole layer (LayerNorm, affine, softplus
+transforms and the ODE loop, and their backward) is one library call each way
+(`ltc_cuda.ltc_module_forward`). In eval mode the reference's transform cache
+applies (ltc.py:270-288) and the cached boundary tensors go through
+`ltc_cuda.ltc_cuda_forward`, as in the reference. If the library is not
 loaded, the call raises: on a GPU the fused path is never swapped for another
 one behind the caller's back. CPU tensors, non-fp32 tensors and an explicit
 `module._force_torchscript = True` use the TorchScript loop below, which is
@@ -214,6 +218,23 @@ class TrueLiquidTimeConstant(nn.Module):
         if h0 is not None:
             state = h0[0]
 
+        force_ts = getattr(self, "_force_torchscript", False)
+        on_hip = x_seq.is_cuda and x_seq.dtype == torch.float32 and not force_ts
+        if on_hip and self.training and self._module_path_ok(D):
+            # Whole layer in two library calls: LayerNorm, affine and the
+            # positivity transforms run inside the fused kernels.
+            ltc_cuda.require_kernels()
+            if state.dtype != x_seq.dtype:
+                state = state.to(x_seq.dtype)
+            leaves = [self.w, self.erev, self.sparsity_mask, self.mu, self.sigma,
+                      self.sensory_w, self.sensory_erev, self.sensory_sparsity_mask,
+                      self.sensory_mu, self.sensory_sigma, self.gleak, self.vleak, self.cm,
+                      self.input_w, self.input_b, self.input_norm.weight, self.input_norm.bias]
+            outputs, state = ltc_cuda.ltc_module_forward(
+                x_seq, state, leaves, self.dt, self.ode_unfolds, self.epsilon,
+                self.input_norm.eps)
+            return outputs, (state, state)
+
         x_seq = self.input_norm(x_seq)
         if state.dtype != x_seq.dtype:
             state = state.to(x_seq.dtype)
@@ -231,8 +252,7 @@ class TrueLiquidTimeConstant(nn.Module):
                     "gleak_pos": gleak_pos, "sensory_w_pos": sensory_w_pos,
                 }
 
-        force_ts = getattr(self, "_force_torchscript", False)
-        if x_seq.is_cuda and x_seq.dtype == torch.float32 and not force_ts:
+        if on_hip:
             ltc_cuda.require_kernels()
             outputs, state = ltc_cuda.ltc_cuda_forward(
                 x_seq, state, w_pos, w_erev, self.mu, self.sigma,
@@ -249,6 +269,14 @@ class TrueLiquidTimeConstant(nn.Module):
                 self.sensory_mu, self.sensory_sigma, self.sensory_erev, sensory_w_pos,
                 cm_t, gleak_pos, self.vleak, self.ode_unfolds, self.epsilon)
         return outputs, (state, state)
+
+    def _module_path_ok(self, D: int) -> bool:
+        """Whether the fused module path applies: standard LayerNorm, fp32 leaves, D in range."""
+        norm = self.input_norm
+        return (D <= ltc_cuda.MODULE_MAX_D and isinstance(norm, nn.LayerNorm)
+                and norm.weight is not None and norm.bias is not None
+                and tuple(norm.normalized_shape) == (D,)
+                and self.w.dtype == torch.float32 and self.w.is_cuda)
 
     def train(self, mode: bool = True):
         """Switching to train mode drops the eval-mode transform cache (ltc.py:328-332)."""

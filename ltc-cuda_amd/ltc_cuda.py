@@ -51,11 +51,13 @@ class CApi:
     SYMBOLS = (
         "ltc_abi_version", "ltc_last_error", "ltc_device_count", "ltc_saved_floats",
         "ltc_fwd_workspace_bytes", "ltc_bwd_workspace_bytes", "ltc_full_forward",
-        "ltc_full_backward", "ltc_launch_plan", "ltc_timing_enable", "ltc_timing_read",
-        "ltc_kernel_count", "ltc_kernel_name",
+        "ltc_full_backward", "ltc_module_saved_floats", "ltc_module_fwd_workspace_bytes",
+        "ltc_module_bwd_workspace_bytes", "ltc_module_forward", "ltc_module_backward",
+        "ltc_launch_plan", "ltc_timing_enable", "ltc_timing_read", "ltc_kernel_count",
+        "ltc_kernel_name",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
-                   "NRC", "ode_workgroups", "fuse")
+                   "NRC", "ode_workgroups", "fuse", "stage")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path
@@ -84,6 +86,22 @@ class CApi:
             + [_f32p, _i64, _i64, _i64, _f32p]
             + [_int, _int, _int, _int, _int, _flt]
             + [_f32p] * 13 + [_f32p, _i64, ctypes.c_void_p])
+        for name in ("ltc_module_saved_floats", "ltc_module_fwd_workspace_bytes",
+                     "ltc_module_bwd_workspace_bytes"):
+            fn = getattr(lib, name)
+            fn.restype = _i64
+            fn.argtypes = [_int, _int, _int, _int, _int]
+        lib.ltc_module_forward.restype = _int
+        lib.ltc_module_forward.argtypes = (
+            [_f32p, _i64, _i64, _i64, _f32p] + [_f32p] * 17
+            + [_int, _int, _int, _int, _int, _flt, _flt, _flt, _int]
+            + [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.c_void_p])
+        lib.ltc_module_backward.restype = _int
+        lib.ltc_module_backward.argtypes = (
+            [_f32p, _i64, _i64, _i64] + [_f32p] * 17 + [_f32p]
+            + [_f32p, _i64, _i64, _i64, _f32p]
+            + [_int, _int, _int, _int, _int, _flt, _flt, _flt]
+            + [_f32p] * 17 + [_f32p, _i64, ctypes.c_void_p])
         lib.ltc_launch_plan.restype = _int
         lib.ltc_launch_plan.argtypes = [_int, _int, _int, _int, _int,
                                         ctypes.POINTER(ctypes.c_longlong), _int]
@@ -250,6 +268,127 @@ class _HipModule:
                 *[_ptr(g) for g in grads], _aligned(ws), int(need), _stream_handle(dev))
         self.capi.check(rc, "ltc_full_backward")
         return grads
+
+
+MODULE_MAX_D = 1024  # kModuleMaxD in csrc/ltc_internal.h
+
+# Leaf order of the module path (ltc_module_forward argument order).
+MODULE_LEAVES = ("w", "erev", "sparsity_mask", "mu", "sigma", "sensory_w", "sensory_erev",
+                 "sensory_sparsity_mask", "sensory_mu", "sensory_sigma", "gleak", "vleak", "cm",
+                 "input_w", "input_b", "input_norm.weight", "input_norm.bias")
+# Leaves that get a gradient, in ltc_module_backward output order (after x, state).
+MODULE_GRADS = ("w", "erev", "mu", "sigma", "sensory_w", "sensory_erev", "sensory_mu",
+                "sensory_sigma", "gleak", "vleak", "cm", "input_w", "input_b",
+                "input_norm.weight", "input_norm.bias")
+
+
+def _module_forward(capi, x, state, leaves, dt, U, eps, ln_eps, save):
+    B, T, D = x.shape
+    H = state.shape[1]
+    dev = x.device
+    lib = capi.lib
+    leaves = [t.contiguous() for t in leaves]
+    state_c = state.contiguous()
+    out = torch.empty(B, T, H, device=dev, dtype=torch.float32)
+    h = torch.empty(B, H, device=dev, dtype=torch.float32)
+    saved = None
+    if save:
+        n = lib.ltc_module_saved_floats(B, T, D, H, U)
+        if n < 0:
+            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        saved = torch.empty(max(int(n), 1), device=dev, dtype=torch.float32)
+    need = lib.ltc_module_fwd_workspace_bytes(B, T, D, H, U)
+    if need < 0:
+        raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+    with torch.cuda.device(dev):
+        ws = _workspace(need, dev)
+        sx = x.stride()
+        rc = lib.ltc_module_forward(
+            _ptr(x), sx[0], sx[1], sx[2], _ptr(state_c), *[_ptr(t) for t in leaves],
+            B, T, D, H, U, float(dt), float(eps), float(ln_eps), 1 if save else 0,
+            _ptr(out), _ptr(h), _ptr(saved), _aligned(ws), int(need), _stream_handle(dev))
+    capi.check(rc, "ltc_module_forward")
+    return out, h, saved
+
+
+def _module_backward(capi, x, state, leaves, saved, grad_out, grad_h, dt, U, eps, ln_eps):
+    B, T, D = x.shape
+    H = state.shape[1]
+    dev = x.device
+    lib = capi.lib
+    leaves = [t.contiguous() for t in leaves]
+    go = grad_out
+    if go.dtype != torch.float32 or go.device != dev:
+        go = go.to(device=dev, dtype=torch.float32)
+    ghf = None if grad_h is None else grad_h.to(device=dev, dtype=torch.float32).contiguous()
+    f32 = dict(device=dev, dtype=torch.float32)
+    grads = [torch.empty(B, T, D, **f32), torch.empty(B, H, **f32)]
+    grads += [torch.empty(H, H, **f32) for _ in range(4)]
+    grads += [torch.empty(D, H, **f32) for _ in range(4)]
+    grads += [torch.empty(H, **f32) for _ in range(3)]
+    grads += [torch.empty(D, **f32) for _ in range(4)]
+    need = lib.ltc_module_bwd_workspace_bytes(B, T, D, H, U)
+    if need < 0:
+        raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+    with torch.cuda.device(dev):
+        ws = _workspace(need, dev)
+        sx = x.stride()
+        sg = go.stride()
+        rc = lib.ltc_module_backward(
+            _ptr(x), sx[0], sx[1], sx[2], *[_ptr(t) for t in leaves], _ptr(saved),
+            _ptr(go), sg[0], sg[1], sg[2], _ptr(ghf), B, T, D, H, U, float(dt), float(eps),
+            float(ln_eps), *[_ptr(g) for g in grads], _aligned(ws), int(need),
+            _stream_handle(dev))
+    capi.check(rc, "ltc_module_backward")
+    return grads
+
+
+class LTCModuleFunction(torch.autograd.Function):
+    """The whole layer forward/backward in two library calls.
+
+    Inputs: x (B,T,D) raw (before LayerNorm), state (B,H), then the module's
+    leaves in MODULE_LEAVES order (masks are buffers and get no gradient),
+    then dt, ode_unfolds, epsilon, ln_eps, needs_grad. The pre-transforms of
+    the reference module (ltc.py:259-283) run inside the library, so their
+    ~25 PyTorch launches and autograd nodes are gone.
+    """
+
+    @staticmethod
+    def forward(ctx, x, state, *rest):
+        leaves = rest[:17]
+        dt, U, eps, ln_eps, needs_grad = rest[17:]
+        capi = require_kernels().capi
+        out, h, saved = _module_forward(capi, x, state, leaves, dt, U, eps, ln_eps, needs_grad)
+        if needs_grad:
+            ctx.save_for_backward(x, state, *leaves, saved)
+        ctx.cfg = (dt, U, eps, ln_eps)
+        return out, h
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_h):
+        saved_t = ctx.saved_tensors
+        if not saved_t:
+            raise RuntimeError("LTCModuleFunction.backward called on a forward run without grad")
+        x, state = saved_t[0], saved_t[1]
+        leaves, buf = saved_t[2:19], saved_t[19]
+        dt, U, eps, ln_eps = ctx.cfg
+        if grad_out is None:
+            grad_out = torch.zeros(x.shape[0], x.shape[1], state.shape[1], device=x.device)
+        g = _module_backward(require_kernels().capi, x, state, leaves, buf, grad_out, grad_h,
+                             dt, U, eps, ln_eps)
+        gx, gstate = g[0], g[1]
+        (gw, gerev, gmu, gsig, gsw, gserev, gsmu, gssig, ggl, gvl, gcm, giw, gib, glw,
+         glb) = g[2:]
+        leaf_grads = (gw, gerev, None, gmu, gsig, gsw, gserev, None, gsmu, gssig, ggl, gvl,
+                      gcm, giw, gib, glw, glb)
+        return (gx, gstate, *leaf_grads, None, None, None, None, None)
+
+
+def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
+    """Whole-layer fused call; `leaves` in MODULE_LEAVES order."""
+    needs_grad = torch.is_grad_enabled()
+    return LTCModuleFunction.apply(x_seq, state, *leaves, float(dt), int(ode_unfolds),
+                                   float(epsilon), float(ln_eps), needs_grad)
 
 
 def load_capi(path: str = LIB_PATH) -> CApi:

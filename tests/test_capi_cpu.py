@@ -142,6 +142,8 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     owned = p["NB"] if p["NB"] <= 2 else p["NB"] // 4
     assert -(-p["NB"] // p["KS"]) <= owned
     assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
+    if p["stage"]:
+        assert p["NB"] <= 4 and (2 * U + 1) * p["NB"] * p["Hp"] <= 8 * p["threads"]
     assert 1 <= p["NRC"] <= 64
     if p["fuse"]:
         # one partial per chain workgroup; operands and accumulators in registers

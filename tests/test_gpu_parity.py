@@ -319,3 +319,119 @@ def test_full_size_forward_rows_and_backward_linearity(cfg):
     got = gpu_backward(ds, sv, go2, None)
     ref = oracle_grads(sub, go2.cpu(), None)
     assert_grads_close(got, ref, f"{cfg} two-row backward")
+
+
+# --------------------------------------------------------------------------- module path
+
+def _perturbed_module(D, H, seed, mapping="affine", sparsity=0.5):
+    """Module with every leaf away from its default, including softplus's x > 20 branch."""
+    torch.manual_seed(seed)
+    m = ltc.TrueLiquidTimeConstant(D, H, sparsity=sparsity, sensory_sparsity=sparsity,
+                                   input_mapping=mapping)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        m.input_norm.weight.add_(0.2 * torch.randn(D, generator=g))
+        m.input_norm.bias.add_(0.1 * torch.randn(D, generator=g))
+        m.input_w.add_(0.2 * torch.randn(D, generator=g))
+        m.input_b.add_(0.1 * torch.randn(D, generator=g))
+        m.w.view(-1)[:3] = 25.0
+        m.sensory_w.view(-1)[:2] = 22.0
+        m.cm.view(-1)[:1] = 21.0
+    return m
+
+
+def _oracle_module_grads(m, x, h0, G, Gh):
+    p = {k: v.detach().cpu().double().clone() for k, v in m.state_dict().items()}
+    names = dict(m.named_parameters())
+    leaves = {k: v.requires_grad_(k in names) for k, v in p.items()}
+    xd = x.detach().cpu().double().clone().requires_grad_(True)
+    hd = h0.detach().cpu().double().clone().requires_grad_(True)
+    out, (h, _) = O.module_forward(leaves, xd, (hd, hd), dt=m.dt, ode_unfolds=m.ode_unfolds,
+                                   epsilon=m.epsilon)
+    ((out * G.double()).sum() + (h * Gh.double()).sum()).backward()
+    return out.detach(), h.detach(), {k: leaves[k].grad for k in names}, xd.grad, hd.grad
+
+
+MODULE_SHAPES = [(4, 8, 32, 16), (2, 4, 32, 33), (24, 8, 128, 64), (3, 2, 100, 65),
+                 (2, 3, 1024, 8), (2, 2, 1100, 8), (6, 3, 48, 130)]
+
+
+@pytest.mark.parametrize("shape", MODULE_SHAPES, ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_module_path_matches_oracle(shape):
+    """Training-mode layer (fused module path when D <= 1024) vs the float64 oracle."""
+    B, T, D, H = shape
+    m = _perturbed_module(D, H, seed=B + D + H).to(DEV)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, T, D, generator=g) * 2.0
+    h0 = torch.randn(B, H, generator=g) * 0.2
+    G = torch.randn(B, T, H, generator=g)
+    Gh = torch.randn(B, H, generator=g)
+    xg = x.to(DEV).requires_grad_(True)
+    hg = h0.to(DEV).requires_grad_(True)
+    out, (h, _) = m(xg, (hg, hg))
+    ((out * G.to(DEV)).sum() + (h * Gh.to(DEV)).sum()).backward()
+    r_out, r_h, r_g, r_gx, r_gh = _oracle_module_grads(m, x, h0, G, Gh)
+    assert (out.detach().cpu().double() - r_out).abs().max().item() <= 1e-3
+    assert (h.detach().cpu().double() - r_h).abs().max().item() <= 1e-3
+    got = [xg.grad.cpu(), hg.grad.cpu()] + [p.grad.cpu() for _, p in m.named_parameters()]
+    ref = [r_gx, r_gh] + [r_g[n] for n, _ in m.named_parameters()]
+    names = ["x", "h0"] + [n for n, _ in m.named_parameters()]
+    for name, a, r in zip(names, got, ref):
+        err = (a.double() - r).abs().max().item()
+        scale = r.abs().max().item()
+        assert torch.isfinite(a).all(), name
+        assert torch.allclose(a.double(), r, rtol=5e-2, atol=1e-2), f"{shape} {name}: {err:.2e}"
+        assert err <= 2e-3 * scale + 1e-6, f"{shape} {name}: err {err:.2e} scale {scale:.2e}"
+
+
+@pytest.mark.parametrize("mapping", ["linear", "none"])
+def test_module_path_input_mappings(mapping):
+    B, T, D, H = 3, 4, 20, 12
+    m = _perturbed_module(D, H, seed=21, mapping=mapping).to(DEV)
+    x = torch.randn(B, T, D)
+    h0 = torch.zeros(B, H)
+    G, Gh = torch.randn(B, T, H), torch.zeros(B, H)
+    out, (h, _) = m(x.to(DEV), (h0.to(DEV), h0.to(DEV)))
+    (out * G.to(DEV)).sum().backward()
+    r_out, _, r_g, _, _ = _oracle_module_grads(m, x, h0, G, Gh)
+    assert (out.detach().cpu().double() - r_out).abs().max().item() <= 1e-3
+    for n, p in m.named_parameters():
+        err = (p.grad.cpu().double() - r_g[n]).abs().max().item()
+        assert err <= 2e-3 * r_g[n].abs().max().item() + 1e-6, f"{mapping} {n}: {err:.2e}"
+
+
+def test_module_path_strided_input_and_determinism():
+    B, T, D, H = 32, 4, 64, 64
+    m = _perturbed_module(D, H, seed=5).to(DEV)
+    wide = torch.randn(B, T, 2 * D, device=DEV)
+    xv = wide[:, :, 0::2]
+    xc = xv.contiguous()
+    res = []
+    for x in (xv, xc, xv):
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        out.sum().backward()
+        res.append([out.detach().clone()] + [p.grad.clone() for p in m.parameters()])
+    for other in res[1:]:
+        for a, b in zip(res[0], other):
+            assert torch.equal(a, b)
+    with torch.no_grad():
+        out_ng, _ = m(xv)
+    assert torch.equal(out_ng, res[0][0])
+
+
+def test_eval_mode_uses_cached_transforms_like_the_reference():
+    """Eval mode keeps the reference's cache semantics: stale after an in-place edit."""
+    torch.manual_seed(42)
+    m = ltc.TrueLiquidTimeConstant(32, 16).to(DEV).eval()
+    x = torch.randn(4, 8, 32, device=DEV)
+    with torch.no_grad():
+        a, _ = m(x)
+        m.w.add_(1.0)              # not seen until train() drops the cache (ltc.py:328-332)
+        b, _ = m(x)
+        m.train()
+        c, _ = m(x)
+    assert torch.equal(a, b) and not torch.allclose(a, c)
+    p = {k: v.detach().cpu() for k, v in m.state_dict().items()}
+    r, _ = O.module_forward(p, x.cpu())
+    assert (c.cpu() - r).abs().max().item() <= 1e-3
