@@ -134,6 +134,37 @@ def time_split(m, x, target, iters):
     return statistics.median(fwd), statistics.median(tot), statistics.median(inf)
 
 
+class _GraphStep(torch.nn.Module):
+    """Layer forward returning plain tensors, for torch.cuda.make_graphed_callables."""
+
+    def __init__(self, inner):
+        super().__init__()
+        self.inner = inner
+
+    def forward(self, x):
+        out, (h, _) = self.inner(x)
+        return out, h
+
+
+def graphed_step_ms(m, x, target, steps, warmup):
+    """Same step with the layer's fwd and bwd captured into HIP graphs (replayed)."""
+    g = torch.cuda.make_graphed_callables(_GraphStep(m), (x,))
+
+    def one():
+        out, _ = g(x)
+        loss_of(out, target).backward()
+        m.zero_grad(set_to_none=True)
+
+    for _ in range(warmup):
+        one()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
 def kernel_times(capi, fn, iters):
     """Mean per-launch duration of each library kernel over `iters` calls of fn."""
     capi.timing_enable(True)
@@ -324,6 +355,7 @@ def main():
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
     fwd_ms, tot_ms, inf_ms = time_split(m, x, target, max(10, args.steps // 2))
+    graphed_ms = graphed_step_ms(m, x, target, args.steps, args.warmup)
     kt = kernel_times(capi, lambda: step(m, x, target), max(10, args.steps // 2))
     ksum = sum(v[0] * v[1] for v in kt.values())
     line = {
@@ -347,6 +379,8 @@ def main():
         "bwd_ms": round(tot_ms - fwd_ms, 5),
         "fwd_bwd_event_ms": round(tot_ms, 5),
         "fwd_only_nograd_ms": round(inf_ms, 5),
+        "graphed_ms_per_step": round(graphed_ms, 5),
+        "graphed_synapse_updates_per_s": n_syn(c) / (graphed_ms * 1e-3),
         "kernels_ms": {k: round(v[0], 5) for k, v in kt.items()},
         "kernel_ms_sum": round(ksum, 5),
         "issue_frac_step": round(issue_fraction(c, ms, "fwdbwd"), 5),

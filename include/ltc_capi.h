@@ -187,11 +187,11 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
  * workgroup, forward LDS bytes, backward LDS bytes, NCH (recurrent gradient
  * chunks, or one per workgroup when fused), NRC (sensory backward row
  * chunks), ODE workgroups, 1 when the recurrent parameter gradients are
- * accumulated inside the chain kernel, and 1 when the chain kernel stages
- * each time step's saved states in LDS. Returns the number of values
- * written, or -1 for invalid sizes.
+ * accumulated inside the chain kernel, then the chain kernel's own KS, RC
+ * and threads (the fields before them describe the forward kernel). Returns
+ * the number of values written, or -1 for invalid sizes.
  */
-#define LTC_PLAN_FIELDS 13
+#define LTC_PLAN_FIELDS 15
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

@@ -46,45 +46,53 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
   // Split of the reduction axis: as many waves as the thread bound allows,
   // with LDS partials under 64 KiB and at least 4 synapses per thread. When
   // even KS = 1 does not fit, fewer rows per workgroup.
-  auto lds_ok = [&](int nb, int k) {
-    const long long f = (long long)nb * p.Hp * 4 + (long long)k * nb * p.Hp * 8;
-    const long long b = (long long)nb * p.Hp * 8 + (long long)k * nb * p.Hp * 4;
-    return f <= 65536 && b <= 65536;
+  auto lds_fwd = [&](int nb, int k) {
+    return (long long)nb * p.Hp * 4 + (long long)k * nb * p.Hp * 8;
   };
-  for (;;) {
-    // KS is a power of two <= 16, so it always divides Hp/4 (Hp is a multiple
-    // of 64). With NB >= 4 rows, KS >= 4 keeps the rows each thread finishes
-    // within ode_owned_rows(NB).
-    const int cap = ltc::ode_max_threads(p.NB) / p.Hp;
-    const int ks_min = p.NB >= 4 ? 4 : 1;
+  auto lds_bwd = [&](int nb, int k) {
+    return (long long)nb * p.Hp * 8 + (long long)k * nb * p.Hp * 4;
+  };
+  // KS is a power of two <= 16, so it always divides Hp/4 (Hp is a multiple
+  // of 64). With NB >= 4 rows, KS >= 4 keeps the rows each thread finishes
+  // within ode_owned_rows(NB). When no split fits, fewer rows per workgroup.
+  auto pick_ks = [&](int nb, int want, bool bwd) {
+    const int cap = ltc::ode_max_threads(nb) / p.Hp;
+    const int ks_min = nb >= 4 ? 4 : 1;
     int ks = 0;
     for (int k = 16; k >= 1; k >>= 1) {
-      if (k <= cap) {
+      if (k <= cap && k <= want) {
         ks = k;
         break;
       }
     }
-    while (ks > ks_min && (!lds_ok(p.NB, ks) || p.Hp / ks < 4)) ks >>= 1;
-    if ((ks >= ks_min && lds_ok(p.NB, ks) && p.Hp / ks >= 4) || p.NB == 1) {
-      p.KS = ks < 1 ? 1 : ks;
+    auto fits = [&](int k) {
+      return k >= ks_min && p.Hp / k >= 4 &&
+             (bwd ? lds_bwd(nb, k) : lds_fwd(nb, k)) <= 65536;
+    };
+    while (ks > ks_min && !fits(ks)) ks >>= 1;
+    return fits(ks) ? ks : 0;
+  };
+  // Per-unfold latency is lowest with one wave per SIMD for the forward at
+  // small H (fewer partials, same VALU work per CU); the chain kernel keeps
+  // the widest split, whose register-resident operands carry the fused
+  // gradient accumulators.
+  const int want_f = p.Hp <= 64 ? 4 : 16;
+  for (;;) {
+    const int kf = pick_ks(p.NB, want_f, false), kb = pick_ks(p.NB, 16, true);
+    if ((kf > 0 && kb > 0) || p.NB == 1) {
+      p.KS = kf > 0 ? kf : 1;
+      p.KSB = kb > 0 ? kb : 1;
       break;
     }
     p.NB >>= 1;
   }
   p.RC = p.Hp / p.KS;
+  p.RCB = p.Hp / p.KSB;
   p.N = (long long)T * U * B;
   // When each thread's synapse operands fit in registers (RC in {4, 8, 16}),
   // the chain kernel also accumulates the recurrent parameter gradients and
   // writes one partial per workgroup.
-  p.FUSE = ltc::ode_fuse_ok(p.NB, p.RC);
-  // Step staging for the chain kernel: two step buffers of (2U+1)*NB*Hp
-  // floats next to its other LDS arrays, at most 8 staged floats per thread.
-  {
-    const long long slots = (2LL * U + 1) * p.NB * p.Hp;
-    const long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4;
-    p.STAGE = ltc::ode_stage_ok(p.NB) && base + 2 * slots * 4 <= 65536 &&
-              slots <= 8LL * p.Hp * p.KS;
-  }
+  p.FUSE = ltc::ode_fuse_ok(p.NB, p.RCB);
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
   if (p.FUSE) {
@@ -697,9 +705,9 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, (long long)p.Hp * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8,
-      (long long)p.NB * p.Hp * 8 + (long long)p.KS * p.NB * p.Hp * 4 +
-          (p.STAGE ? 2 * (2LL * ode_unfolds + 1) * p.NB * p.Hp * 4 : 0),
-      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0, p.STAGE ? 1 : 0};
+      (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4,
+      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0, p.KSB, p.RCB,
+      (long long)p.Hp * p.KSB};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

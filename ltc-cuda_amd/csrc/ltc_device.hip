@@ -50,6 +50,31 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Sum of the K partials base[0], base[stride], ..., base[(K-1)*stride]: all K
+// LDS reads are issued before the first add, then a fixed pairwise tree.
+template <int K, class V>
+__device__ __forceinline__ V tree_sum(const V* base, int stride) {
+  V v[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) v[s] = base[s * stride];
+#pragma unroll
+  for (int w = 1; w < K; w *= 2) {
+#pragma unroll
+    for (int s = 0; s + w < K; s += 2 * w) v[s] += v[s + w];
+  }
+  return v[0];
+}
+
+// KS (a power of two <= 16) is a runtime value: groups of four reads are in
+// flight together and summed pairwise, groups are added in order.
+template <class V>
+__device__ __forceinline__ V ks_sum(const V* base, int stride, int KS) {
+  if (KS < 4) return KS == 2 ? base[0] + base[stride] : base[0];
+  V acc = tree_sum<4>(base, stride);
+  for (int g = 4; g < KS; g += 4) acc += tree_sum<4>(base + g * stride, stride);
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // Parameter images (one launch, flat index space over three segments).
 // ---------------------------------------------------------------------------
@@ -265,9 +290,28 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
 #pragma unroll
         for (int rr = 0; rr < RCP; ++rr) fwd_synapse<NB>(preg[rr], vs, Hp, r0 + rr, na, qa);
       } else {
+        // Operands stream from L2: the next four are requested while the
+        // current four are evaluated (RC is a multiple of 8 here).
         const float4* pc = k.recF + (long long)r0 * Hp + o;
-#pragma unroll 4
-        for (int rr = 0; rr < RC; ++rr) fwd_synapse<NB>(pc[(long long)rr * Hp], vs, Hp, r0 + rr, na, qa);
+        float4 pa[4], pb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp];
+        for (int rr = 0; rr < RC; rr += 8) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pb[q] = pc[(long long)(rr + 4 + q) * Hp];
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pa[q], vs, Hp, r0 + rr + q, na, qa);
+          __builtin_amdgcn_sched_barrier(0);
+          if (rr + 8 < RC) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)(rr + 8 + q) * Hp];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pb[q], vs, Hp, r0 + rr + 4 + q, na, qa);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
@@ -276,12 +320,8 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
-          float n = 0.f, q = 0.f;
-          for (int s = 0; s < KS; ++s) {
-            const float2 rv = red[(s * NB + b) * Hp + o];
-            n += rv.x;
-            q += rv.y;
-          }
+          const float2 nq = ks_sum(red + b * Hp + o, NB * Hp, KS);
+          const float n = nq.x, q = nq.y;
           const float vold = vs[b * Hp + o];
           const float den = CG + (q + sdr[m]) + k.eps;
           const float num = C * vold + GL + (n + snr[m]);
@@ -340,10 +380,6 @@ struct BwdK {
   float* rpart;     // per-workgroup recurrent partials [grid][4][Hp][Hp] (fused only)
   int B, T, H, Hp, U, KS, RC;
 };
-
-constexpr int kStageRegs = 8;  // staged floats per thread and step (plan keeps (2U+1)*NB*Hp within)
-
-__device__ __forceinline__ int b0_of(const BwdK&, int nb) { return blockIdx.x * nb; }
 
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
 // FUSE the parameter-gradient sums of this synapse ride along in gacc:
@@ -404,12 +440,7 @@ __device__ __forceinline__ void bwd_load_gout(const BwdK& k, int t, int b0, int 
 // FUSE (register-resident operands only): each operand also carries its
 // gradient accumulators, which removes the separate parameter-gradient pass
 // and its second gate evaluation.
-// STAGE: the saved states and denominators of a whole time step (all U
-// unfolds, the tile's NB rows) are copied into an LDS double buffer one step
-// ahead: the loads are issued at the start of a step and written to LDS at
-// its end, so every unfold reads its operands from LDS and pays no global
-// load latency. Used when two step buffers fit next to the other LDS arrays.
-template <int NB, int RCP, bool FUSE, bool STAGE>
+template <int NB, int RCP, bool FUSE>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   static_assert(!FUSE || RCP > 0, "fused gradients need register-resident operands");
   constexpr int MO = ode_owned_rows(NB);
@@ -418,36 +449,6 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   const int RC = RCP > 0 ? RCP : k.RC;
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][Hp]
-  float* stg = red + KS * NB * Hp;                      // [2][2U+1][NB][Hp] when STAGE
-  const int SL = (2 * U + 1) * NB * Hp;                 // floats per step buffer
-  const int NBHp = NB * Hp;
-  float sreg[STAGE ? kStageRegs : 1];
-  // Step t's slots: v^0..v^U (U+1 slots) then den^0..den^{U-1}; rows past B
-  // read as v = 0, den = 1.
-  auto stage_issue = [&](int t) {
-#pragma unroll
-    for (int q = 0; q < kStageRegs; ++q) {
-      const int e = threadIdx.x + q * blockDim.x;
-      float v = 0.f;
-      if (e < SL) {
-        const int slot = e / NBHp, w = e - slot * NBHp;
-        if (b0_of(k, NB) + w / Hp < B) {
-          v = slot <= U ? k.vsave[(((long long)t * U + slot) * B + b0_of(k, NB)) * Hp + w]
-                        : k.densave[(((long long)t * U + slot - U - 1) * B + b0_of(k, NB)) * Hp + w];
-        } else if (slot > U) {
-          v = 1.f;
-        }
-      }
-      sreg[q] = v;
-    }
-  };
-  auto stage_commit = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < kStageRegs; ++q) {
-      const int e = threadIdx.x + q * blockDim.x;
-      if (e < SL) stg[buf * SL + e] = sreg[q];
-    }
-  };
   const int tid = threadIdx.x;
   const int ks = tid / Hp, o = tid - ks * Hp;
   const int b0 = blockIdx.x * NB;
@@ -475,28 +476,17 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   }
   if (T == 0) return;
 
-  // Operands of the current unfold; without STAGE they are software-pipelined
-  // one unfold ahead from global memory, with STAGE they come from LDS.
+  // Operands of the current unfold, software-pipelined one unfold ahead.
   float cvi[NB], cden[MO], cvk[MO], cvk1[MO];
   float nvi[NB], nden[MO], nvk[MO], nvk1[MO];
   float gcur[MO], gnext[MO];
 #pragma unroll
   for (int m = 0; m < MO; ++m) gnext[m] = 0.f;
-  int cur = 0;
-  if constexpr (STAGE) {
-    stage_issue(T - 1);
-    stage_commit(0);
-    lds_barrier();
-  } else {
-    bwd_load_unfold<NB, MO>(k, (long long)T * U - 1, b0, ks, o, cvi, cden, cvk, cvk1);
-  }
+  bwd_load_unfold<NB, MO>(k, (long long)T * U - 1, b0, ks, o, cvi, cden, cvk, cvk1);
   bwd_load_gout<NB, MO>(k, T - 1, b0, ks, o, gcur);
 
   for (int t = T - 1; t >= 0; --t) {
-    if (t > 0) {
-      bwd_load_gout<NB, MO>(k, t - 1, b0, ks, o, gnext);
-      if constexpr (STAGE) stage_issue(t - 1);
-    }
+    if (t > 0) bwd_load_gout<NB, MO>(k, t - 1, b0, ks, o, gnext);
     float accA[MO], accB[MO];
 #pragma unroll
     for (int m = 0; m < MO; ++m) {
@@ -505,22 +495,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
     }
     for (int u = U - 1; u >= 0; --u) {
       const long long n = (long long)t * U + u;
-      if constexpr (STAGE) {
-        const float* sb = stg + cur * SL;
-#pragma unroll
-        for (int b = 0; b < NB; ++b) cvi[b] = sb[(u * NB + b) * Hp + o];
-#pragma unroll
-        for (int m = 0; m < MO; ++m) {
-          const int b = ks + m * KS;
-          if (b < NB) {
-            cvk[m] = sb[(u * NB + b) * Hp + o];
-            cvk1[m] = sb[((u + 1) * NB + b) * Hp + o];
-            cden[m] = sb[((U + 1 + u) * NB + b) * Hp + o];
-          }
-        }
-      } else {
-        if (n > 0) bwd_load_unfold<NB, MO>(k, n - 1, b0, ks, o, nvi, nden, nvk, nvk1);
-      }
+      if (n > 0) bwd_load_unfold<NB, MO>(k, n - 1, b0, ks, o, nvi, nden, nvk, nvk1);
       float gdir[MO];
 #pragma unroll
       for (int m = 0; m < MO; ++m) {
@@ -558,11 +533,30 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
         for (int rr = 0; rr < RCP; ++rr)
           bwd_synapse<NB, false>(preg[rr], ab, Hp, r0 + rr, cvi, acc, unused);
       } else {
+        // Streamed operands, double-buffered four at a time (RC % 8 == 0).
         float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
         const float4* pc = k.recB + (long long)r0 * Hp + o;
-#pragma unroll 4
-        for (int rr = 0; rr < RC; ++rr)
-          bwd_synapse<NB, false>(pc[(long long)rr * Hp], ab, Hp, r0 + rr, cvi, acc, unused);
+        float4 pa[4], pb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp];
+        for (int rr = 0; rr < RC; rr += 8) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pb[q] = pc[(long long)(rr + 4 + q) * Hp];
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bwd_synapse<NB, false>(pa[q], ab, Hp, r0 + rr + q, cvi, acc, unused);
+          __builtin_amdgcn_sched_barrier(0);
+          if (rr + 8 < RC) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)(rr + 8 + q) * Hp];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bwd_synapse<NB, false>(pb[q], ab, Hp, r0 + rr + 4 + q, cvi, acc, unused);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = acc[b];
@@ -571,29 +565,19 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
       for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
-          float s = 0.f;
-          for (int q = 0; q < KS; ++q) s += red[(q * NB + b) * Hp + o];
+          const float s = ks_sum(red + b * Hp + o, NB * Hp, KS);
           g[m] = o < H ? fmaf(kNegLn2, s, gdir[m]) : 0.f;
         }
       }
-      if constexpr (!STAGE) {
-        if (n > 0) {
+      if (n > 0) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) cvi[b] = nvi[b];
+        for (int b = 0; b < NB; ++b) cvi[b] = nvi[b];
 #pragma unroll
-          for (int m = 0; m < MO; ++m) {
-            cden[m] = nden[m];
-            cvk[m] = nvk[m];
-            cvk1[m] = nvk1[m];
-          }
+        for (int m = 0; m < MO; ++m) {
+          cden[m] = nden[m];
+          cvk[m] = nvk[m];
+          cvk1[m] = nvk1[m];
         }
-      }
-    }
-    if constexpr (STAGE) {
-      if (t > 0) {
-        stage_commit(cur ^ 1);
-        lds_barrier();
-        cur ^= 1;
       }
     }
 #pragma unroll
@@ -1179,8 +1163,7 @@ size_t fwd_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * p.Hp * 8;
 }
 size_t bwd_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KS * p.NB * p.Hp * 4 +
-         (p.STAGE ? (size_t)2 * (2 * p.U + 1) * p.NB * p.Hp * 4 : 0);
+  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KSB * p.NB * p.Hp * 4;
 }
 
 template <int NB>
@@ -1197,12 +1180,12 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int NB, bool STAGE>
-hipError_t bwd_by_rcp_stage(const Plan& p, const BwdK& a, hipStream_t s) {
-  const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
+template <int NB>
+hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
+  const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KSB);
   const size_t lds = bwd_lds_bytes(p);
-  const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
-#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F, STAGE>), grid, block, lds, s, a)
+  const int rcp = (p.RCB == 4 || p.RCB == 8 || p.RCB == 16) ? p.RCB : 0;
+#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
   if (p.FUSE) {
     // Only the spill-free pairs of ode_fuse_ok() are instantiated.
     if constexpr (ode_fuse_ok(NB, 8)) {
@@ -1221,14 +1204,6 @@ hipError_t bwd_by_rcp_stage(const Plan& p, const BwdK& a, hipStream_t s) {
   }
 #undef LTC_BWD
   return hipGetLastError();
-}
-
-template <int NB>
-hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
-  if constexpr (ode_stage_ok(NB)) {
-    if (p.STAGE) return bwd_by_rcp_stage<NB, true>(p, a, s);
-  }
-  return bwd_by_rcp_stage<NB, false>(p, a, s);
 }
 
 }  // namespace
@@ -1294,7 +1269,7 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           const float* ghfin, float2* absave, float* dsn, float* dsd,
                           float* npart, float* gstate, float* rpart, hipStream_t s) {
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
-         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC};
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB};
   switch (p.NB) {
     case 16: return bwd_by_rcp<16>(p, a, s);
     case 8: return bwd_by_rcp<8>(p, a, s);

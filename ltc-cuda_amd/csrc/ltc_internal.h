@@ -12,14 +12,11 @@ namespace ltc {
 // Threads per workgroup of the persistent ODE kernels for NB batch rows per
 // workgroup. More rows per thread means more live registers, so fewer
 // threads; the same bound is the kernels' __launch_bounds__.
-constexpr int ode_max_threads(int nb) { return nb <= 2 ? 1024 : (nb <= 4 ? 512 : 256); }
+constexpr int ode_max_threads(int nb) { return nb <= 1 ? 1024 : (nb <= 4 ? 512 : 256); }
 
 // Rows each thread finishes per unfold (the compile-time size of its per-row
 // registers). The launch plan keeps ceil(NB / KS) within it: KS >= 4 when NB >= 4.
 constexpr int ode_owned_rows(int nb) { return nb <= 2 ? nb : nb / 4; }
-
-// Batch tiles whose chain kernel may stage a whole time step in LDS.
-constexpr bool ode_stage_ok(int nb) { return nb <= 4; }
 
 // (NB, RC) pairs whose chain kernel can also keep the four recurrent
 // gradient accumulators of every register-resident operand without spilling
@@ -48,10 +45,11 @@ struct Plan {
   int B, T, D, H, U;
   int Hp, Dp;      // H and D rounded up to 64 (one wave of lanes per 64 columns)
   int NB;          // batch rows per workgroup in the persistent ODE kernels
-  int KS;          // split of the reduction axis across waves of one workgroup
-  int RC;          // reduction chunk per thread = Hp / KS
+  int KS;          // forward: split of the reduction axis across waves of one workgroup
+  int RC;          // forward: reduction chunk per thread = Hp / KS
+  int KSB;         // chain (backward) kernel: the same split
+  int RCB;         // chain kernel: Hp / KSB
   bool FUSE;       // recurrent parameter gradients accumulated inside the chain kernel
-  bool STAGE;      // chain kernel stages each step's saved states in LDS
   int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances

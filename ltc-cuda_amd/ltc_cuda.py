@@ -57,10 +57,12 @@ class CApi:
         "ltc_kernel_name",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
-                   "NRC", "ode_workgroups", "fuse", "stage")
+                   "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
+                   "threads_bwd")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path
+        self._sizes = {}
         lib = ctypes.CDLL(path)
         self.lib = lib
         lib.ltc_abi_version.restype = _int
@@ -114,6 +116,23 @@ class CApi:
         lib.ltc_kernel_count.argtypes = []
         lib.ltc_kernel_name.restype = ctypes.c_char_p
         lib.ltc_kernel_name.argtypes = [_int]
+
+    def sizes(self, kind: str, B: int, T: int, D: int, H: int, U: int) -> int:
+        """Cached size query (saved floats / workspace bytes) for one shape."""
+        key = (kind, B, T, D, H, U)
+        v = self._sizes.get(key)
+        if v is None:
+            fn = {"saved": lambda: self.lib.ltc_saved_floats(B, T, H, U),
+                  "fwd_ws": lambda: self.lib.ltc_fwd_workspace_bytes(B, T, D, H, U),
+                  "bwd_ws": lambda: self.lib.ltc_bwd_workspace_bytes(B, T, D, H, U),
+                  "msaved": lambda: self.lib.ltc_module_saved_floats(B, T, D, H, U),
+                  "mfwd_ws": lambda: self.lib.ltc_module_fwd_workspace_bytes(B, T, D, H, U),
+                  "mbwd_ws": lambda: self.lib.ltc_module_bwd_workspace_bytes(B, T, D, H, U)}[kind]
+            v = int(fn())
+            if v < 0:
+                raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+            self._sizes[key] = v
+        return v
 
     def last_error(self) -> str:
         return self.lib.ltc_last_error().decode(errors="replace")
@@ -208,13 +227,9 @@ class _HipModule:
         h = torch.empty(B, H, device=dev, dtype=torch.float32)
         saved = None
         if save_intermediates:
-            n = lib.ltc_saved_floats(B, T, H, U)
-            if n < 0:
-                raise ValueError(f"bad sizes for ltc_saved_floats: B={B} T={T} H={H} U={U}")
-            saved = torch.empty(max(int(n), 1), device=dev, dtype=torch.float32)
-        need = lib.ltc_fwd_workspace_bytes(B, T, D, H, U)
-        if need < 0:
-            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+            n = self.capi.sizes("saved", B, T, D, H, U)
+            saved = torch.empty(max(n, 1), device=dev, dtype=torch.float32)
+        need = self.capi.sizes("fwd_ws", B, T, D, H, U)
         with torch.cuda.device(dev):
             ws = _workspace(need, dev)
             sx = x_seq.stride()
@@ -253,9 +268,7 @@ class _HipModule:
         grads += [torch.empty(H, H, **f32) for _ in range(4)]
         grads += [torch.empty(D, H, **f32) for _ in range(4)]
         grads += [torch.empty(H, **f32) for _ in range(3)]
-        need = lib.ltc_bwd_workspace_bytes(B, T, D, H, U)
-        if need < 0:
-            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        need = self.capi.sizes("bwd_ws", B, T, D, H, U)
         with torch.cuda.device(dev):
             ws = _workspace(need, dev)
             sx = x_seq.stride()
@@ -287,19 +300,15 @@ def _module_forward(capi, x, state, leaves, dt, U, eps, ln_eps, save):
     H = state.shape[1]
     dev = x.device
     lib = capi.lib
-    leaves = [t.contiguous() for t in leaves]
-    state_c = state.contiguous()
+    leaves = [t if t.is_contiguous() else t.contiguous() for t in leaves]
+    state_c = state if state.is_contiguous() else state.contiguous()
     out = torch.empty(B, T, H, device=dev, dtype=torch.float32)
     h = torch.empty(B, H, device=dev, dtype=torch.float32)
     saved = None
     if save:
-        n = lib.ltc_module_saved_floats(B, T, D, H, U)
-        if n < 0:
-            raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
-        saved = torch.empty(max(int(n), 1), device=dev, dtype=torch.float32)
-    need = lib.ltc_module_fwd_workspace_bytes(B, T, D, H, U)
-    if need < 0:
-        raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+        n = capi.sizes("msaved", B, T, D, H, U)
+        saved = torch.empty(max(n, 1), device=dev, dtype=torch.float32)
+    need = capi.sizes("mfwd_ws", B, T, D, H, U)
     with torch.cuda.device(dev):
         ws = _workspace(need, dev)
         sx = x.stride()
@@ -316,7 +325,7 @@ def _module_backward(capi, x, state, leaves, saved, grad_out, grad_h, dt, U, eps
     H = state.shape[1]
     dev = x.device
     lib = capi.lib
-    leaves = [t.contiguous() for t in leaves]
+    leaves = [t if t.is_contiguous() else t.contiguous() for t in leaves]
     go = grad_out
     if go.dtype != torch.float32 or go.device != dev:
         go = go.to(device=dev, dtype=torch.float32)
@@ -327,9 +336,7 @@ def _module_backward(capi, x, state, leaves, saved, grad_out, grad_h, dt, U, eps
     grads += [torch.empty(D, H, **f32) for _ in range(4)]
     grads += [torch.empty(H, **f32) for _ in range(3)]
     grads += [torch.empty(D, **f32) for _ in range(4)]
-    need = lib.ltc_module_bwd_workspace_bytes(B, T, D, H, U)
-    if need < 0:
-        raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
+    need = capi.sizes("mbwd_ws", B, T, D, H, U)
     with torch.cuda.device(dev):
         ws = _workspace(need, dev)
         sx = x.stride()

@@ -117,7 +117,7 @@ def test_no_device_reported_without_gpu(capi):
 
 def _max_threads(nb):
     # Mirror of ode_max_threads() in ltc-cuda_amd/csrc/ltc_internal.h.
-    return 1024 if nb <= 2 else (512 if nb <= 4 else 256)
+    return 1024 if nb <= 1 else (512 if nb <= 4 else 256)
 
 
 SHAPES = [(B, T, D, H, U) for B in (1, 2, 24, 255, 256, 257, 511, 1024, 4096, 5000)
@@ -138,17 +138,17 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     assert p["NB"] in (1, 2, 4, 8, 16)
     assert p["KS"] >= 1 and p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 4 == 0
     assert p["threads"] == p["Hp"] * p["KS"] <= _max_threads(p["NB"])
+    assert p["KSB"] >= 1 and p["KSB"] * p["RCB"] == p["Hp"] and p["RCB"] % 4 == 0
+    assert p["threads_bwd"] == p["Hp"] * p["KSB"] <= _max_threads(p["NB"])
     # rows finished per thread fit the kernel's compile-time per-row registers
     owned = p["NB"] if p["NB"] <= 2 else p["NB"] // 4
-    assert -(-p["NB"] // p["KS"]) <= owned
+    assert -(-p["NB"] // p["KS"]) <= owned and -(-p["NB"] // p["KSB"]) <= owned
     assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
-    if p["stage"]:
-        assert p["NB"] <= 4 and (2 * U + 1) * p["NB"] * p["Hp"] <= 8 * p["threads"]
     assert 1 <= p["NRC"] <= 64
     if p["fuse"]:
         # one partial per chain workgroup; operands and accumulators in registers
-        assert p["RC"] in (4, 8, 16) and p["NCH"] == p["ode_workgroups"]
-        assert (p["NB"], p["RC"]) in ((1, 4), (4, 4), (4, 8), (8, 4), (8, 8), (16, 4))
+        assert p["RCB"] in (4, 8, 16) and p["NCH"] == p["ode_workgroups"]
+        assert (p["NB"], p["RCB"]) in ((1, 4), (4, 4), (4, 8), (8, 4), (8, 8), (16, 4))
     else:
         assert 1 <= p["NCH"] <= 64
     assert p["ode_workgroups"] * p["NB"] >= B > (p["ode_workgroups"] - 1) * p["NB"] or B == 0

@@ -435,3 +435,40 @@ def test_eval_mode_uses_cached_transforms_like_the_reference():
     p = {k: v.detach().cpu() for k, v in m.state_dict().items()}
     r, _ = O.module_forward(p, x.cpu())
     assert (c.cpu() - r).abs().max().item() <= 1e-3
+
+
+def test_hip_graph_capture_replays_match_eager():
+    """The layer's fwd+bwd captures into HIP graphs (torch.cuda.make_graphed_callables):
+    the library only launches kernels on the current stream and allocates nothing, so
+    every replay must reproduce the eager results bit for bit, with eager work and
+    synchronisations between replays."""
+    m = _perturbed_module(128, 64, seed=31).to(DEV)
+    x = torch.randn(24, 8, 128, device=DEV)
+
+    class Step(torch.nn.Module):
+        def __init__(self, inner):
+            super().__init__()
+            self.inner = inner
+
+        def forward(self, xx):
+            out, (h, _) = self.inner(xx)
+            return out, h
+
+    step = Step(m)
+
+    def run(fn):
+        m.zero_grad(set_to_none=True)
+        out, h = fn(x)
+        (out.sum() + 0.5 * h.sum()).backward()
+        torch.cuda.synchronize()
+        return [out.detach().clone(), h.detach().clone()] + [p.grad.clone() for p in m.parameters()]
+
+    ref = run(step)
+    graphed = torch.cuda.make_graphed_callables(step, (x,))
+    for _ in range(4):
+        got = run(graphed)
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+        with torch.no_grad():
+            step(x)                      # eager work between replays
+        torch.cuda.synchronize()
