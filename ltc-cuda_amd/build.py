@@ -40,6 +40,8 @@ def command(out: str = LIB_PATH) -> list:
         "-mcode-object-version=5",
         # Resolve libamdhip64.so.7 by SONAME (torch's copy once torch is loaded).
         "-fno-rtlib-add-rpath",
+        # Fixed SONAME: the torch extension and ctypes then share one instance.
+        "-Wl,-soname," + LIB_NAME,
         # No packed-FP32 (v_pk_*_f32) instructions anywhere in device code.
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wall",
@@ -66,6 +68,51 @@ def build_probe(verbose: bool = False) -> str:
     return PROBE_BIN
 
 
+EXT_SRC = os.path.join(CSRC, "ltc_torch_ext.cpp")
+EXT_NAME = "_ltc_torch"
+
+
+def ext_path() -> str:
+    import sysconfig
+    return os.path.join(HERE, EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def ext_command(out: str) -> list:
+    """Host-only C++ build of the torch glue (the autograd Function of the
+    fused module path), linked against libltc_hip.so through $ORIGIN."""
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension as ce
+    incs = ce.include_paths("cuda") + [sysconfig.get_paths()["include"]]
+    libs = ce.library_paths("cuda")[:1]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return [
+        os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared",
+        "-fvisibility=hidden", "-w",
+        # The HIP headers torch includes select their AMD half with this macro.
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-DTORCH_EXTENSION_NAME={EXT_NAME}",
+        "-DTORCH_API_INCLUDE_EXTENSION_H",
+        *[f"-I{d}" for d in incs], EXT_SRC, "-o", out,
+        f"-L{HERE}", "-lltc_hip", *[f"-L{d}" for d in libs],
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        "-Wl,-rpath,$ORIGIN", "-Wl,--no-as-needed",
+    ]
+
+
+def build_ext(verbose: bool = False) -> str:
+    out = ext_path()
+    tmp = out + ".tmp"
+    cmd = ext_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("torch extension build failed:\n" + proc.stdout + proc.stderr)
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     cmd = command(tmp)
@@ -79,6 +126,7 @@ def build(verbose: bool = False) -> str:
     if verbose and msgs:
         print("\n".join(msgs), flush=True)
     os.replace(tmp, LIB_PATH)
+    build_ext(verbose)
     build_probe(verbose)
     return LIB_PATH
 

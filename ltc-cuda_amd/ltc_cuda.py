@@ -34,6 +34,9 @@ logger = logging.getLogger(__name__)
 _HAS_CUDA_KERNELS = False
 _cuda_module = None
 _LOAD_ERROR: str | None = None
+# C++ autograd Function of the fused module path (csrc/ltc_torch_ext.cpp), over
+# the same library; None when that extension is not built.
+_torch_ext = None
 
 LIB_NAME = "libltc_hip.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
@@ -392,7 +395,16 @@ class LTCModuleFunction(torch.autograd.Function):
 
 
 def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
-    """Whole-layer fused call; `leaves` in MODULE_LEAVES order."""
+    """Whole-layer fused call; `leaves` in MODULE_LEAVES order.
+
+    Runs through the C++ autograd Function when the torch extension is built
+    (no Python in the per-step forward or backward), else through
+    LTCModuleFunction; both call the same two library entry points.
+    """
+    require_kernels()
+    if _torch_ext is not None:
+        return tuple(_torch_ext.module_apply(x_seq, state, list(leaves), float(dt),
+                                             int(ode_unfolds), float(epsilon), float(ln_eps)))
     needs_grad = torch.is_grad_enabled()
     return LTCModuleFunction.apply(x_seq, state, *leaves, float(dt), int(ode_unfolds),
                                    float(epsilon), float(ln_eps), needs_grad)
@@ -434,8 +446,36 @@ def _try_load_hip_kernels() -> bool:
     _cuda_module = _HipModule(capi)
     _HAS_CUDA_KERNELS = True
     _LOAD_ERROR = None
+    _load_torch_ext()
     logger.info("Loaded LTC HIP kernels from %s", LIB_PATH)
     return True
+
+
+def _load_torch_ext() -> None:
+    """Import the C++ autograd glue built beside the library, if present."""
+    global _torch_ext
+    import importlib.machinery
+    import importlib.util
+    import sysconfig
+    _torch_ext = None
+    path = os.path.join(os.path.dirname(LIB_PATH),
+                        "_ltc_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not os.path.isfile(path):
+        logger.info("LTC torch extension not built; module path uses the Python Function")
+        return
+    try:
+        loader = importlib.machinery.ExtensionFileLoader("_ltc_torch", path)
+        spec = importlib.util.spec_from_file_location("_ltc_torch", path, loader=loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+    except ImportError as exc:
+        logger.warning("LTC torch extension failed to load (%s); using the Python Function",
+                       exc)
+        return
+    if mod.abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path}: linked against ABI {mod.abi_version()}, "
+                           f"expected {ABI_VERSION}")
+    _torch_ext = mod
 
 
 # Name kept for callers of the reference loader.

@@ -152,3 +152,30 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     else:
         assert 1 <= p["NCH"] <= 64
     assert p["ode_workgroups"] * p["NB"] >= B > (p["ode_workgroups"] - 1) * p["NB"] or B == 0
+
+
+def _ext_path():
+    import sysconfig
+    return os.path.join(os.path.dirname(ltc_cuda.LIB_PATH),
+                        "_ltc_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+@pytest.mark.skipif(not os.path.isfile(_ext_path()), reason="torch extension not built")
+def test_torch_extension_shares_the_library_and_validates_on_cpu():
+    """The C++ autograd glue links libltc_hip.so by SONAME (one library instance per
+    process) and rejects host tensors before it reaches the library."""
+    import importlib.machinery
+    import importlib.util
+    loader = importlib.machinery.ExtensionFileLoader("_ltc_torch", _ext_path())
+    spec = importlib.util.spec_from_file_location("_ltc_torch", _ext_path(), loader=loader)
+    ext = importlib.util.module_from_spec(spec)
+    loader.exec_module(ext)
+    assert ext.abi_version() == ltc_cuda.ABI_VERSION
+    B, T, D, H = 2, 3, 4, 5
+    leaves = [torch.zeros(H, H)] * 5 + [torch.zeros(D, H)] * 5 + [torch.zeros(H)] * 3 \
+        + [torch.zeros(D)] * 4
+    with pytest.raises(RuntimeError, match="fp32-only"):
+        ext.module_apply(torch.zeros(B, T, D), torch.zeros(B, H), leaves, 0.1, 6, 1e-8, 1e-5)
+    with pytest.raises(RuntimeError, match="17 LTC leaves"):
+        ext.module_apply(torch.zeros(B, T, D), torch.zeros(B, H), leaves[:3], 0.1, 6, 1e-8,
+                         1e-5)

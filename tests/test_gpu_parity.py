@@ -420,6 +420,40 @@ def test_module_path_strided_input_and_determinism():
     assert torch.equal(out_ng, res[0][0])
 
 
+def test_cpp_and_python_module_functions_agree_bitwise():
+    """The C++ autograd Function (torch extension) and the Python LTCModuleFunction call
+    the same two library entry points; outputs and every gradient must be identical."""
+    assert ltc_cuda._torch_ext is not None, "torch extension (_ltc_torch) not loaded"
+    B, T, D, H = 8, 5, 48, 40
+    m = _perturbed_module(D, H, seed=9).to(DEV)
+    leaves_sd = dict(m.named_parameters())
+    leaves_sd.update(dict(m.named_buffers()))
+    x = torch.randn(B, T, D, device=DEV)
+    h0 = 0.1 * torch.randn(B, H, device=DEV)
+    G = torch.randn(B, T, H, device=DEV)
+    Gh = torch.randn(B, H, device=DEV)
+    res = []
+    for use_ext in (True, False):
+        saved_ext = ltc_cuda._torch_ext
+        if not use_ext:
+            ltc_cuda._torch_ext = None
+        try:
+            xs = x.clone().requires_grad_(True)
+            hs = h0.clone().requires_grad_(True)
+            leaves = [leaves_sd[k] for k in ltc_cuda.MODULE_LEAVES]
+            for p in m.parameters():
+                p.grad = None
+            out, h = ltc_cuda.ltc_module_forward(xs, hs, leaves, m.dt, m.ode_unfolds,
+                                                 m.epsilon, m.input_norm.eps)
+            ((out * G).sum() + (h * Gh).sum()).backward()
+        finally:
+            ltc_cuda._torch_ext = saved_ext
+        res.append([out.detach(), h.detach(), xs.grad, hs.grad]
+                   + [p.grad for p in m.parameters()])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
 def test_eval_mode_uses_cached_transforms_like_the_reference():
     """Eval mode keeps the reference's cache semantics: stale after an in-place edit."""
     torch.manual_seed(42)
