@@ -281,7 +281,7 @@ def measure_large(name, c, capi):
     rec["ms_per_step"] = round(ms, 4)
     rec["synapse_updates_per_s"] = n_syn(c) / (ms * 1e-3)
     rec["kernels_ms"] = {k: round(v[0], 5) for k, v in kt.items()}
-    rec["roofline"] = roofline(c, kt)
+    rec["roofline"] = roofline(c, kt, load_traffic(name))
     which = "fwd" if c["loss"] is None else "fwdbwd"
     ksum = sum(v[0] * v[1] for v in kt.values())
     rec["kernel_ms_sum"] = round(ksum, 4)
