@@ -188,10 +188,13 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
  * chunks, or one per workgroup when fused), NRC (sensory backward row
  * chunks), ODE workgroups, 1 when the recurrent parameter gradients are
  * accumulated inside the chain kernel, then the chain kernel's own KS, RC
- * and threads (the fields before them describe the forward kernel). Returns
- * the number of values written, or -1 for invalid sizes.
+ * and threads (the fields before them describe the forward kernel), then CP
+ * and NCL: with CP > 0 the ODE kernels run as NCL clusters of CP workgroups
+ * that each own 64 columns of NB rows (threads and LDS fields then describe
+ * one cluster member). Returns the number of values written, or -1 for
+ * invalid sizes. The plan depends on the current device's CU count.
  */
-#define LTC_PLAN_FIELDS 15
+#define LTC_PLAN_FIELDS 17
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

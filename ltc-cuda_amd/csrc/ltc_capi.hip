@@ -22,10 +22,64 @@ int fail(int code, const std::string& msg) {
 
 long long round_up(long long v, long long m) { return (v + m - 1) / m * m; }
 
+// Compute units of the current device (cached per device). Without a device
+// the plan is made for MI355X's 256.
+int device_cus() {
+  constexpr int kMaxDev = 64;
+  static int cache[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n < 1) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Cluster path (H > 192): CP = Hp/64 workgroups share NB rows, one 64-column
+// slice each, so every operand serves NB rows while up to one workgroup per
+// CU runs. The whole grid must be resident at once (members wait on each
+// other), so it is used only when NCL * CP <= CUs, with 1024 threads and at
+// most 64 KiB of LDS per workgroup (one workgroup fits on any CU).
+// Dynamic LDS of a cluster member, leaving room for its static flag word.
+constexpr long long kClusterLds = 60 * 1024;
+
+bool plan_cluster(ltc::Plan& p, int ncu) {
+  if (p.Hp < 256 || p.B < 1) return false;
+  const int cp = p.Hp / 64;
+  const int slots = ncu / cp;
+  for (int nb : {1, 2, 4, 8}) {
+    const int ncl = (p.B + nb - 1) / nb;
+    if (ncl > slots) continue;
+    for (int ks = 16; ks >= nb && ks >= 8; ks >>= 1) {
+      if ((p.Hp / ks) % 8 != 0) continue;  // streamed operands come eight rows at a time
+      const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
+      const long long lb = (long long)nb * p.Hp * 8 + (long long)ks * nb * 64 * 4;
+      if (lf > kClusterLds || lb > kClusterLds) continue;
+      p.CP = cp;
+      p.NCL = ncl;
+      p.NB = nb;
+      p.KS = p.KSB = ks;
+      p.RC = p.RCB = p.Hp / ks;
+      p.FUSE = false;
+      return true;
+    }
+  }
+  return false;
+}
+
 // ---------------------------------------------------------------------------
 // Launch plan
 // ---------------------------------------------------------------------------
-ltc::Plan make_plan(int B, int T, int D, int H, int U) {
+ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
   ltc::Plan p{};
   p.B = B;
   p.T = T;
@@ -93,6 +147,8 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U) {
   // the chain kernel also accumulates the recurrent parameter gradients and
   // writes one partial per workgroup.
   p.FUSE = ltc::ode_fuse_ok(p.NB, p.RCB);
+  p.CP = p.NCL = 0;
+  plan_cluster(p, ncu);
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
   if (p.FUSE) {
@@ -138,19 +194,34 @@ struct Carver {
   }
 };
 
+// Operand image rows: the cluster kernels' streamed prefetch may read a few
+// rows past the end.
+long long image_rows(const ltc::Plan& p) { return p.Hp + (p.CP > 0 ? ltc::kImageSlackRows : 0); }
+
+ltc::ClusterBuf carve_cluster(const ltc::Plan& p, Carver& c) {
+  ltc::ClusterBuf cb{nullptr, nullptr};
+  if (p.CP > 0) {
+    cb.xch = c.take<unsigned long long>(ltc::cluster_words(p));
+    cb.status = c.take<int>(1);
+  }
+  return cb;
+}
+
 struct FwdWs {
   ltc::Prepped pp;
   float* sn;
   float* sd;
+  ltc::ClusterBuf cb;
 };
 
 FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
   FwdWs w{};
-  w.pp.recF = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
   w.pp.neuron = c.take<float>(3LL * p.Hp);
   w.sn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.sd = c.take<float>((long long)p.B * p.T * p.Hp);
+  w.cb = carve_cluster(p, c);
   return w;
 }
 
@@ -163,12 +234,13 @@ struct BwdWs {
   float* rpart;
   float* spart;
   float* dxpart;
+  ltc::ClusterBuf cb;
 };
 
 BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   BwdWs w{};
   w.pp.recF = c.take<float4>((long long)p.Hp * p.Hp);
-  w.pp.recB = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.recB = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
   w.pp.neuron = c.take<float>(3LL * p.Hp);
   w.absave = p.FUSE ? nullptr : c.take<float2>(p.N * p.Hp);
@@ -178,6 +250,7 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   w.rpart = c.take<float>((long long)p.NCH * 4 * p.Hp * p.Hp);
   w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
   w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
+  w.cb = carve_cluster(p, c);
   return w;
 }
 
@@ -376,7 +449,8 @@ int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd
   e = timed(ltc::K_SENS_FWD, s, [&] { return ltc::launch_sens_fwd(p, x, xs, w.pp, w.sn, w.sd, s); });
   if (e != hipSuccess) return hip_fail("sensory forward launch", e);
   e = timed(ltc::K_ODE_FWD, s, [&] {
-    return ltc::launch_ode_fwd(p, w.pp, w.sn, w.sd, state, epsilon, out, h_final, vsave, densave, s);
+    return ltc::launch_ode_fwd(p, w.pp, w.sn, w.sd, state, epsilon, out, h_final, vsave, densave,
+                               w.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
   return LTC_OK;
@@ -462,7 +536,7 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
   if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_ODE_BWD, s, [&] {
     return ltc::launch_ode_bwd(p, w.pp, vsave, densave, grad_out, gs, grad_h_final, w.absave,
-                               w.dsn, w.dsd, w.npart, grad_state, w.rpart, s);
+                               w.dsn, w.dsd, w.npart, grad_state, w.rpart, w.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE backward launch", e);
   if (!p.FUSE) {
@@ -578,7 +652,7 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   if (e != hipSuccess) return hip_fail("sensory forward launch", e);
   e = timed(ltc::K_ODE_FWD, s, [&] {
     return ltc::launch_ode_fwd(p, wfw.pp, wfw.sn, wfw.sd, state, epsilon, out, h_final, vsave,
-                               densave, s);
+                               densave, wfw.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
   return LTC_OK;
@@ -677,7 +751,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_ODE_BWD, s, [&] {
     return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.absave,
-                               wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, s);
+                               wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, wb.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE backward launch", e);
   if (!p.FUSE) {
@@ -702,12 +776,14 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n) {
   if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || !out || n < 0) return -1;
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
+  // Columns each workgroup of the ODE kernels owns: all Hp, or 64 per member.
+  const long long cols = p.CP > 0 ? 64 : p.Hp;
   const long long v[LTC_PLAN_FIELDS] = {
-      p.Hp, p.Dp, p.NB, p.KS, p.RC, (long long)p.Hp * p.KS,
-      (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8,
-      (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4,
-      p.NCH, p.NRC, (B + p.NB - 1) / p.NB, p.FUSE ? 1 : 0, p.KSB, p.RCB,
-      (long long)p.Hp * p.KSB};
+      p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
+      (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8,
+      (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * cols * 4,
+      p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
+      p.FUSE ? 1 : 0, p.KSB, p.RCB, cols * p.KSB, p.CP, p.NCL};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

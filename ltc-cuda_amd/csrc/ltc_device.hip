@@ -1157,6 +1157,468 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
 }
 
 // ---------------------------------------------------------------------------
+// Cluster ODE kernels (H >= 256 with few batch rows per CU).
+// A cluster of CP workgroups advances NB batch rows together. Member p owns
+// the 64 columns [64p, 64p + 64) and keeps only that column slice of the
+// operand image, so every operand it reads serves NB rows while all CUs have
+// work. Workgroup g runs on XCD g % 8 and is member g % CP, so an XCD's L2
+// holds only the slices of the members it runs.
+// After every unfold each member publishes its new column values as 64-bit
+// words {value bits, unfold tag} (agent-scope atomic stores) and reads the
+// other members' words until their tags are current. A word is written and
+// read whole, so no fence or counter is involved. Two slots alternate by tag
+// parity: a member overwrites a slot only after all partners have published
+// the following unfold, which they do after they finished reading that slot.
+// Every wait is bounded (kSpinTicks of the 100 MHz wall clock). A member that
+// gives up sets *status, writes NaN into its final state and returns; its
+// partners then give up the same way, so the grid always drains.
+// Exchange layout: [cluster][2 slots][CP members][NB rows][64 columns] words,
+// cleared (tag 0) before every launch; tags start at 1.
+// ---------------------------------------------------------------------------
+constexpr int kClW = 64;                    // columns per cluster member
+constexpr long long kSpinTicks = 20000000;  // 0.2 s at 100 MHz
+
+__device__ __forceinline__ void xch_put(unsigned long long* w, float v, unsigned tag) {
+  const unsigned long long word =
+      (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+  __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long xch_get(unsigned long long* w) {
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reads the (CP-1)*PER words of the other members for unfold `tag`, XB per
+// thread at a time. For each word: pre(x, a) is called once before the first
+// poll (to start the loads its delivery needs), deliver(x, a, value) once the
+// tag is current; a = q*PER + b*64 + col is the word's offset in the slot and
+// x its index in the batch. Returns false if a wait ran out.
+constexpr int kXchBatch = 2;
+
+template <int PER, class Pre, class Deliver>
+__device__ __forceinline__ bool xch_gather(unsigned long long* slot, int p, int nwords, int tid,
+                                           int nthr, unsigned tag, Pre&& pre, Deliver&& deliver) {
+  constexpr int XB = kXchBatch;
+  for (int e0 = tid; e0 < nwords; e0 += XB * nthr) {
+    unsigned long long w[XB];
+    int at[XB];
+    bool wait[XB];
+#pragma unroll
+    for (int x = 0; x < XB; ++x) {
+      const int e = e0 + x * nthr;
+      wait[x] = e < nwords;
+      at[x] = e + (e / PER >= p ? PER : 0);  // skip this member's own words
+      if (wait[x]) {
+        w[x] = xch_get(slot + at[x]);
+        pre(x, at[x]);
+      }
+    }
+    const long long t0 = wall_clock64();
+    for (;;) {
+      bool any = false;
+#pragma unroll
+      for (int x = 0; x < XB; ++x) {
+        if (wait[x]) {
+          if ((unsigned)(w[x] >> 32) == tag) {
+            wait[x] = false;
+            deliver(x, at[x], __uint_as_float((unsigned)w[x]));
+          } else {
+            any = true;
+          }
+        }
+      }
+      if (!any) break;
+      if (wall_clock64() - t0 > kSpinTicks) return false;
+#pragma unroll
+      for (int x = 0; x < XB; ++x)
+        if (wait[x]) w[x] = xch_get(slot + at[x]);
+    }
+  }
+  return true;
+}
+
+struct FwdCK {
+  const float4* recF;  // [Hp + 8][Hp]: 8 zero rows of slack for the streamed prefetch
+  const float* neuron;
+  const float* sn;
+  const float* sd;
+  const float* state0;
+  float* out;
+  float* hfin;
+  float* vsave;
+  float* densave;
+  unsigned long long* xch;
+  int* status;
+  int B, T, H, Hp, U, KS, RC, CP;
+  float eps;
+};
+
+template <int NB, int RCP>
+__global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
+  constexpr int PER = NB * kClW;
+  extern __shared__ float4 lds4[];
+  __shared__ int gave_up;
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
+  const int RC = RCP > 0 ? RCP : k.RC;
+  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp]
+  float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][64]
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  const int p = blockIdx.x % CP, cl = blockIdx.x / CP;
+  const int c = p * kClW + o;  // output column of this thread
+  const int b0 = cl * NB;
+  const int r0 = ks * RC;
+  const bool owner = ks < NB;  // finishes row ks of column c (the plan keeps KS >= NB)
+  const int bo = ks;
+  const bool live = owner && b0 + bo < B;
+  unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
+  const int nwords = (CP - 1) * PER;
+
+  const float C = k.neuron[c], G = k.neuron[Hp + c], L = k.neuron[2 * Hp + c];
+  const float GL = G * L, CG = C + G;
+
+  float4 preg[RCP > 0 ? RCP : 1];
+  if constexpr (RCP > 0) {
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * Hp + c];
+  }
+  if (tid == 0) gave_up = 0;
+  for (int e = tid; e < NB * Hp; e += nthr) {
+    const int b = e / Hp, j = e - b * Hp;
+    vs[e] = (b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j] : 0.f;
+  }
+  lds_barrier();
+
+  float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
+  auto load_sens = [&](int t, float& a, float& d) {
+    a = d = 0.f;
+    if (live) {
+      const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
+      a = k.sn[e];
+      d = k.sd[e];
+    }
+  };
+  if (T > 0) load_sens(0, snr, sdr);
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) load_sens(t + 1, snn, sdn);
+    for (int u = 0; u < U; ++u) {
+      float na[NB], qa[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) na[b] = qa[b] = 0.f;
+      if constexpr (RCP > 0) {
+#pragma unroll
+        for (int rr = 0; rr < RCP; ++rr) fwd_synapse<NB>(preg[rr], vs, Hp, r0 + rr, na, qa);
+      } else {
+        // Streamed operands, double-buffered four rows at a time. The wave's
+        // row offset is uniform (scalar base address); the prefetch past the
+        // chunk's end reads the next chunk or the zero slack rows.
+        const float4* pc = k.recF + (long long)r0 * Hp;
+        float4 pa[4], pb[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp + c];
+        for (int rr = 0; rr < RC; rr += 8) {
+          const float4* pr = pc + (long long)rr * Hp;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pb[q] = pr[(long long)(4 + q) * Hp + c];
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pa[q], vs, Hp, r0 + rr + q, na, qa);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) pa[q] = pr[(long long)(8 + q) * Hp + c];
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pb[q], vs, Hp, r0 + rr + 4 + q, na, qa);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = make_float2(na[b], qa[b]);
+      lds_barrier();
+      const unsigned tag = (unsigned)(t * U + u + 1);
+      unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
+      if (owner) {
+        const float2 nq = ks_sum(red + bo * kClW + o, NB * kClW, KS);
+        const float vold = vs[bo * Hp + c];
+        const float den = CG + (nq.y + sdr) + k.eps;
+        const float num = C * vold + GL + (nq.x + snr);
+        const float vnew = c < H ? num / den : 0.f;
+        if (k.vsave != nullptr && live) {
+          const long long e = ((long long)(t * U + u) * B + b0 + bo) * Hp + c;
+          k.vsave[e] = vold;
+          k.densave[e] = den;
+        }
+        vs[bo * Hp + c] = vnew;
+        if (u == U - 1 && live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
+        xch_put(slot + p * PER + bo * kClW + o, vnew, tag);
+      }
+      const bool ok = xch_gather<PER>(
+          slot, p, nwords, tid, nthr, tag, [](int, int) {},
+          [&](int, int a, float v) {
+            const int q = a / PER, r = a - q * PER;
+            vs[(r >> 6) * Hp + q * kClW + (r & 63)] = v;
+          });
+      if (!ok) gave_up = 1;
+      lds_barrier();
+      if (gave_up) {
+        if (live && c < H) k.hfin[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
+        if (tid == 0) __hip_atomic_store(k.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+    }
+    snr = snn;
+    sdr = sdn;
+  }
+  if (live) {
+    const float v = vs[bo * Hp + c];
+    if (c < H) k.hfin[(long long)(b0 + bo) * H + c] = v;
+    if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0 + bo) * Hp + c] = v;
+  }
+}
+
+struct BwdCK {
+  const float4* recB;  // [Hp + 8][Hp], 8 zero rows of slack
+  const float* neuron;
+  const float* vsave;
+  const float* densave;
+  const float* gout;
+  Strides3 gs;
+  const float* ghfin;
+  float2* absave;
+  float* dsn;
+  float* dsd;
+  float* npart;
+  float* gstate;
+  unsigned long long* xch;
+  int* status;
+  int B, T, H, Hp, U, KS, RC, CP;
+};
+
+// Cluster chain: member p forms dL/dv_i for its 64 columns i (reduction over
+// every postsynaptic j) and publishes them; alpha_j/beta_j of the other
+// members' columns are then rebuilt from the published dL/dv_j and the saved
+// den_j, v_j, so only one value per (row, column) crosses the cluster.
+template <int NB, int RCP>
+__global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
+  constexpr int PER = NB * kClW;
+  extern __shared__ float4 lds4[];
+  __shared__ int gave_up;
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
+  const int RC = RCP > 0 ? RCP : k.RC;
+  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
+  float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][64]
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  const int p = blockIdx.x % CP, cl = blockIdx.x / CP;
+  const int c = p * kClW + o;
+  const int b0 = cl * NB;
+  const int r0 = ks * RC;
+  const bool owner = ks < NB;
+  const int bo = ks;
+  const bool live = owner && b0 + bo < B;
+  unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
+  const int nwords = (CP - 1) * PER;
+  const long long BHp = (long long)B * Hp;
+  const float C = k.neuron[c];
+  if (T == 0) return;
+
+  float4 preg[RCP > 0 ? RCP : 1];
+  if constexpr (RCP > 0) {
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + c];
+  }
+  if (tid == 0) gave_up = 0;
+
+  // Owner state: g = dL/dv of (row bo, column c) after the current unfold.
+  float g = 0.f, gdir = 0.f, accA = 0.f, accB = 0.f, pC = 0.f, pGv = 0.f, pA = 0.f;
+  // alpha/beta of unfold n for the owned entry; accumulates the per-step and
+  // per-row sums that the sensory and neuron gradients need.
+  auto own_ab = [&](long long n, float den, float vk, float vk1) {
+    float al = 0.f, be = 0.f;
+    gdir = 0.f;
+    if (live && c < H) {
+      const float rden = 1.0f / den;
+      al = g * rden;
+      be = -g * vk1 * rden;
+      accA += al;
+      accB += be;
+      pC += al * (vk - vk1);
+      pGv += al * vk1;
+      pA += al;
+      gdir = al * C;
+    }
+    ab[bo * Hp + c] = make_float2(al, be);
+    if (live) k.absave[(n * B + b0 + bo) * Hp + c] = make_float2(al, be);
+  };
+  auto gout_at = [&](int b, int t, int col) {
+    return k.gout[(long long)(b0 + b) * k.gs.b + (long long)t * k.gs.t + (long long)col * k.gs.c];
+  };
+
+  const long long n_last = (long long)T * U - 1;
+  if (owner) {
+    if (live && c < H) {
+      g = gout_at(bo, T - 1, c);
+      if (k.ghfin != nullptr) g += k.ghfin[(long long)(b0 + bo) * H + c];
+    }
+    float den = 1.f, vk = 0.f, vk1 = 0.f;
+    if (live) {
+      const long long e = (n_last * B + b0 + bo) * Hp + c;
+      den = k.densave[e];
+      vk = k.vsave[e];
+      vk1 = k.vsave[e + BHp];
+    }
+    own_ab(n_last, den, vk, vk1);
+  }
+  // The other members' columns for the last unfold come straight from the
+  // output gradients (no exchange needed yet).
+  for (int e = tid; e < nwords; e += nthr) {
+    const int a = e + (e / PER >= p ? PER : 0);
+    const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+    float al = 0.f, be = 0.f;
+    if (b0 + b < B && col < H) {
+      float gg = gout_at(b, T - 1, col);
+      if (k.ghfin != nullptr) gg += k.ghfin[(long long)(b0 + b) * H + col];
+      const long long ee = (n_last * B + b0 + b) * Hp + col;
+      const float rden = 1.0f / k.densave[ee];
+      al = gg * rden;
+      be = -gg * k.vsave[ee + BHp] * rden;
+    }
+    ab[b * Hp + col] = make_float2(al, be);
+  }
+  lds_barrier();
+
+  float cvi[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    cvi[b] = b0 + b < B ? k.vsave[(n_last * B + b0 + b) * Hp + c] : 0.f;
+
+  for (long long n = n_last; n >= 0; --n) {
+    const int t = (int)(n / U), u = (int)(n - (long long)t * U);
+    // Output gradient entering at this step boundary (owner only).
+    float gnext = 0.f;
+    if (n > 0 && u == 0 && live && c < H) gnext = gout_at(bo, t - 1, c);
+    float acc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+    float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (RCP > 0) {
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr)
+        bwd_synapse<NB, false>(preg[rr], ab, Hp, r0 + rr, cvi, acc, unused);
+    } else {
+      const float4* pc = k.recB + (long long)r0 * Hp;
+      float4 pa[4], pb[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp + c];
+      for (int rr = 0; rr < RC; rr += 8) {
+        const float4* pr = pc + (long long)rr * Hp;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pb[q] = pr[(long long)(4 + q) * Hp + c];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bwd_synapse<NB, false>(pa[q], ab, Hp, r0 + rr + q, cvi, acc, unused);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pa[q] = pr[(long long)(8 + q) * Hp + c];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          bwd_synapse<NB, false>(pb[q], ab, Hp, r0 + rr + 4 + q, cvi, acc, unused);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = acc[b];
+    // Saved values of unfold n-1, requested now and consumed after the
+    // exchange, whose wait covers their latency.
+    float nden = 1.f, nvk = 0.f, nvk1 = 0.f;
+    if (n > 0) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+        acc[b] = b0 + b < B ? k.vsave[((n - 1) * B + b0 + b) * Hp + c] : 0.f;
+      if (live) {
+        const long long e = ((n - 1) * B + b0 + bo) * Hp + c;
+        nden = k.densave[e];
+        nvk = k.vsave[e];
+        nvk1 = k.vsave[e + BHp];
+      }
+    }
+    lds_barrier();
+    // ab and red of unfold n are consumed: publish dL/dv^n and build unfold
+    // n-1's alpha/beta.
+    const unsigned tag = (unsigned)n;
+    unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
+    if (owner) {
+      const float s = ks_sum(red + bo * kClW + o, NB * kClW, KS);
+      g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
+      if (u == 0 && live) {
+        const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
+        k.dsn[e] = accA;
+        k.dsd[e] = accB;
+      }
+      if (u == 0) accA = accB = 0.f;
+      if (n > 0) {
+        g += gnext;
+        xch_put(slot + p * PER + bo * kClW + o, g, tag);
+      }
+    }
+    if (n > 0) {
+      float pden[kXchBatch], pvk1[kXchBatch];
+      const bool ok = xch_gather<PER>(
+          slot, p, nwords, tid, nthr, tag,
+          [&](int x, int a) {
+            const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+            pden[x] = 1.f;
+            pvk1[x] = 0.f;
+            if (b0 + b < B) {
+              const long long ee = ((n - 1) * B + b0 + b) * Hp + col;
+              pden[x] = k.densave[ee];
+              pvk1[x] = k.vsave[ee + BHp];
+            }
+          },
+          [&](int x, int a, float gg) {
+            const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+            float al = 0.f, be = 0.f;
+            if (b0 + b < B && col < H) {
+              const float rden = 1.0f / pden[x];
+              al = gg * rden;
+              be = -gg * pvk1[x] * rden;
+            }
+            ab[b * Hp + col] = make_float2(al, be);
+          });
+      if (!ok) gave_up = 1;
+      if (owner) own_ab(n - 1, nden, nvk, nvk1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) cvi[b] = acc[b];
+    }
+    lds_barrier();
+    if (gave_up) {
+      if (live && c < H) k.gstate[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
+      if (tid == 0) __hip_atomic_store(k.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
+  if (live) {
+    if (c < H) k.gstate[(long long)(b0 + bo) * H + c] = g;
+    float* np = k.npart + (long long)(b0 + bo) * 3 * Hp + c;
+    np[0] = pC;
+    np[Hp] = pGv;
+    np[2 * Hp] = pA;
+  }
+}
+
+// Clears the cluster exchange words (tag 0) and the status word before a
+// cluster launch; a kernel rather than a memset so that graph capture
+// records a kernel node.
+__global__ __launch_bounds__(256) void clear_words_kernel(unsigned long long* w, long long n,
+                                                          int* status) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) w[i] = 0ULL;
+  if (i == 0 && status != nullptr) *status = 0;
+}
+
+// ---------------------------------------------------------------------------
 // Template dispatch helpers.
 // ---------------------------------------------------------------------------
 size_t fwd_lds_bytes(const Plan& p) {
@@ -1206,6 +1668,44 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Cluster path: grid NCL * CP, 64 * KS threads; RC = 16 keeps the operands
+// in registers, otherwise they stream (RC is a multiple of 8).
+size_t fwd_cl_lds_bytes(const Plan& p) {
+  return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * 64 * 8;
+}
+size_t bwd_cl_lds_bytes(const Plan& p) {
+  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KSB * p.NB * 64 * 4;
+}
+
+hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, hipStream_t s) {
+  const long long n = cluster_words(p);
+  hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     cb.xch, n, cb.status);
+  return hipGetLastError();
+}
+
+template <int NB>
+hipError_t fwd_cl_by_rcp(const Plan& p, const FwdCK& a, hipStream_t s) {
+  const dim3 grid(p.NCL * p.CP), block(64 * p.KS);
+  const size_t lds = fwd_cl_lds_bytes(p);
+  if (p.RC == 16)
+    hipLaunchKernelGGL((ode_fwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL((ode_fwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
+template <int NB>
+hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
+  const dim3 grid(p.NCL * p.CP), block(64 * p.KSB);
+  const size_t lds = bwd_cl_lds_bytes(p);
+  if (p.RCB == 16)
+    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
@@ -1252,7 +1752,19 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
 
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
                           const float* state0, float eps, float* out, float* hfin,
-                          float* vsave, float* densave, hipStream_t s) {
+                          float* vsave, float* densave, const ClusterBuf& cb, hipStream_t s) {
+  if (p.CP > 0) {
+    hipError_t e = clear_cluster(p, cb, s);
+    if (e != hipSuccess) return e;
+    FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
+            p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, eps};
+    switch (p.NB) {
+      case 8: return fwd_cl_by_rcp<8>(p, a, s);
+      case 4: return fwd_cl_by_rcp<4>(p, a, s);
+      case 2: return fwd_cl_by_rcp<2>(p, a, s);
+      default: return fwd_cl_by_rcp<1>(p, a, s);
+    }
+  }
   FwdK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave,
          p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, eps};
   switch (p.NB) {
@@ -1267,7 +1779,20 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
 hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           const float* densave, const float* gout, Strides3 gs,
                           const float* ghfin, float2* absave, float* dsn, float* dsd,
-                          float* npart, float* gstate, float* rpart, hipStream_t s) {
+                          float* npart, float* gstate, float* rpart, const ClusterBuf& cb,
+                          hipStream_t s) {
+  if (p.CP > 0) {
+    hipError_t e = clear_cluster(p, cb, s);
+    if (e != hipSuccess) return e;
+    BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
+            gstate, cb.xch, cb.status, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, p.CP};
+    switch (p.NB) {
+      case 8: return bwd_cl_by_rcp<8>(p, a, s);
+      case 4: return bwd_cl_by_rcp<4>(p, a, s);
+      case 2: return bwd_cl_by_rcp<2>(p, a, s);
+      default: return bwd_cl_by_rcp<1>(p, a, s);
+    }
+  }
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
          rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB};
   switch (p.NB) {

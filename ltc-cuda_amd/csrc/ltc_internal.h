@@ -50,6 +50,8 @@ struct Plan {
   int KSB;         // chain (backward) kernel: the same split
   int RCB;         // chain kernel: Hp / KSB
   bool FUSE;       // recurrent parameter gradients accumulated inside the chain kernel
+  int CP;          // cluster path: workgroups per cluster (0 = one workgroup per NB rows)
+  int NCL;         // cluster path: clusters = ceil(B / NB); grid = NCL * CP
   int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances
@@ -134,13 +136,26 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
                             const LnBuf* ln, hipStream_t s);
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
+// Cluster path scratch: exchange words and a status word (nonzero after a
+// cluster member gave up waiting for its partners).
+struct ClusterBuf {
+  unsigned long long* xch;
+  int* status;
+};
+// Exchange words of one cluster launch.
+inline long long cluster_words(const Plan& p) { return 2LL * p.NCL * p.CP * p.NB * 64; }
+// Rows of slack after the [Hp][Hp] operand images that the cluster kernels'
+// streamed prefetch may read.
+constexpr int kImageSlackRows = 8;
+
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
                           const float* state0, float eps, float* out, float* hfin,
-                          float* vsave, float* densave, hipStream_t s);
+                          float* vsave, float* densave, const ClusterBuf& cb, hipStream_t s);
 hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           const float* densave, const float* gout, Strides3 gs,
                           const float* ghfin, float2* absave, float* dsn, float* dsd,
-                          float* npart, float* gstate, float* rpart, hipStream_t s);
+                          float* npart, float* gstate, float* rpart, const ClusterBuf& cb,
+                          hipStream_t s);
 hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
                            const float2* absave, float* rpart, hipStream_t s);
 hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,

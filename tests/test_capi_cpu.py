@@ -122,7 +122,7 @@ def _max_threads(nb):
 
 SHAPES = [(B, T, D, H, U) for B in (1, 2, 24, 255, 256, 257, 511, 1024, 4096, 5000)
           for (D, H) in ((1, 1), (5, 4), (128, 64), (32, 65), (128, 128), (7, 192), (256, 256),
-                         (512, 512), (64, 1000), (3, 1024))
+                         (512, 512), (64, 1000), (3, 1024), (16, 320), (16, 200))
           for (T, U) in ((8, 6), (1, 1))]
 
 
@@ -135,6 +135,21 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     p = capi.plan(B, T, D, H, U)
     assert p["Hp"] % 64 == 0 and p["Hp"] >= H and p["Hp"] - H < 64
     assert p["Dp"] % 64 == 0 and p["Dp"] >= D and p["Dp"] - D < 64
+    assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
+    assert 1 <= p["NRC"] <= 64
+    if p["CP"] > 0:
+        # Cluster path: CP members of 64 columns each, the whole grid resident
+        # at once (one 1024-thread workgroup per CU at most; 256 CUs without a
+        # device), and every member finishes at most one row per thread.
+        assert p["Hp"] >= 256 and p["CP"] == p["Hp"] // 64
+        assert p["NB"] in (1, 2, 4, 8)
+        assert p["NCL"] == -(-B // p["NB"]) and p["ode_workgroups"] == p["NCL"] * p["CP"]
+        assert p["ode_workgroups"] <= 256
+        assert p["KS"] == p["KSB"] and p["KS"] in (8, 16) and p["KS"] >= p["NB"]
+        assert p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 8 == 0
+        assert p["threads"] == p["threads_bwd"] == 64 * p["KS"] <= 1024
+        assert not p["fuse"] and 1 <= p["NCH"] <= 64
+        return
     assert p["NB"] in (1, 2, 4, 8, 16)
     assert p["KS"] >= 1 and p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 4 == 0
     assert p["threads"] == p["Hp"] * p["KS"] <= _max_threads(p["NB"])
@@ -143,8 +158,6 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     # rows finished per thread fit the kernel's compile-time per-row registers
     owned = p["NB"] if p["NB"] <= 2 else p["NB"] // 4
     assert -(-p["NB"] // p["KS"]) <= owned and -(-p["NB"] // p["KSB"]) <= owned
-    assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
-    assert 1 <= p["NRC"] <= 64
     if p["fuse"]:
         # one partial per chain workgroup; operands and accumulators in registers
         assert p["RCB"] in (4, 8, 16) and p["NCH"] == p["ode_workgroups"]
@@ -152,6 +165,16 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     else:
         assert 1 <= p["NCH"] <= 64
     assert p["ode_workgroups"] * p["NB"] >= B > (p["ode_workgroups"] - 1) * p["NB"] or B == 0
+
+
+def test_cluster_path_is_planned_for_the_large_configurations(capi):
+    """C3 and C4 run as clusters that fill the 256 CUs with 4 rows per member."""
+    c3 = capi.plan(256, 64, 256, 256, 6)
+    assert (c3["CP"], c3["NB"], c3["NCL"], c3["RC"]) == (4, 4, 64, 16)
+    c4 = capi.plan(128, 32, 512, 512, 6)
+    assert (c4["CP"], c4["NB"], c4["NCL"], c4["RC"]) == (8, 4, 32, 32)
+    assert capi.plan(24, 8, 128, 64, 6)["CP"] == 0      # C1: one workgroup per row
+    assert capi.plan(4096, 4, 64, 64, 6)["CP"] == 0     # C5
 
 
 def _ext_path():

@@ -135,6 +135,65 @@ def test_backward_matches_oracle(shape):
     assert_grads_close(got, ref, f"backward {shape}")
 
 
+# Cluster path (H > 192): shapes chosen so the plan covers every cluster size
+# class, 1-8 rows per cluster, ragged last clusters and padded columns.
+CLUSTER_SHAPES = [  # (B, T, D, H, expected CP, expected NB)
+    (70, 2, 8, 200, 4, 2),     # Hp 256, register-resident operands
+    (150, 2, 8, 256, 4, 4),
+    (300, 1, 4, 256, 4, 8),
+    (33, 2, 8, 320, 5, 1),     # Hp 320: KS 8, operands streamed
+    (45, 1, 8, 512, 8, 2),
+    (100, 1, 4, 512, 8, 4),
+    (20, 1, 4, 1000, 16, 2),   # Hp 1024
+]
+
+
+@pytest.mark.parametrize("shape", CLUSTER_SHAPES, ids=lambda s: "B%dT%dD%dH%d" % s[:4])
+def test_cluster_path_forward_matches_oracle(shape):
+    B, T, D, H, cp, nb = shape
+    plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
+    assert (plan["CP"], plan["NB"]) == (cp, nb), plan
+    args = boundary(B, T, D, H, seed=B + H)
+    _, (out, h) = gpu_forward(args)
+    ref_out, ref_h = oracle_forward(args)
+    e_out = (out.cpu().double() - ref_out).abs().max().item()
+    e_h = (h.cpu().double() - ref_h).abs().max().item()
+    print(f"cluster forward {shape}: max|out err|={e_out:.2e} max|h err|={e_h:.2e}", flush=True)
+    assert torch.isfinite(out).all() and torch.isfinite(h).all()
+    assert e_out <= 1e-3 and e_h <= 1e-3
+    assert torch.equal(out[:, -1].cpu(), h.cpu())
+
+
+@pytest.mark.parametrize("shape", [CLUSTER_SHAPES[0], CLUSTER_SHAPES[3], CLUSTER_SHAPES[4],
+                                   CLUSTER_SHAPES[6]], ids=lambda s: "B%dT%dD%dH%d" % s[:4])
+def test_cluster_path_backward_matches_oracle(shape):
+    B, T, D, H, _, _ = shape
+    args = boundary(B, T, D, H, seed=3 * B + H)
+    dev_args, (out, h, saved) = gpu_forward(args, save=True)
+    g = torch.Generator().manual_seed(B + 5 * H)
+    g_out = torch.randn(B, T, H, generator=g)
+    g_h = torch.randn(B, H, generator=g)
+    got = gpu_backward(dev_args, saved, g_out.to(DEV), g_h.to(DEV))
+    ref = oracle_grads(args, g_out, g_h)
+    assert_grads_close(got, ref, f"cluster backward {shape}")
+
+
+def test_cluster_path_is_bitwise_reproducible():
+    """The exchange carries values unchanged and every sum has a fixed order."""
+    B, T, D, H = 150, 2, 8, 256
+    args = boundary(B, T, D, H, seed=11)
+    g = torch.Generator().manual_seed(12)
+    g_out = torch.randn(B, T, H, generator=g).to(DEV)
+    runs = []
+    for _ in range(3):
+        dev_args, (out, h, saved) = gpu_forward(args, save=True)
+        grads = gpu_backward(dev_args, saved, g_out, None)
+        runs.append([out.cpu(), h.cpu()] + grads)
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            assert torch.equal(a, b)
+
+
 def test_backward_expanded_grad_and_no_grad_state():
     """loss = out.sum() hands an expanded (stride-0) gradient and no dL/dh."""
     B, T, D, H = 4, 5, 12, 20
