@@ -1668,8 +1668,8 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Cluster path: grid NCL * CP, 64 * KS threads; RC = 16 keeps the operands
-// in registers, otherwise they stream (RC is a multiple of 8).
+// Cluster path: grid NCL * CP, 64 * KS threads. The forward keeps its operands
+// in registers when RC = 16, otherwise they stream (RC is a multiple of 8).
 size_t fwd_cl_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * 64 * 8;
 }
@@ -1699,10 +1699,9 @@ template <int NB>
 hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
   const dim3 grid(p.NCL * p.CP), block(64 * p.KSB);
   const size_t lds = bwd_cl_lds_bytes(p);
-  if (p.RCB == 16)
-    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
-  else
-    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
+  // The chain streams its operands even when RC = 16: its register-resident
+  // form spills at 1024 threads and measured slower.
+  hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
   return hipGetLastError();
 }
 
