@@ -55,7 +55,11 @@ def n_syn(c):
 
 
 def kernel_flops(c):
-    """Algorithmic FLOP per launch of each kernel (measurement)."""
+    """Algorithmic FLOP per launch of each kernel, per synapse (evaluation):
+    forward 10 (z 2, sigmoid 4, two products 2, two sums 2), chain 14 per
+    recurrent synapse-unfold (sigmoid recompute 6, sigmoid' 2, delta 4, dv 2),
+    8 for the four recurrent parameter sums, 22 per sensory synapse backward.
+    Per-neuron, LayerNorm and finalize work is not counted."""
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
     sens = c["B"] * c["T"] * c["D"] * c["H"]
     return {
@@ -65,6 +69,7 @@ def kernel_flops(c):
         "ltc_rec_grad": 8 * rec,
         "ltc_sens_bwd": 22 * sens,
         "ltc_prep": 0,
+        "ltc_ln_bwd": 0,
         "ltc_finalize": 0,
     }
 

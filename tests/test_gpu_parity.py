@@ -194,6 +194,42 @@ def test_cluster_path_is_bitwise_reproducible():
             assert torch.equal(a, b)
 
 
+def test_cluster_path_graph_replay_matches_eager():
+    """Cluster launches (exchange clear + persistent kernel) are ordinary kernel
+    launches, so they capture into a HIP graph; replays, with eager work between
+    them, must reproduce the eager results bit for bit."""
+    B, T, D, H = 40, 2, 8, 256
+    args = boundary(B, T, D, H, seed=21)
+    dev_args = [a.to(DEV) for a in args]
+    mod = ltc_cuda._cuda_module
+    g_out = torch.randn(B, T, H, generator=torch.Generator().manual_seed(22)).to(DEV)
+    assert mod.capi.plan(B, T, D, H, 6)["CP"] == 4
+
+    def step():
+        out, h, saved = mod.ltc_full_forward(*dev_args, 6, EPS, True)
+        grads = mod.ltc_full_backward(*dev_args, saved, g_out, None, 6, EPS, False)
+        return [out, h] + list(grads)
+
+    eager = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(captured, eager):
+            assert torch.equal(a, b)
+        step()
+        torch.cuda.synchronize()
+
+
 def test_backward_expanded_grad_and_no_grad_state():
     """loss = out.sum() hands an expanded (stride-0) gradient and no dL/dh."""
     B, T, D, H = 4, 5, 12, 20
