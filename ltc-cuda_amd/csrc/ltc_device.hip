@@ -75,6 +75,48 @@ __device__ __forceinline__ V ks_sum(const V* base, int stride, int KS) {
   return acc;
 }
 
+// Operand images read through a buffer resource: the wave-uniform row offset
+// is the scalar offset and the lane's column the vector offset, so no
+// per-load address arithmetic runs on the VALU. Reads past `bytes` return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t image_rsrc(const float4* base, long long bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float4*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ float4 image_load(__amdgpu_buffer_rsrc_t r, int lane_bytes,
+                                             int row_bytes) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes,
+                                                                           row_bytes, 0));
+}
+
+// Streams operand rows [r0, r0 + RC) of one image column (RC a multiple of 8)
+// through a double buffer of four rows, calling f(operand, row) for each row.
+// r0 must be wave-uniform. The prefetch past the chunk reads the next chunk's
+// rows, or zeros past the image.
+template <class F>
+__device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_bytes, int r0,
+                                            int RC, int Hp, F&& f) {
+  const int rowb = Hp * 16;
+  const int sb = r0 * rowb;
+  float4 pa[4], pb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + q * rowb);
+  for (int rr = 0; rr < RC; rr += 8) {
+    const int s0 = sb + rr * rowb;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pb[q] = image_load(rs, lane_bytes, s0 + (4 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f(pa[q], r0 + rr + q);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, s0 + (8 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f(pb[q], r0 + rr + 4 + q);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Parameter images (one launch, flat index space over three segments).
 // ---------------------------------------------------------------------------
@@ -92,7 +134,9 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
       v = make_float4(-S * kLog2e, S * M * kLog2e, rp.w_erev[e], rp.w_pos[e]);
     }
     pp.recF[tid] = v;
-    if (bwd) pp.recB[(long long)j * Hp + i] = v;
+    // bwd == 2: the chain's image carries S'*WE and S'*WP (folded; see
+    // bwd_synapse_folded); bwd == 1 keeps WE, WP for the fused chain.
+    if (bwd) pp.recB[(long long)j * Hp + i] = bwd == 2 ? make_float4(v.x, v.y, v.x * v.z, v.x * v.w) : v;
     return;
   }
   tid -= nrec;
@@ -246,7 +290,9 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp]
   float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][Hp]
   const int tid = threadIdx.x;
-  const int ks = tid / Hp, o = tid - ks * Hp;
+  // Hp is a multiple of 64, so ks is uniform across each wave.
+  const int ks = __builtin_amdgcn_readfirstlane(tid / Hp), o = tid - ks * Hp;
+  const __amdgpu_buffer_rsrc_t rsF = image_rsrc(k.recF, (long long)Hp * Hp * 16);
   const int b0 = blockIdx.x * NB;
   const int r0 = ks * RC;
 
@@ -290,28 +336,10 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
 #pragma unroll
         for (int rr = 0; rr < RCP; ++rr) fwd_synapse<NB>(preg[rr], vs, Hp, r0 + rr, na, qa);
       } else {
-        // Operands stream from L2: the next four are requested while the
-        // current four are evaluated (RC is a multiple of 8 here).
-        const float4* pc = k.recF + (long long)r0 * Hp + o;
-        float4 pa[4], pb[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp];
-        for (int rr = 0; rr < RC; rr += 8) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) pb[q] = pc[(long long)(rr + 4 + q) * Hp];
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pa[q], vs, Hp, r0 + rr + q, na, qa);
-          __builtin_amdgcn_sched_barrier(0);
-          if (rr + 8 < RC) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)(rr + 8 + q) * Hp];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pb[q], vs, Hp, r0 + rr + 4 + q, na, qa);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        // Operands stream from L2, the next four requested while the current
+        // four are evaluated.
+        stream_rows(rsF, o * 16, r0, RC, Hp,
+                    [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
@@ -403,6 +431,20 @@ __device__ __forceinline__ void bwd_synapse(const float4 p, const float2* ab, in
   }
 }
 
+// Chain synapse with the folded image {S', c', S'*WE, S'*WP}: the S' factor of
+// dL/dv_i rides in the image, so each row costs one multiply less.
+template <int NB>
+__device__ __forceinline__ void bwd_synapse_folded(const float4 p, const float2* ab, int Hp, int r,
+                                                   const float* vi, float* acc) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float2 c = ab[b * Hp + r];
+    const float a = gate(fmaf(p.x, vi[b], p.y));
+    const float a2 = fmaf(-a, a, a);
+    acc[b] = fmaf(fmaf(c.x, p.z, c.y * p.w), a2, acc[b]);
+  }
+}
+
 // Operands of unfold n for the synapse phase (all rows, column o) and for the
 // rows this thread finishes (den, v^k, v^{k+1}).
 template <int NB, int MO>
@@ -450,7 +492,8 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][Hp]
   const int tid = threadIdx.x;
-  const int ks = tid / Hp, o = tid - ks * Hp;
+  const int ks = __builtin_amdgcn_readfirstlane(tid / Hp), o = tid - ks * Hp;
+  const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
   const int b0 = blockIdx.x * NB;
   const int r0 = ks * RC;
   const float C = k.neuron[o];
@@ -528,35 +571,13 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
         for (int rr = 0; rr < RCP; ++rr)
           bwd_synapse<NB, true>(preg[rr], ab, Hp, r0 + rr, cvi, acc, gacc[rr]);
       } else if constexpr (RCP > 0) {
-        float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int rr = 0; rr < RCP; ++rr)
-          bwd_synapse<NB, false>(preg[rr], ab, Hp, r0 + rr, cvi, acc, unused);
+        for (int rr = 0; rr < RCP; ++rr) bwd_synapse_folded<NB>(preg[rr], ab, Hp, r0 + rr, cvi, acc);
       } else {
-        // Streamed operands, double-buffered four at a time (RC % 8 == 0).
-        float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4* pc = k.recB + (long long)r0 * Hp + o;
-        float4 pa[4], pb[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp];
-        for (int rr = 0; rr < RC; rr += 8) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) pb[q] = pc[(long long)(rr + 4 + q) * Hp];
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            bwd_synapse<NB, false>(pa[q], ab, Hp, r0 + rr + q, cvi, acc, unused);
-          __builtin_amdgcn_sched_barrier(0);
-          if (rr + 8 < RC) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)(rr + 8 + q) * Hp];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            bwd_synapse<NB, false>(pb[q], ab, Hp, r0 + rr + 4 + q, cvi, acc, unused);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        // Streamed (folded) operands, double-buffered four at a time.
+        stream_rows(rsB, o * 16, r0, RC, Hp, [&](const float4 p, int r) {
+          bwd_synapse_folded<NB>(p, ab, Hp, r, cvi, acc);
+        });
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = acc[b];
@@ -957,7 +978,9 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
       v = make_float4(-S * kLog2e, S * M * kLog2e, wp * lp.erev[e], wp);
     }
     pp.recF[tid] = v;
-    if (bwd) pp.recB[(long long)j * Hp + i] = v;
+    // bwd == 2: the chain's image carries S'*WE and S'*WP (folded; see
+    // bwd_synapse_folded); bwd == 1 keeps WE, WP for the fused chain.
+    if (bwd) pp.recB[(long long)j * Hp + i] = bwd == 2 ? make_float4(v.x, v.y, v.x * v.z, v.x * v.w) : v;
     return;
   }
   tid -= nrec;
@@ -1269,6 +1292,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   const int b0 = cl * NB;
   const int r0 = ks * RC;
   const bool owner = ks < NB;  // finishes row ks of column c (the plan keeps KS >= NB)
+  const __amdgpu_buffer_rsrc_t rsF = image_rsrc(k.recF, (long long)Hp * Hp * 16);
   const int bo = ks;
   const bool live = owner && b0 + bo < B;
   unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
@@ -1309,28 +1333,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
 #pragma unroll
         for (int rr = 0; rr < RCP; ++rr) fwd_synapse<NB>(preg[rr], vs, Hp, r0 + rr, na, qa);
       } else {
-        // Streamed operands, double-buffered four rows at a time. The wave's
-        // row offset is uniform (scalar base address); the prefetch past the
-        // chunk's end reads the next chunk or the zero slack rows.
-        const float4* pc = k.recF + (long long)r0 * Hp;
-        float4 pa[4], pb[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp + c];
-        for (int rr = 0; rr < RC; rr += 8) {
-          const float4* pr = pc + (long long)rr * Hp;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) pb[q] = pr[(long long)(4 + q) * Hp + c];
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pa[q], vs, Hp, r0 + rr + q, na, qa);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) pa[q] = pr[(long long)(8 + q) * Hp + c];
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) fwd_synapse<NB>(pb[q], vs, Hp, r0 + rr + 4 + q, na, qa);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        stream_rows(rsF, c * 16, r0, RC, Hp,
+                    [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = make_float2(na[b], qa[b]);
@@ -1415,6 +1419,7 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
   const int r0 = ks * RC;
   const bool owner = ks < NB;
   const int bo = ks;
+  const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
   const bool live = owner && b0 + bo < B;
   unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
   const int nwords = (CP - 1) * PER;
@@ -1500,33 +1505,13 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-    float4 unused = make_float4(0.f, 0.f, 0.f, 0.f);
     if constexpr (RCP > 0) {
 #pragma unroll
-      for (int rr = 0; rr < RCP; ++rr)
-        bwd_synapse<NB, false>(preg[rr], ab, Hp, r0 + rr, cvi, acc, unused);
+      for (int rr = 0; rr < RCP; ++rr) bwd_synapse_folded<NB>(preg[rr], ab, Hp, r0 + rr, cvi, acc);
     } else {
-      const float4* pc = k.recB + (long long)r0 * Hp;
-      float4 pa[4], pb[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) pa[q] = pc[(long long)q * Hp + c];
-      for (int rr = 0; rr < RC; rr += 8) {
-        const float4* pr = pc + (long long)rr * Hp;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pb[q] = pr[(long long)(4 + q) * Hp + c];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          bwd_synapse<NB, false>(pa[q], ab, Hp, r0 + rr + q, cvi, acc, unused);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) pa[q] = pr[(long long)(8 + q) * Hp + c];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          bwd_synapse<NB, false>(pb[q], ab, Hp, r0 + rr + 4 + q, cvi, acc, unused);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      stream_rows(rsB, c * 16, r0, RC, Hp, [&](const float4 p, int r) {
+        bwd_synapse_folded<NB>(p, ab, Hp, r, cvi, acc);
+      });
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = acc[b];
@@ -1712,7 +1697,7 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(prep_kernel, dim3(blocks), dim3(256), 0, s, rp, pp, p.H, p.D, p.Hp, p.Dp,
-                     bwd ? 1 : 0);
+                     bwd ? (p.FUSE ? 1 : 2) : 0);
   return hipGetLastError();
 }
 
@@ -1841,7 +1826,7 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   const int nln = ln ? (BT + 3) / 4 : 0;
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   hipLaunchKernelGGL(prep_leaf_kernel, dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, p.D,
-                     p.Hp, p.Dp, bwd ? 1 : 0, nprep, lb, p.T, BT);
+                     p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, nprep, lb, p.T, BT);
   return hipGetLastError();
 }
 
