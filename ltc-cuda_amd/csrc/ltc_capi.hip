@@ -90,8 +90,12 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
   p.Dp = (int)round_up(D > 0 ? D : 1, 64);
   // Rows per persistent workgroup: keep at least 256 workgroups (one per CU)
   // while B allows, and reuse each synapse operand NB times otherwise.
+  // At Hp = 64 the operands of every thread stay in registers, so reuse over
+  // more rows buys nothing, while more workgroups per CU hide latency
+  // (measured: NB = 4 beats 8 and 16 for both ODE kernels at large B).
   p.NB = 1;
   for (int nb : {16, 8, 4, 2}) {
+    if (p.Hp <= 64 && nb > 4) continue;
     if ((B + nb - 1) / nb >= 256) {
       p.NB = nb;
       break;
@@ -235,6 +239,7 @@ struct BwdWs {
   float* spart;
   float* dxpart;
   ltc::ClusterBuf cb;
+  ltc::PresumBuf ps;
 };
 
 BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
@@ -251,6 +256,8 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
   w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
   w.cb = carve_cluster(p, c);
+  w.ps.rec = c.take<float>((long long)ltc::presum_parts(p.NCH) * 4 * p.Hp * p.Hp);
+  w.ps.neuron = c.take<float>((long long)ltc::presum_parts(p.B) * 3 * p.Hp);
   return w;
 }
 
@@ -549,7 +556,7 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
   });
   if (e != hipSuccess) return hip_fail("sensory backward launch", e);
   e = timed(ltc::K_FINALIZE, s, [&] {
-    return ltc::launch_finalize(p, rp, w.rpart, w.spart, w.dxpart, w.npart, go, s);
+    return ltc::launch_finalize(p, rp, w.rpart, w.spart, w.dxpart, w.npart, w.ps, go, s);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
   return LTC_OK;
@@ -767,7 +774,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
             [&] { return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s); });
   if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
   e = timed(ltc::K_FINALIZE, s, [&] {
-    return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, lg, s);
+    return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
   return LTC_OK;

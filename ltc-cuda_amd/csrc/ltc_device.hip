@@ -826,7 +826,7 @@ struct FinK {
   const float* dxpart;
   const float* npart;
   GradOut g;
-  int B, D, H, Hp, Dp, NCH, NRC, HB, BT;
+  int B, D, H, Hp, Dp, NCH, NRC, HB, BT;  // B, NCH: counts of neuron / recurrent partials
 };
 
 // Sum of n strided partials with 8 loads in flight per round.
@@ -842,6 +842,18 @@ __device__ __forceinline__ float sum_partials(const float* p, long long stride, 
   }
   for (; z < n; ++z) acc += p[(long long)z * stride];
   return acc;
+}
+
+// First pass of a long partial sum: dst[r][n] = sum of src rows
+// [r*rpb, min(M, (r+1)*rpb)) at column n (row stride `stride`), in row order.
+__global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ src,
+                                                       long long stride, int M, long long N,
+                                                       int rpb, float* __restrict__ dst) {
+  const long long n = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const int r0 = (int)blockIdx.y * rpb;
+  const int cnt = M - r0 < rpb ? M - r0 : rpb;
+  dst[(long long)blockIdx.y * N + n] = sum_partials(src + (long long)r0 * stride + n, stride, cnt);
 }
 
 __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
@@ -1113,7 +1125,7 @@ struct FinLeafK {
   const float* npart;
   const float* lnpart;
   LeafGrads g;
-  int B, D, H, Hp, Dp, NCH, NRC, NLN;
+  int B, D, H, Hp, Dp, NCH, NRC, NLN;  // B, NCH: counts of neuron / recurrent partials
 };
 
 __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
@@ -1806,12 +1818,45 @@ hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Pre
   return hipGetLastError();
 }
 
+// Applies the first pass to the recurrent and neuron partials when they are
+// long; returns the partial pointers and counts the finalize kernel sums.
+struct Partials {
+  const float* rpart;
+  int nrec;
+  const float* npart;
+  int nneuron;
+};
+
+hipError_t presum(const Plan& p, const float* rpart, const float* npart, const PresumBuf& ps,
+                  hipStream_t s, Partials& out) {
+  out = Partials{rpart, p.NCH, npart, p.B};
+  auto pass = [&](const float* src, int M, long long N, float* dst) {
+    const int parts = presum_parts(M);
+    const int rpb = (M + parts - 1) / parts;
+    hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
+                       dim3(256), 0, s, src, N, M, N, rpb, dst);
+    return parts;
+  };
+  if (presum_parts(p.NCH) > 0) {
+    out.nrec = pass(rpart, p.NCH, 4LL * p.Hp * p.Hp, ps.rec);
+    out.rpart = ps.rec;
+  }
+  if (presum_parts(p.B) > 0) {
+    out.nneuron = pass(npart, p.B, 3LL * p.Hp, ps.neuron);
+    out.npart = ps.neuron;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
-                           const GradOut& g, hipStream_t s) {
+                           const PresumBuf& ps, const GradOut& g, hipStream_t s) {
   const int BT = p.B * p.T;
-  FinK a{rp, rpart, spart, dxpart, npart, g, p.B, p.D, p.H, p.Hp, p.Dp, p.NCH, p.NRC,
-         p.Hp / 32, BT};
+  Partials pt;
+  hipError_t e = presum(p, rpart, npart, ps, s, pt);
+  if (e != hipSuccess) return e;
+  FinK a{rp, pt.rpart, spart, dxpart, pt.npart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp, pt.nrec,
+         p.NRC, p.Hp / 32, BT};
   const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + (long long)BT * p.D;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
@@ -1841,9 +1886,12 @@ hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
 
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
                                 const float* spart, const float* npart, const float* lnpart,
-                                const LeafGrads& g, hipStream_t s) {
-  FinLeafK a{lp, rpart, spart, npart, lnpart, g, p.B, p.D, p.H, p.Hp, p.Dp, p.NCH, p.NRC,
-             ln_bwd_blocks(p)};
+                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s) {
+  Partials pt;
+  hipError_t e = presum(p, rpart, npart, ps, s, pt);
+  if (e != hipSuccess) return e;
+  FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
+             pt.nrec, p.NRC, ln_bwd_blocks(p)};
   const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);

@@ -175,9 +175,23 @@ struct GradOut {
   float* gleak;
   float* vleak;
 };
+// Long partial sums (the per-row neuron partials over B, the recurrent
+// gradient partials over NCH) get a parallel first pass into at most 64
+// partials each: presum_parts(M) of them, or 0 when M is small enough to sum
+// directly. The scratch buffers hold presum_parts(NCH) * 4*Hp*Hp and
+// presum_parts(B) * 3*Hp floats.
+inline int presum_parts(int m) {
+  if (m <= 64) return 0;
+  const int rpb = (m + 63) / 64 > 32 ? (m + 63) / 64 : 32;
+  return (m + rpb - 1) / rpb;
+}
+struct PresumBuf {
+  float* rec;     // presum_parts(NCH) x 4*Hp*Hp
+  float* neuron;  // presum_parts(B) x 3*Hp
+};
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
-                           const GradOut& g, hipStream_t s);
+                           const PresumBuf& ps, const GradOut& g, hipStream_t s);
 
 // Module path backward.
 struct LeafGrads {
@@ -205,6 +219,6 @@ hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
                          const float* dxpart, float* gx, float* lnpart, hipStream_t s);
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
                                 const float* spart, const float* npart, const float* lnpart,
-                                const LeafGrads& g, hipStream_t s);
+                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s);
 
 }  // namespace ltc
