@@ -258,6 +258,7 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   w.cb = carve_cluster(p, c);
   w.ps.rec = c.take<float>((long long)ltc::presum_parts(p.NCH) * 4 * p.Hp * p.Hp);
   w.ps.neuron = c.take<float>((long long)ltc::presum_parts(p.B) * 3 * p.Hp);
+  w.ps.ln = c.take<float>((long long)ltc::presum_parts(ltc::ln_bwd_blocks(p)) * 4 * p.Dp);
   return w;
 }
 

@@ -1025,24 +1025,24 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
   }
 }
 
-// LayerNorm + affine backward. Block 256 = 4 waves, kLnRows rows per block,
-// each wave takes rows w, w+4, ... With gxa = dL/dxa (sum of the h-block
-// partials), xh = (x - mean)*rstd, gxn = gxa*input_w, gxh = gxn*ln_w:
+// LayerNorm + affine backward. Block 256 = 4 waves, `rpb` rows per block (4
+// or 16), each wave takes rows w, w+4, ...; CPL column slots per lane (D <=
+// 64*CPL). With gxa = dL/dxa (sum of the h-block partials),
+// xh = (x - mean)*rstd, gxn = gxa*input_w, gxh = gxn*ln_w:
 //   dx = rstd*(gxh - mean_d(gxh) - xh*mean_d(gxh*xh))
 // and the column sums dinput_w = sum gxa*xn, dinput_b = sum gxa,
 // dln_w = sum gxn*xh, dln_b = sum gxn are accumulated per lane, combined over
 // the 4 waves in LDS in a fixed order and written as one partial per block.
-constexpr int kLnRows = 16;
-
+template <int CPL>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, const float* dxpart,
                                                      float* gx, float* lnpart, int T, int D,
-                                                     int Dp, int BT, int HB) {
-  __shared__ float col[4][kModuleMaxD];
+                                                     int Dp, int BT, int HB, int rpb) {
+  __shared__ float col[4][64 * CPL];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  float cw[kLnPerLane], cb[kLnPerLane], cl[kLnPerLane], cbl[kLnPerLane];
-  float iw[kLnPerLane], lw[kLnPerLane], lb[kLnPerLane];
+  float cw[CPL], cb[CPL], cl[CPL], cbl[CPL];
+  float iw[CPL], lw[CPL], lb[CPL];
 #pragma unroll
-  for (int c = 0; c < kLnPerLane; ++c) {
+  for (int c = 0; c < CPL; ++c) {
     const int d = lane + 64 * c;
     cw[c] = cb[c] = cl[c] = cbl[c] = 0.f;
     iw[c] = d < D ? lp.input_w[d] : 0.f;
@@ -1050,16 +1050,16 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, co
     lb[c] = d < D ? lp.ln_b[d] : 0.f;
   }
   const long long hstride = (long long)BT * Dp;
-  for (int i = 0; i < kLnRows / 4; ++i) {
-    const int row = blockIdx.x * kLnRows + w + 4 * i;
+  for (int i = w; i < rpb; i += 4) {
+    const int row = blockIdx.x * rpb + i;
     if (row >= BT) break;
     const int b = row / T, t = row - b * T;
     const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
     const float mean = ln.stats[2LL * row], rstd = ln.stats[2LL * row + 1];
-    float xh[kLnPerLane], gxh[kLnPerLane];
+    float xh[CPL], gxh[CPL];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
-    for (int c = 0; c < kLnPerLane; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       const int d = lane + 64 * c;
       xh[c] = gxh[c] = 0.f;
       if (d < D) {
@@ -1081,7 +1081,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, co
     const float m1 = wave_sum(s1) / (float)D, m2 = wave_sum(s2) / (float)D;
     float* go = gx + (long long)row * D;
 #pragma unroll
-    for (int c = 0; c < kLnPerLane; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       const int d = lane + 64 * c;
       if (d < D) go[d] = rstd * (gxh[c] - m1 - xh[c] * m2);
     }
@@ -1090,7 +1090,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, co
   for (int wv = 0; wv < 4; ++wv) {
     if (w == wv) {
 #pragma unroll
-      for (int c = 0; c < kLnPerLane; ++c) {
+      for (int c = 0; c < CPL; ++c) {
         const int d = lane + 64 * c;
         if (d < D) {
           if (wv == 0) {
@@ -1875,12 +1875,26 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   return hipGetLastError();
 }
 
-int ln_bwd_blocks(const Plan& p) { return (p.B * p.T + kLnRows - 1) / kLnRows; }
+// Rows per LayerNorm-backward block: one per wave while B*T is small (more
+// blocks in flight), four per wave otherwise (fewer column partials).
+int ln_rows_per_block(const Plan& p) { return (long long)p.B * p.T >= 4096 ? 16 : 4; }
+
+int ln_bwd_blocks(const Plan& p) {
+  const int rpb = ln_rows_per_block(p);
+  return (p.B * p.T + rpb - 1) / rpb;
+}
 
 hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
                          const float* dxpart, float* gx, float* lnpart, hipStream_t s) {
-  hipLaunchKernelGGL(ln_bwd_kernel, dim3(ln_bwd_blocks(p)), dim3(256), 0, s, lp, ln, dxpart, gx,
-                     lnpart, p.T, p.D, p.Dp, p.B * p.T, p.Hp / 32);
+  const dim3 grid(ln_bwd_blocks(p)), block(256);
+  const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = p.Hp / 32;
+#define LTC_LNB(C) hipLaunchKernelGGL((ln_bwd_kernel<C>), grid, block, 0, s, lp, ln, dxpart, gx, lnpart, p.T, p.D, p.Dp, BT, HB, rpb)
+  if (p.D <= 64) LTC_LNB(1);
+  else if (p.D <= 128) LTC_LNB(2);
+  else if (p.D <= 256) LTC_LNB(4);
+  else if (p.D <= 512) LTC_LNB(8);
+  else LTC_LNB(16);
+#undef LTC_LNB
   return hipGetLastError();
 }
 
@@ -1890,8 +1904,19 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
   Partials pt;
   hipError_t e = presum(p, rpart, npart, ps, s, pt);
   if (e != hipSuccess) return e;
+  int nln = ln_bwd_blocks(p);
+  if (presum_parts(nln) > 0) {
+    const int parts = presum_parts(nln), rpb = (nln + parts - 1) / parts;
+    const long long N = 4LL * p.Dp;
+    hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
+                       dim3(256), 0, s, lnpart, N, nln, N, rpb, ps.ln);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    lnpart = ps.ln;
+    nln = parts;
+  }
   FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
-             pt.nrec, p.NRC, ln_bwd_blocks(p)};
+             pt.nrec, p.NRC, nln};
   const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);

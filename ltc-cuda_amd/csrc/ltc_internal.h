@@ -188,6 +188,7 @@ inline int presum_parts(int m) {
 struct PresumBuf {
   float* rec;     // presum_parts(NCH) x 4*Hp*Hp
   float* neuron;  // presum_parts(B) x 3*Hp
+  float* ln;      // module path: presum_parts(ln_bwd_blocks) x 4*Dp
 };
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
