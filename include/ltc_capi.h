@@ -191,10 +191,12 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
  * and threads (the fields before them describe the forward kernel), then CP
  * and NCL: with CP > 0 the ODE kernels run as NCL clusters of CP workgroups
  * that each own 64 columns of NB rows (threads and LDS fields then describe
- * one cluster member). Returns the number of values written, or -1 for
- * invalid sizes. The plan depends on the current device's CU count.
+ * one cluster member), then the chain kernel's cluster size, rows per
+ * cluster and workgroups (its clusters may differ from the forward's when
+ * its parameter gradients are fused). Returns the number of values written,
+ * or -1 for invalid sizes. The plan depends on the current device's CU count.
  */
-#define LTC_PLAN_FIELDS 17
+#define LTC_PLAN_FIELDS 20
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

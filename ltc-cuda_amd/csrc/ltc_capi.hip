@@ -52,6 +52,26 @@ int device_cus() {
 // Dynamic LDS of a cluster member, leaving room for its static flag word.
 constexpr long long kClusterLds = 60 * 1024;
 
+// Hp = 256: the chain runs as clusters of 8 members of 32 columns with 512
+// threads, 16 register-resident synapses per thread and their four gradient
+// sums in registers, which removes the separate parameter-gradient pass.
+void plan_fused_chain(ltc::Plan& p, int ncu) {
+  if (p.Hp != 256) return;
+  const int cp = p.Hp / 32, slots = ncu / cp;
+  for (int nb : {1, 2, 4, 8}) {
+    const int ncl = (p.B + nb - 1) / nb;
+    if (ncl > slots) continue;
+    p.CPB = cp;
+    p.JWB = 32;
+    p.NBB = nb;
+    p.NCLB = ncl;
+    p.KSB = 16;
+    p.RCB = 16;
+    p.FUSE = true;
+    return;
+  }
+}
+
 bool plan_cluster(ltc::Plan& p, int ncu) {
   if (p.Hp < 256 || p.B < 1) return false;
   const int cp = p.Hp / 64;
@@ -70,6 +90,11 @@ bool plan_cluster(ltc::Plan& p, int ncu) {
       p.KS = p.KSB = ks;
       p.RC = p.RCB = p.Hp / ks;
       p.FUSE = false;
+      p.CPB = cp;
+      p.JWB = 64;
+      p.NBB = nb;
+      p.NCLB = ncl;
+      plan_fused_chain(p, ncu);
       return true;
     }
   }
@@ -152,11 +177,14 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
   // writes one partial per workgroup.
   p.FUSE = ltc::ode_fuse_ok(p.NB, p.RCB);
   p.CP = p.NCL = 0;
+  p.CPB = p.NBB = p.NCLB = 0;
+  p.JWB = 64;
   plan_cluster(p, ncu);
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
   if (p.FUSE) {
-    p.NCH = (B + p.NB - 1) / p.NB;
+    // One partial per chain workgroup, or per chain cluster.
+    p.NCH = p.CP > 0 ? p.NCLB : (B + p.NB - 1) / p.NB;
     if (p.NCH < 1) p.NCH = 1;
   } else {
     const long long bpc = (long long)(p.Hp / 64) * (p.Hp / 32);
@@ -202,10 +230,10 @@ struct Carver {
 // rows past the end.
 long long image_rows(const ltc::Plan& p) { return p.Hp + (p.CP > 0 ? ltc::kImageSlackRows : 0); }
 
-ltc::ClusterBuf carve_cluster(const ltc::Plan& p, Carver& c) {
+ltc::ClusterBuf carve_cluster(const ltc::Plan& p, Carver& c, bool bwd) {
   ltc::ClusterBuf cb{nullptr, nullptr};
   if (p.CP > 0) {
-    cb.xch = c.take<unsigned long long>(ltc::cluster_words(p));
+    cb.xch = c.take<unsigned long long>(bwd ? ltc::cluster_words_bwd(p) : ltc::cluster_words(p));
     cb.status = c.take<int>(1);
   }
   return cb;
@@ -225,7 +253,7 @@ FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
   w.pp.neuron = c.take<float>(3LL * p.Hp);
   w.sn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.sd = c.take<float>((long long)p.B * p.T * p.Hp);
-  w.cb = carve_cluster(p, c);
+  w.cb = carve_cluster(p, c, false);
   return w;
 }
 
@@ -255,7 +283,7 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   w.rpart = c.take<float>((long long)p.NCH * 4 * p.Hp * p.Hp);
   w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
   w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
-  w.cb = carve_cluster(p, c);
+  w.cb = carve_cluster(p, c, true);
   w.ps.rec = c.take<float>((long long)ltc::presum_parts(p.NCH) * 4 * p.Hp * p.Hp);
   w.ps.neuron = c.take<float>((long long)ltc::presum_parts(p.B) * 3 * p.Hp);
   w.ps.ln = c.take<float>((long long)ltc::presum_parts(ltc::ln_bwd_blocks(p)) * 4 * p.Dp);
@@ -784,14 +812,17 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n) {
   if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || !out || n < 0) return -1;
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
-  // Columns each workgroup of the ODE kernels owns: all Hp, or 64 per member.
+  // Columns each workgroup of the ODE kernels owns: all Hp, or one member's.
   const long long cols = p.CP > 0 ? 64 : p.Hp;
+  const long long colsb = p.CP > 0 ? p.JWB : p.Hp;
+  const long long nbb = p.CP > 0 ? p.NBB : p.NB;
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8,
-      (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * cols * 4,
+      nbb * p.Hp * 8 + (long long)p.KSB * nbb * colsb * 4,
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
-      p.FUSE ? 1 : 0, p.KSB, p.RCB, cols * p.KSB, p.CP, p.NCL};
+      p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
+      p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -1393,7 +1393,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
 }
 
 struct BwdCK {
-  const float4* recB;  // [Hp + 8][Hp], 8 zero rows of slack
+  const float4* recB;  // [Hp][Hp] (+ slack rows)
   const float* neuron;
   const float* vsave;
   const float* densave;
@@ -1405,33 +1405,41 @@ struct BwdCK {
   float* dsd;
   float* npart;
   float* gstate;
+  float* rpart;  // FUSE: one recurrent-gradient partial per cluster, [NCL][4][Hp][Hp]
   unsigned long long* xch;
   int* status;
   int B, T, H, Hp, U, KS, RC, CP;
 };
 
-// Cluster chain: member p forms dL/dv_i for its 64 columns i (reduction over
+// Cluster chain: member p forms dL/dv_i for its JW columns i (reduction over
 // every postsynaptic j) and publishes them; alpha_j/beta_j of the other
 // members' columns are then rebuilt from the published dL/dv_j and the saved
 // den_j, v_j, so only one value per (row, column) crosses the cluster.
-template <int NB, int RCP>
-__global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
-  constexpr int PER = NB * kClW;
+// Thread (o, ks): column i = p*JW + o, postsynaptic rows [ks*RC, ks*RC + RC).
+// FUSE (JW = 32, RCP register-resident operands of the unfolded image): the
+// thread also accumulates the four recurrent parameter-gradient sums of its
+// RCP synapses over all rows and unfolds, and writes one partial per cluster,
+// so the separate parameter-gradient pass and its gate evaluation go away.
+template <int NB, int JW, int RCP, bool FUSE>
+__global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) {
+  static_assert(!FUSE || RCP > 0, "the fused chain keeps its operands in registers");
+  constexpr int PER = NB * JW;
   extern __shared__ float4 lds4[];
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
   const int RC = RCP > 0 ? RCP : k.RC;
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
-  float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][64]
+  float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
   const int tid = threadIdx.x, nthr = blockDim.x;
-  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  // With JW = 64 ks is uniform across each wave; with JW = 32 a wave holds two.
+  const int ks = JW == 64 ? __builtin_amdgcn_readfirstlane(tid / JW) : tid / JW;
+  const int o = tid % JW;
   const int p = blockIdx.x % CP, cl = blockIdx.x / CP;
-  const int c = p * kClW + o;
+  const int c = p * JW + o;
   const int b0 = cl * NB;
   const int r0 = ks * RC;
   const bool owner = ks < NB;
   const int bo = ks;
-  const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
   const bool live = owner && b0 + bo < B;
   unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
   const int nwords = (CP - 1) * PER;
@@ -1443,6 +1451,11 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
   if constexpr (RCP > 0) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + c];
+  }
+  float4 gacc[FUSE ? RCP : 1];
+  if constexpr (FUSE) {
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (tid == 0) gave_up = 0;
 
@@ -1465,10 +1478,16 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
       gdir = al * C;
     }
     ab[bo * Hp + c] = make_float2(al, be);
-    if (live) k.absave[(n * B + b0 + bo) * Hp + c] = make_float2(al, be);
+    if (!FUSE && live) k.absave[(n * B + b0 + bo) * Hp + c] = make_float2(al, be);
   };
   auto gout_at = [&](int b, int t, int col) {
     return k.gout[(long long)(b0 + b) * k.gs.b + (long long)t * k.gs.t + (long long)col * k.gs.c];
+  };
+  // Word offset a = q*PER + b*JW + col-in-member of a slot -> (row, column).
+  auto word_rc = [&](int a, int& b, int& col) {
+    const int q = a / PER, r = a - q * PER;
+    b = r / JW;
+    col = q * JW + (r - b * JW);
   };
 
   const long long n_last = (long long)T * U - 1;
@@ -1489,8 +1508,8 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
   // The other members' columns for the last unfold come straight from the
   // output gradients (no exchange needed yet).
   for (int e = tid; e < nwords; e += nthr) {
-    const int a = e + (e / PER >= p ? PER : 0);
-    const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+    int b, col;
+    word_rc(e + (e / PER >= p ? PER : 0), b, col);
     float al = 0.f, be = 0.f;
     if (b0 + b < B && col < H) {
       float gg = gout_at(b, T - 1, col);
@@ -1517,16 +1536,26 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-    if constexpr (RCP > 0) {
+    if constexpr (FUSE) {
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) {
+        bwd_synapse<NB, true>(preg[rr], ab, Hp, r0 + rr, cvi, acc, gacc[rr]);
+        // Pin the accumulators here: otherwise the compiler sinks these sums
+        // past the barrier and keeps every synapse's temporaries alive.
+        asm volatile("" : "+v"(gacc[rr].x), "+v"(gacc[rr].y), "+v"(gacc[rr].z), "+v"(gacc[rr].w));
+      }
+    } else if constexpr (RCP > 0) {
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) bwd_synapse_folded<NB>(preg[rr], ab, Hp, r0 + rr, cvi, acc);
     } else {
-      stream_rows(rsB, c * 16, r0, RC, Hp, [&](const float4 p, int r) {
-        bwd_synapse_folded<NB>(p, ab, Hp, r, cvi, acc);
+      static_assert(FUSE || RCP > 0 || JW == 64, "streamed operands need wave-uniform rows");
+      const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
+      stream_rows(rsB, c * 16, r0, RC, Hp, [&](const float4 pv, int r) {
+        bwd_synapse_folded<NB>(pv, ab, Hp, r, cvi, acc);
       });
     }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = acc[b];
+    for (int b = 0; b < NB; ++b) red[(ks * NB + b) * JW + o] = acc[b];
     // Saved values of unfold n-1, requested now and consumed after the
     // exchange, whose wait covers their latency.
     float nden = 1.f, nvk = 0.f, nvk1 = 0.f;
@@ -1547,7 +1576,7 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
     const unsigned tag = (unsigned)n;
     unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
     if (owner) {
-      const float s = ks_sum(red + bo * kClW + o, NB * kClW, KS);
+      const float s = ks_sum(red + bo * JW + o, NB * JW, KS);
       g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
       if (u == 0 && live) {
         const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
@@ -1557,7 +1586,7 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
       if (u == 0) accA = accB = 0.f;
       if (n > 0) {
         g += gnext;
-        xch_put(slot + p * PER + bo * kClW + o, g, tag);
+        xch_put(slot + p * PER + bo * JW + o, g, tag);
       }
     }
     if (n > 0) {
@@ -1565,7 +1594,8 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
       const bool ok = xch_gather<PER>(
           slot, p, nwords, tid, nthr, tag,
           [&](int x, int a) {
-            const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+            int b, col;
+            word_rc(a, b, col);
             pden[x] = 1.f;
             pvk1[x] = 0.f;
             if (b0 + b < B) {
@@ -1575,7 +1605,8 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
             }
           },
           [&](int x, int a, float gg) {
-            const int q = a / PER, r = a - q * PER, b = r >> 6, col = q * kClW + (r & 63);
+            int b, col;
+            word_rc(a, b, col);
             float al = 0.f, be = 0.f;
             if (b0 + b < B && col < H) {
               const float rden = 1.0f / pden[x];
@@ -1602,6 +1633,19 @@ __global__ __launch_bounds__(1024) void ode_bwd_cl_kernel(BwdCK k) {
     np[0] = pC;
     np[Hp] = pGv;
     np[2 * Hp] = pA;
+  }
+  if constexpr (FUSE) {
+    // This cluster's share of the recurrent parameter gradients for synapses
+    // (i = c, j = r0 + rr), layout [cluster][4][i][j] as rec_grad_kernel's.
+    const long long HH = (long long)Hp * Hp;
+    float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp + r0;
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      out[rr] = gacc[rr].x;
+      out[HH + rr] = gacc[rr].y;
+      out[2 * HH + rr] = gacc[rr].z;
+      out[3 * HH + rr] = gacc[rr].w;
+    }
   }
 }
 
@@ -1671,11 +1715,11 @@ size_t fwd_cl_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * 64 * 8;
 }
 size_t bwd_cl_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KSB * p.NB * 64 * 4;
+  return (size_t)p.NBB * p.Hp * 8 + (size_t)p.KSB * p.NBB * p.JWB * 4;
 }
 
-hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, hipStream_t s) {
-  const long long n = cluster_words(p);
+hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s) {
+  const long long n = bwd ? cluster_words_bwd(p) : cluster_words(p);
   hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      cb.xch, n, cb.status);
   return hipGetLastError();
@@ -1694,11 +1738,17 @@ hipError_t fwd_cl_by_rcp(const Plan& p, const FwdCK& a, hipStream_t s) {
 
 template <int NB>
 hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
-  const dim3 grid(p.NCL * p.CP), block(64 * p.KSB);
+  const dim3 grid(p.NCLB * p.CPB), block(p.JWB * p.KSB);
   const size_t lds = bwd_cl_lds_bytes(p);
-  // The chain streams its operands even when RC = 16: its register-resident
-  // form spills at 1024 threads and measured slower.
-  hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
+  if (p.FUSE) {
+    // 32-column members, 512 threads, 16 register-resident synapses each.
+    if (p.JWB != 32 || p.RCB != 16 || p.KSB != 16) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
+  } else {
+    // Streamed operands (a register-resident form spilled at 1024 threads
+    // and measured slower).
+    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 64, 0, false>), grid, block, lds, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -1750,7 +1800,7 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
                           const float* state0, float eps, float* out, float* hfin,
                           float* vsave, float* densave, const ClusterBuf& cb, hipStream_t s) {
   if (p.CP > 0) {
-    hipError_t e = clear_cluster(p, cb, s);
+    hipError_t e = clear_cluster(p, cb, false, s);
     if (e != hipSuccess) return e;
     FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
             p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, eps};
@@ -1778,11 +1828,11 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           float* npart, float* gstate, float* rpart, const ClusterBuf& cb,
                           hipStream_t s) {
   if (p.CP > 0) {
-    hipError_t e = clear_cluster(p, cb, s);
+    hipError_t e = clear_cluster(p, cb, true, s);
     if (e != hipSuccess) return e;
     BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
-            gstate, cb.xch, cb.status, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, p.CP};
-    switch (p.NB) {
+            gstate, rpart, cb.xch, cb.status, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, p.CPB};
+    switch (p.NBB) {
       case 8: return bwd_cl_by_rcp<8>(p, a, s);
       case 4: return bwd_cl_by_rcp<4>(p, a, s);
       case 2: return bwd_cl_by_rcp<2>(p, a, s);

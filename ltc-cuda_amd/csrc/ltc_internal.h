@@ -52,6 +52,10 @@ struct Plan {
   bool FUSE;       // recurrent parameter gradients accumulated inside the chain kernel
   int CP;          // cluster path: workgroups per cluster (0 = one workgroup per NB rows)
   int NCL;         // cluster path: clusters = ceil(B / NB); grid = NCL * CP
+  // Cluster path, chain kernel: its own geometry (equal to the forward's
+  // unless the chain is fused): CPB members of JWB columns, NBB rows per
+  // cluster, NCLB clusters.
+  int CPB, JWB, NBB, NCLB;
   int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances
@@ -142,8 +146,11 @@ struct ClusterBuf {
   unsigned long long* xch;
   int* status;
 };
-// Exchange words of one cluster launch.
+// Exchange words of one cluster launch (forward / chain).
 inline long long cluster_words(const Plan& p) { return 2LL * p.NCL * p.CP * p.NB * 64; }
+inline long long cluster_words_bwd(const Plan& p) {
+  return 2LL * p.NCLB * p.CPB * p.NBB * p.JWB;
+}
 // Rows of slack after the [Hp][Hp] operand images that the cluster kernels'
 // streamed prefetch may read.
 constexpr int kImageSlackRows = 8;

@@ -145,10 +145,21 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         assert p["NB"] in (1, 2, 4, 8)
         assert p["NCL"] == -(-B // p["NB"]) and p["ode_workgroups"] == p["NCL"] * p["CP"]
         assert p["ode_workgroups"] <= 256
-        assert p["KS"] == p["KSB"] and p["KS"] in (8, 16) and p["KS"] >= p["NB"]
+        assert p["KS"] in (8, 16) and p["KS"] >= p["NB"]
         assert p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 8 == 0
-        assert p["threads"] == p["threads_bwd"] == 64 * p["KS"] <= 1024
-        assert not p["fuse"] and 1 <= p["NCH"] <= 64
+        assert p["threads"] == 64 * p["KS"] <= 1024
+        assert p["ode_workgroups_bwd"] <= 256 and p["NBB"] in (1, 2, 4, 8)
+        assert p["ode_workgroups_bwd"] == p["CPB"] * -(-B // p["NBB"])
+        assert p["KSB"] >= p["NBB"] and p["lds_bwd"] <= 65536
+        if p["fuse"]:
+            # Hp = 256 chain: 8 members of 32 columns, 512 threads, 16
+            # register-resident synapses per thread, one partial per cluster.
+            assert p["Hp"] == 256 and p["CPB"] == 8 and p["KSB"] == 16 and p["RCB"] == 16
+            assert p["threads_bwd"] == 512
+            assert p["NCH"] == p["ode_workgroups_bwd"] // p["CPB"]
+        else:
+            assert (p["CPB"], p["NBB"], p["KSB"], p["RCB"]) == (p["CP"], p["NB"], p["KS"], p["RC"])
+            assert p["threads_bwd"] == 64 * p["KSB"] and 1 <= p["NCH"] <= 64
         return
     assert p["NB"] in (1, 2, 4, 8, 16)
     assert p["KS"] >= 1 and p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 4 == 0
@@ -171,6 +182,7 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     """C3 and C4 run as clusters that fill the 256 CUs with 4 rows per member."""
     c3 = capi.plan(256, 64, 256, 256, 6)
     assert (c3["CP"], c3["NB"], c3["NCL"], c3["RC"]) == (4, 4, 64, 16)
+    assert (c3["fuse"], c3["CPB"], c3["NBB"], c3["NCH"]) == (1, 8, 8, 32)
     c4 = capi.plan(128, 32, 512, 512, 6)
     assert (c4["CP"], c4["NB"], c4["NCL"], c4["RC"]) == (8, 4, 32, 32)
     assert capi.plan(24, 8, 128, 64, 6)["CP"] == 0      # C1: one workgroup per row

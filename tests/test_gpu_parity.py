@@ -138,7 +138,7 @@ def test_backward_matches_oracle(shape):
 # Cluster path (H > 192): shapes chosen so the plan covers every cluster size
 # class, 1-8 rows per cluster, ragged last clusters and padded columns.
 CLUSTER_SHAPES = [  # (B, T, D, H, expected CP, expected NB)
-    (70, 2, 8, 200, 4, 2),     # Hp 256, register-resident operands
+    (70, 2, 8, 200, 4, 2),     # Hp 256, register-resident operands; fused chain
     (150, 2, 8, 256, 4, 4),
     (300, 1, 4, 256, 4, 8),
     (33, 2, 8, 320, 5, 1),     # Hp 320: KS 8, operands streamed
@@ -165,7 +165,9 @@ def test_cluster_path_forward_matches_oracle(shape):
 
 
 @pytest.mark.parametrize("shape", [CLUSTER_SHAPES[0], CLUSTER_SHAPES[3], CLUSTER_SHAPES[4],
-                                   CLUSTER_SHAPES[6]], ids=lambda s: "B%dT%dD%dH%d" % s[:4])
+                                   CLUSTER_SHAPES[6], (9, 2, 8, 256, 4, 1),
+                                   (250, 1, 4, 256, 4, 4)],
+                         ids=lambda s: "B%dT%dD%dH%d" % s[:4])
 def test_cluster_path_backward_matches_oracle(shape):
     B, T, D, H, _, _ = shape
     args = boundary(B, T, D, H, seed=3 * B + H)
