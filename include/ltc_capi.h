@@ -181,6 +181,79 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
                         void* workspace, long long workspace_bytes, void* stream);
 
 /*
+ * Per-step entry points. The reference exports them beside the T-loop
+ * drivers (csrc/ltc_kernels.cu:1308-1311) for a Python-level time loop; its
+ * own Python no longer calls them. Each one runs the same kernels as the
+ * drivers with T = 1. Tensors are contiguous unless strides are given, and
+ * outputs must not alias inputs.
+ */
+
+/* One step's sensory sums. Replaces ltc_sensory_fwd
+ * (csrc/ltc_kernels.cu:675-713), including its argument order (sigma, mu,
+ * w_pos, erev).
+ *   inputs       (B,D) with element strides sib, sid
+ *   w_num_sensory, w_den_sensory   (B,H) outputs: sum_d Ws*sig*Es, sum_d Ws*sig */
+long long ltc_sensory_fwd_workspace_bytes(int B, int D, int H);
+int ltc_sensory_fwd(const float* inputs, long long sib, long long sid,
+                    const float* sensory_sigma, const float* sensory_mu,
+                    const float* sensory_w_pos, const float* sensory_erev,
+                    int B, int D, int H,
+                    float* w_num_sensory, float* w_den_sensory,
+                    void* workspace, long long workspace_bytes, void* stream);
+
+/* One step's U implicit-Euler unfolds. Replaces ltc_ode_unfold_fwd
+ * (csrc/ltc_kernels.cu:716-777).
+ *   state        (B,H) state before the step; never written
+ *   w_num_sensory, w_den_sensory   (B,H) the step's sensory sums
+ *   state_out    (B,H) state after the U unfolds
+ *   v_buffer     (U,B,H) the pre-state of every unfold, written when
+ *                save_intermediates is nonzero (may be NULL otherwise) */
+long long ltc_ode_unfold_fwd_workspace_bytes(int B, int H, int ode_unfolds);
+int ltc_ode_unfold_fwd(const float* state, const float* w_pos, const float* w_erev,
+                       const float* mu, const float* sigma,
+                       const float* w_num_sensory, const float* w_den_sensory,
+                       const float* cm_t, const float* gleak_pos, const float* vleak,
+                       int B, int H, int ode_unfolds, float epsilon, int save_intermediates,
+                       float* state_out, float* v_buffer,
+                       void* workspace, long long workspace_bytes, void* stream);
+
+/* Backward of ltc_sensory_fwd. Replaces ltc_sensory_bwd
+ * (csrc/ltc_kernels.cu:780-837), same output order.
+ *   grad_w_num, grad_w_den   (B,H) dL/d w_num_sensory, dL/d w_den_sensory
+ *   grad_inputs  (B,D) contiguous; the four (D,H) parameter gradients */
+long long ltc_sensory_bwd_workspace_bytes(int B, int D, int H);
+int ltc_sensory_bwd(const float* grad_w_num, const float* grad_w_den,
+                    const float* inputs, long long sib, long long sid,
+                    const float* sensory_sigma, const float* sensory_mu,
+                    const float* sensory_w_pos, const float* sensory_erev,
+                    int B, int D, int H,
+                    float* grad_inputs, float* grad_sensory_sigma, float* grad_sensory_mu,
+                    float* grad_sensory_w_pos, float* grad_sensory_erev,
+                    void* workspace, long long workspace_bytes, void* stream);
+
+/* Backward of ltc_ode_unfold_fwd. Replaces ltc_ode_unfold_bwd
+ * (csrc/ltc_kernels.cu:845-950), same output order.
+ *   v_buffer     (U,B,H) from ltc_ode_unfold_fwd. The unfolds are recomputed
+ *                from v_buffer[0], as the reference's backward kernels
+ *                recompute each unfold (csrc/ltc_kernels.cu:549-668); the
+ *                other slices are not read.
+ *   grad_output  (B,H) dL/d state_out
+ * Outputs: grad_v (B,H) = dL/d state, grad_w_num_sensory and
+ * grad_w_den_sensory (B,H), grad_w_pos, grad_w_erev, grad_mu, grad_sigma
+ * (H,H), grad_cm_t, grad_gleak_pos, grad_vleak (H). */
+long long ltc_ode_unfold_bwd_workspace_bytes(int B, int H, int ode_unfolds);
+int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w_erev,
+                       const float* mu, const float* sigma,
+                       const float* w_num_sensory, const float* w_den_sensory,
+                       const float* cm_t, const float* gleak_pos, const float* vleak,
+                       const float* grad_output, int B, int H, int ode_unfolds, float epsilon,
+                       float* grad_v, float* grad_w_num_sensory, float* grad_w_den_sensory,
+                       float* grad_w_pos, float* grad_w_erev, float* grad_mu,
+                       float* grad_sigma, float* grad_cm_t, float* grad_gleak_pos,
+                       float* grad_vleak,
+                       void* workspace, long long workspace_bytes, void* stream);
+
+/*
  * Launch plan of one call, for diagnostics and host-side bounds tests. No
  * counterpart in the reference. Writes up to n of: Hp, Dp, NB (batch rows
  * per ODE workgroup), KS (reduction split), RC (= Hp/KS), threads per ODE

@@ -272,7 +272,7 @@ struct BwdWs {
 
 BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
   BwdWs w{};
-  w.pp.recF = c.take<float4>((long long)p.Hp * p.Hp);
+  w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.recB = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
   w.pp.neuron = c.take<float>(3LL * p.Hp);
@@ -804,6 +804,346 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
   e = timed(ltc::K_FINALIZE, s, [&] {
     return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s);
+  });
+  if (e != hipSuccess) return hip_fail("finalize launch", e);
+  return LTC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Per-step entry points of the reference (csrc/ltc_kernels.cu:674-950): one
+// time step's sensory sums, one step's U unfolds, and their backward passes,
+// as thin wrappers over the same kernels with T = 1.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct SensWs {
+  ltc::Prepped pp;
+  float* sn;    // [B][Hp]
+  float* sd;
+  float* spart;
+  float* dxpart;
+};
+
+SensWs carve_sens(const ltc::Plan& p, Carver& c, bool bwd) {
+  SensWs w{};
+  const long long img = (long long)p.Dp * p.Hp;
+  if (bwd)
+    w.pp.sensB = c.take<float4>(img);
+  else
+    w.pp.sensF = c.take<float4>(img);
+  w.sn = c.take<float>((long long)p.B * p.Hp);
+  w.sd = c.take<float>((long long)p.B * p.Hp);
+  if (bwd) {
+    w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
+    w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.Dp);
+  }
+  return w;
+}
+
+// One-step unfold workspace: the full-path regions with T = 1 (the backward
+// also recomputes the forward, so it holds both), plus the padded sensory
+// sums, the recomputed unfold states and a scratch final state.
+struct UnfoldWs {
+  FwdWs f;
+  BwdWs b;
+  float* vsave;  // saved_floats(p)
+  float* hscr;   // [B][H]
+};
+
+UnfoldWs carve_unfold(const ltc::Plan& p, Carver& c, bool bwd) {
+  UnfoldWs w{};
+  w.f = carve_fwd(p, c);
+  if (bwd) {
+    w.b = carve_bwd(p, c);
+    w.hscr = c.take<float>((long long)p.B * p.H);
+  }
+  w.vsave = c.take<float>(saved_floats(p));
+  return w;
+}
+
+int check_ws(long long need, void* workspace, long long workspace_bytes) {
+  if (workspace_bytes < need || (need > 0 && !workspace))
+    return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need) + " bytes");
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+    return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
+  return LTC_OK;
+}
+
+int check_step_dims(int B, int D, int H, int U) {
+  if (B < 0 || D < 1 || H < 1) return fail(LTC_EINVAL, "dimensions must satisfy B >= 0, D >= 1, H >= 1");
+  return check_dims(B, 1, D, H, U);
+}
+
+}  // namespace
+
+long long ltc_sensory_fwd_workspace_bytes(int B, int D, int H) {
+  if (check_step_dims(B, D, H, 1) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, 1, D, H, 1);
+  Carver c{nullptr};
+  carve_sens(p, c, false);
+  return round_up(c.off, 256);
+}
+
+long long ltc_sensory_bwd_workspace_bytes(int B, int D, int H) {
+  if (check_step_dims(B, D, H, 1) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, 1, D, H, 1);
+  Carver c{nullptr};
+  carve_sens(p, c, true);
+  return round_up(c.off, 256);
+}
+
+long long ltc_ode_unfold_fwd_workspace_bytes(int B, int H, int ode_unfolds) {
+  if (check_step_dims(B, 1, H, ode_unfolds) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, 1, 1, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_unfold(p, c, false);
+  return round_up(c.off, 256);
+}
+
+long long ltc_ode_unfold_bwd_workspace_bytes(int B, int H, int ode_unfolds) {
+  if (check_step_dims(B, 1, H, ode_unfolds) != LTC_OK) return -1;
+  const ltc::Plan p = make_plan(B, 1, 1, H, ode_unfolds);
+  Carver c{nullptr};
+  carve_unfold(p, c, true);
+  return round_up(c.off, 256);
+}
+
+int ltc_sensory_fwd(const float* inputs, long long sib, long long sid,
+                    const float* sensory_sigma, const float* sensory_mu,
+                    const float* sensory_w_pos, const float* sensory_erev, int B, int D, int H,
+                    float* w_num_sensory, float* w_den_sensory, void* workspace,
+                    long long workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_step_dims(B, D, H, 1);
+  if (rc != LTC_OK) return rc;
+  if (!sensory_sigma || !sensory_mu || !sensory_w_pos || !sensory_erev)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (B > 0 && (!inputs || !w_num_sensory || !w_den_sensory))
+    return fail(LTC_EINVAL, "inputs/w_num_sensory/w_den_sensory pointer is NULL");
+  const ltc::Plan p = make_plan(B, 1, D, H, 1);
+  Carver need{nullptr};
+  carve_sens(p, need, false);
+  rc = check_ws(need.off, workspace, workspace_bytes);
+  if (rc != LTC_OK) return rc;
+  if (B == 0) return LTC_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  Carver c{static_cast<char*>(workspace)};
+  const SensWs w = carve_sens(p, c, false);
+  const ltc::RawParams rp{nullptr, nullptr, nullptr, nullptr, sensory_mu, sensory_sigma,
+                          sensory_erev, sensory_w_pos, nullptr, nullptr, nullptr};
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep(p, rp, w.pp, false, s, ltc::kPrepSens); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = timed(ltc::K_SENS_FWD, s, [&] {
+    return ltc::launch_sens_fwd(p, inputs, ltc::Strides3{sib, 0, sid}, w.pp, w.sn, w.sd, s);
+  });
+  if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  e = ltc::launch_copy_rows(w.sn, p.Hp, w_num_sensory, H, B, H, s);
+  if (e == hipSuccess) e = ltc::launch_copy_rows(w.sd, p.Hp, w_den_sensory, H, B, H, s);
+  if (e != hipSuccess) return hip_fail("copy launch", e);
+  return LTC_OK;
+}
+
+int ltc_sensory_bwd(const float* grad_w_num, const float* grad_w_den, const float* inputs,
+                    long long sib, long long sid, const float* sensory_sigma,
+                    const float* sensory_mu, const float* sensory_w_pos,
+                    const float* sensory_erev, int B, int D, int H, float* grad_inputs,
+                    float* grad_sensory_sigma, float* grad_sensory_mu,
+                    float* grad_sensory_w_pos, float* grad_sensory_erev, void* workspace,
+                    long long workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_step_dims(B, D, H, 1);
+  if (rc != LTC_OK) return rc;
+  if (!sensory_sigma || !sensory_mu || !sensory_w_pos || !sensory_erev)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (!grad_sensory_sigma || !grad_sensory_mu || !grad_sensory_w_pos || !grad_sensory_erev)
+    return fail(LTC_EINVAL, "gradient output pointer is NULL");
+  if (B > 0 && (!grad_w_num || !grad_w_den || !inputs || !grad_inputs))
+    return fail(LTC_EINVAL, "grad_w_num/grad_w_den/inputs/grad_inputs pointer is NULL");
+  const ltc::Plan p = make_plan(B, 1, D, H, 1);
+  Carver need{nullptr};
+  carve_sens(p, need, true);
+  rc = check_ws(need.off, workspace, workspace_bytes);
+  if (rc != LTC_OK) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (B == 0) {
+    float* zd[] = {grad_sensory_sigma, grad_sensory_mu, grad_sensory_w_pos, grad_sensory_erev};
+    for (float* z : zd) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    return LTC_OK;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  const SensWs w = carve_sens(p, c, true);
+  const ltc::RawParams rp{nullptr, nullptr, nullptr, nullptr, sensory_mu, sensory_sigma,
+                          sensory_erev, sensory_w_pos, nullptr, nullptr, nullptr};
+  const ltc::Strides3 xs{sib, 0, sid};
+  ltc::GradOut go{};
+  go.x = grad_inputs;
+  go.s_mu = grad_sensory_mu;
+  go.s_sigma = grad_sensory_sigma;
+  go.s_erev = grad_sensory_erev;
+  go.s_wpos = grad_sensory_w_pos;
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep(p, rp, w.pp, true, s, ltc::kPrepSens); });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = ltc::launch_copy_rows(grad_w_num, H, w.sn, p.Hp, B, H, s);
+  if (e == hipSuccess) e = ltc::launch_copy_rows(grad_w_den, H, w.sd, p.Hp, B, H, s);
+  if (e != hipSuccess) return hip_fail("copy launch", e);
+  e = timed(ltc::K_SENS_BWD, s, [&] {
+    return ltc::launch_sens_bwd(p, inputs, xs, w.pp, w.sn, w.sd, w.spart, w.dxpart, s);
+  });
+  if (e != hipSuccess) return hip_fail("sensory backward launch", e);
+  e = timed(ltc::K_FINALIZE, s, [&] {
+    return ltc::launch_finalize(p, rp, nullptr, w.spart, w.dxpart, nullptr, ltc::PresumBuf{},
+                                go, s, ltc::kFinSens);
+  });
+  if (e != hipSuccess) return hip_fail("finalize launch", e);
+  return LTC_OK;
+}
+
+int ltc_ode_unfold_fwd(const float* state, const float* w_pos, const float* w_erev,
+                       const float* mu, const float* sigma, const float* w_num_sensory,
+                       const float* w_den_sensory, const float* cm_t, const float* gleak_pos,
+                       const float* vleak, int B, int H, int ode_unfolds, float epsilon,
+                       int save_intermediates, float* state_out, float* v_buffer,
+                       void* workspace, long long workspace_bytes, void* stream) {
+  g_err.clear();
+  int rc = check_step_dims(B, 1, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (!w_pos || !w_erev || !mu || !sigma || !cm_t || !gleak_pos || !vleak)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (B > 0 && (!state || !w_num_sensory || !w_den_sensory || !state_out))
+    return fail(LTC_EINVAL, "state/w_num_sensory/w_den_sensory/state_out pointer is NULL");
+  if (B > 0 && save_intermediates && !v_buffer)
+    return fail(LTC_EINVAL, "v_buffer pointer is NULL");
+  const ltc::Plan p = make_plan(B, 1, 1, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_unfold(p, need, false);
+  rc = check_ws(need.off, workspace, workspace_bytes);
+  if (rc != LTC_OK) return rc;
+  if (B == 0) return LTC_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  Carver c{static_cast<char*>(workspace)};
+  const UnfoldWs w = carve_unfold(p, c, false);
+  const ltc::RawParams rp{w_pos, w_erev, mu, sigma, nullptr, nullptr, nullptr, nullptr,
+                          cm_t, gleak_pos, vleak};
+  float* vsave = save_intermediates ? w.vsave : nullptr;
+  float* densave = save_intermediates ? w.vsave + ((long long)ode_unfolds + 1) * B * p.Hp : nullptr;
+  hipError_t e;
+  e = timed(ltc::K_PREP, s, [&] {
+    return ltc::launch_prep(p, rp, w.f.pp, false, s, ltc::kPrepRec | ltc::kPrepNeuron);
+  });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = ltc::launch_copy_rows(w_num_sensory, H, w.f.sn, p.Hp, B, H, s);
+  if (e == hipSuccess) e = ltc::launch_copy_rows(w_den_sensory, H, w.f.sd, p.Hp, B, H, s);
+  if (e != hipSuccess) return hip_fail("copy launch", e);
+  // T = 1: the kernel's (B,T,H) output and its final state are the same (B,H)
+  // values, written by the same thread.
+  e = timed(ltc::K_ODE_FWD, s, [&] {
+    return ltc::launch_ode_fwd(p, w.f.pp, w.f.sn, w.f.sd, state, epsilon, state_out, state_out,
+                               vsave, densave, w.f.cb, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  if (save_intermediates) {
+    e = ltc::launch_copy_rows(vsave, p.Hp, v_buffer, H, (long long)ode_unfolds * B, H, s);
+    if (e != hipSuccess) return hip_fail("copy launch", e);
+  }
+  return LTC_OK;
+}
+
+int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w_erev,
+                       const float* mu, const float* sigma, const float* w_num_sensory,
+                       const float* w_den_sensory, const float* cm_t, const float* gleak_pos,
+                       const float* vleak, const float* grad_output, int B, int H,
+                       int ode_unfolds, float epsilon, float* grad_v,
+                       float* grad_w_num_sensory, float* grad_w_den_sensory,
+                       float* grad_w_pos, float* grad_w_erev, float* grad_mu,
+                       float* grad_sigma, float* grad_cm_t, float* grad_gleak_pos,
+                       float* grad_vleak, void* workspace, long long workspace_bytes,
+                       void* stream) {
+  g_err.clear();
+  int rc = check_step_dims(B, 1, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  if (!w_pos || !w_erev || !mu || !sigma || !cm_t || !gleak_pos || !vleak)
+    return fail(LTC_EINVAL, "parameter pointer is NULL");
+  if (!grad_w_pos || !grad_w_erev || !grad_mu || !grad_sigma || !grad_cm_t || !grad_gleak_pos ||
+      !grad_vleak)
+    return fail(LTC_EINVAL, "gradient output pointer is NULL");
+  if (B > 0 && (!v_buffer || !w_num_sensory || !w_den_sensory || !grad_output || !grad_v ||
+                !grad_w_num_sensory || !grad_w_den_sensory))
+    return fail(LTC_EINVAL, "v_buffer/sensory/grad_output/grad_v pointer is NULL");
+  const ltc::Plan p = make_plan(B, 1, 1, H, ode_unfolds);
+  Carver need{nullptr};
+  carve_unfold(p, need, true);
+  rc = check_ws(need.off, workspace, workspace_bytes);
+  if (rc != LTC_OK) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (B == 0) {
+    float* zs[] = {grad_w_pos, grad_w_erev, grad_mu, grad_sigma};
+    for (float* z : zs) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    float* zh[] = {grad_cm_t, grad_gleak_pos, grad_vleak};
+    for (float* z : zh) {
+      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
+      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
+    }
+    return LTC_OK;
+  }
+  Carver c{static_cast<char*>(workspace)};
+  const UnfoldWs w = carve_unfold(p, c, true);
+  const ltc::RawParams rp{w_pos, w_erev, mu, sigma, nullptr, nullptr, nullptr, nullptr,
+                          cm_t, gleak_pos, vleak};
+  const int U = ode_unfolds;
+  float* vsave = w.vsave;
+  float* densave = w.vsave + ((long long)U + 1) * B * p.Hp;
+  ltc::GradOut go{};
+  go.w_pos = grad_w_pos;
+  go.w_erev = grad_w_erev;
+  go.mu = grad_mu;
+  go.sigma = grad_sigma;
+  go.cm = grad_cm_t;
+  go.gleak = grad_gleak_pos;
+  go.vleak = grad_vleak;
+  hipError_t e;
+  // Backward-mode images (recF for the recompute and rec_grad, recB for the
+  // chain) and the per-neuron vectors.
+  e = timed(ltc::K_PREP, s, [&] {
+    return ltc::launch_prep(p, rp, w.b.pp, true, s, ltc::kPrepRec | ltc::kPrepNeuron);
+  });
+  if (e != hipSuccess) return hip_fail("prep launch", e);
+  e = ltc::launch_copy_rows(w_num_sensory, H, w.f.sn, p.Hp, B, H, s);
+  if (e == hipSuccess) e = ltc::launch_copy_rows(w_den_sensory, H, w.f.sd, p.Hp, B, H, s);
+  if (e != hipSuccess) return hip_fail("copy launch", e);
+  // The unfold states and denominators, recomputed from v_buffer[0] (the
+  // reference's backward kernels recompute each unfold from its saved
+  // pre-state, csrc/ltc_kernels.cu:549-668).
+  e = timed(ltc::K_ODE_FWD, s, [&] {
+    return ltc::launch_ode_fwd(p, w.b.pp, w.f.sn, w.f.sd, v_buffer, epsilon, w.hscr, w.hscr,
+                               vsave, densave, w.f.cb, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  // dL/dv^U enters as the output gradient of the single step.
+  const ltc::Strides3 gs{H, 0, 1};
+  e = timed(ltc::K_ODE_BWD, s, [&] {
+    return ltc::launch_ode_bwd(p, w.b.pp, vsave, densave, grad_output, gs, nullptr, w.b.absave,
+                               w.b.dsn, w.b.dsd, w.b.npart, grad_v, w.b.rpart, w.b.cb, s);
+  });
+  if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+  if (!p.FUSE) {
+    e = timed(ltc::K_REC_GRAD, s,
+              [&] { return ltc::launch_rec_grad(p, w.b.pp, vsave, w.b.absave, w.b.rpart, s); });
+    if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  }
+  e = ltc::launch_copy_rows(w.b.dsn, p.Hp, grad_w_num_sensory, H, B, H, s);
+  if (e == hipSuccess) e = ltc::launch_copy_rows(w.b.dsd, p.Hp, grad_w_den_sensory, H, B, H, s);
+  if (e != hipSuccess) return hip_fail("copy launch", e);
+  e = timed(ltc::K_FINALIZE, s, [&] {
+    return ltc::launch_finalize(p, rp, w.b.rpart, nullptr, nullptr, w.b.npart, w.b.ps, go, s,
+                                ltc::kFinRec);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
   return LTC_OK;

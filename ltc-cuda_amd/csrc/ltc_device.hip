@@ -121,10 +121,10 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_
 // Parameter images (one launch, flat index space over three segments).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int H, int D,
-                                                   int Hp, int Dp, int bwd) {
+                                                   int Hp, int Dp, int bwd, int segs) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long long nrec = (long long)Hp * Hp;
-  const long long nsens = (long long)Dp * Hp;
+  const long long nrec = (segs & kPrepRec) ? (long long)Hp * Hp : 0;
+  const long long nsens = (segs & kPrepSens) ? (long long)Dp * Hp : 0;
   if (tid < nrec) {
     const int i = (int)(tid / Hp), j = (int)(tid - (long long)i * Hp);
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
     return;
   }
   tid -= nsens;
-  if (tid < 3LL * Hp) {
+  if ((segs & kPrepNeuron) && tid < 3LL * Hp) {
     const int q = (int)(tid / Hp), j = (int)(tid - (long long)q * Hp);
     const float* src = q == 0 ? rp.cm : (q == 1 ? rp.gleak : rp.vleak);
     pp.neuron[tid] = j < H ? src[j] : 0.f;
@@ -817,7 +817,10 @@ __global__ __launch_bounds__(256) void sens_bwd_kernel(SensBK k) {
 
 // ---------------------------------------------------------------------------
 // Finalize: fixed-order sums of every partial buffer, then the closed forms.
-// Flat index space: (H*H recurrent) + (D*H sensory) + (H neurons) + (BT*D x).
+// Flat index space in four segments: (H*H recurrent) + (H neurons) +
+// (D*H sensory) + (BT*D x). A launch covers [base, base + count) of it, so
+// the per-step entry points can finalize only the recurrent/neuron half or
+// only the sensory/x half.
 // ---------------------------------------------------------------------------
 struct FinK {
   RawParams rp;
@@ -827,6 +830,7 @@ struct FinK {
   const float* npart;
   GradOut g;
   int B, D, H, Hp, Dp, NCH, NRC, HB, BT;  // B, NCH: counts of neuron / recurrent partials
+  long long base, count;
 };
 
 // Sum of n strided partials with 8 loads in flight per round.
@@ -857,7 +861,9 @@ __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__
 }
 
 __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
-  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= k.count) return;
+  long long tid = k.base + gid;
   const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
   const long long nrec = (long long)H * H, nsens = (long long)D * H;
   if (tid < nrec) {
@@ -875,6 +881,18 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     return;
   }
   tid -= nrec;
+  if (tid < H) {
+    const int j = (int)tid;
+    const float* src = k.npart + j;
+    const float c = sum_partials(src, 3LL * Hp, k.B);
+    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
+    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
+    k.g.cm[j] = c;
+    k.g.gleak[j] = k.rp.vleak[j] * ga - gv;
+    k.g.vleak[j] = k.rp.gleak[j] * ga;
+    return;
+  }
+  tid -= H;
   if (tid < nsens) {
     // h-major walk so the partial reads are contiguous in d
     const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
@@ -893,23 +911,25 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     return;
   }
   tid -= nsens;
-  if (tid < H) {
-    const int j = (int)tid;
-    const float* src = k.npart + j;
-    const float c = sum_partials(src, 3LL * Hp, k.B);
-    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
-    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
-    k.g.cm[j] = c;
-    k.g.gleak[j] = k.rp.vleak[j] * ga - gv;
-    k.g.vleak[j] = k.rp.gleak[j] * ga;
-    return;
-  }
-  tid -= H;
   if (tid < (long long)k.BT * D) {
     const long long row = tid / D;
     const int d = (int)(tid - row * D);
     k.g.x[tid] = sum_partials(k.dxpart + row * Dp + d, (long long)k.BT * Dp, k.HB);
   }
+}
+
+// Copies `rows` rows of `cols` floats between row pitches (in floats) and
+// writes zeros into dst columns [cols, dst_ld): pads (B,H) into [B][Hp] and
+// strips the padding again.
+__global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict__ src,
+                                                        long long src_ld, float* __restrict__ dst,
+                                                        long long dst_ld, long long rows,
+                                                        int cols) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * dst_ld) return;
+  const long long r = i / dst_ld;
+  const int c = (int)(i - r * dst_ld);
+  dst[i] = c < cols ? src[r * src_ld + c] : 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -1755,11 +1775,23 @@ hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
-                       hipStream_t s) {
-  const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
+                       hipStream_t s, int segs) {
+  const long long total = ((segs & kPrepRec) ? (long long)p.Hp * p.Hp : 0) +
+                          ((segs & kPrepSens) ? (long long)p.Dp * p.Hp : 0) +
+                          ((segs & kPrepNeuron) ? 3LL * p.Hp : 0);
+  if (total == 0) return hipSuccess;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(prep_kernel, dim3(blocks), dim3(256), 0, s, rp, pp, p.H, p.D, p.Hp, p.Dp,
-                     bwd ? (p.FUSE ? 1 : 2) : 0);
+                     bwd ? (p.FUSE ? 1 : 2) : 0, segs);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long long dst_ld,
+                            long long rows, int cols, hipStream_t s) {
+  const long long n = rows * dst_ld;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
+                     src_ld, dst, dst_ld, rows, cols);
   return hipGetLastError();
 }
 
@@ -1900,15 +1932,21 @@ hipError_t presum(const Plan& p, const float* rpart, const float* npart, const P
 
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
-                           const PresumBuf& ps, const GradOut& g, hipStream_t s) {
+                           const PresumBuf& ps, const GradOut& g, hipStream_t s, int segs) {
   const int BT = p.B * p.T;
-  Partials pt;
-  hipError_t e = presum(p, rpart, npart, ps, s, pt);
-  if (e != hipSuccess) return e;
+  Partials pt{rpart, p.NCH, npart, p.B};
+  if (segs & kFinRec) {
+    hipError_t e = presum(p, rpart, npart, ps, s, pt);
+    if (e != hipSuccess) return e;
+  }
+  const long long nrn = (long long)p.H * p.H + p.H;
+  const long long nsx = (long long)p.D * p.H + (long long)BT * p.D;
+  const long long base = (segs & kFinRec) ? 0 : nrn;
+  const long long count = ((segs & kFinRec) ? nrn : 0) + ((segs & kFinSens) ? nsx : 0);
+  if (count == 0) return hipSuccess;
   FinK a{rp, pt.rpart, spart, dxpart, pt.npart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp, pt.nrec,
-         p.NRC, p.Hp / 32, BT};
-  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + (long long)BT * p.D;
-  const unsigned blocks = (unsigned)((total + 255) / 256);
+         p.NRC, p.Hp / 32, BT, base, count};
+  const unsigned blocks = (unsigned)((count + 255) / 256);
   hipLaunchKernelGGL(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }

@@ -132,8 +132,16 @@ struct LnBuf {
 // Largest input width the module path handles (LayerNorm rows in registers).
 constexpr int kModuleMaxD = 1024;
 
+// Segments of the parameter images that a prep launch builds: the recurrent
+// images, the sensory images and the per-neuron vectors.
+constexpr int kPrepRec = 1, kPrepSens = 2, kPrepNeuron = 4;
+constexpr int kPrepAll = kPrepRec | kPrepSens | kPrepNeuron;
 hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bool bwd,
-                       hipStream_t s);
+                       hipStream_t s, int segs = kPrepAll);
+// Copies rows x cols floats from pitch src_ld to pitch dst_ld (both in
+// floats), zero-filling dst columns [cols, dst_ld).
+hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long long dst_ld,
+                            long long rows, int cols, hipStream_t s);
 // Module path: images from the leaves; with ln != nullptr the same launch
 // also normalises every (b,t) row of x.
 hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, bool bwd,
@@ -197,9 +205,14 @@ struct PresumBuf {
   float* neuron;  // presum_parts(B) x 3*Hp
   float* ln;      // module path: presum_parts(ln_bwd_blocks) x 4*Dp
 };
+// Gradient groups a finalize launch writes: the recurrent and per-neuron
+// gradients (from rpart, npart) and the sensory and input gradients (from
+// spart, dxpart).
+constexpr int kFinRec = 1, kFinSens = 2, kFinAll = kFinRec | kFinSens;
 hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpart,
                            const float* spart, const float* dxpart, const float* npart,
-                           const PresumBuf& ps, const GradOut& g, hipStream_t s);
+                           const PresumBuf& ps, const GradOut& g, hipStream_t s,
+                           int segs = kFinAll);
 
 // Module path backward.
 struct LeafGrads {

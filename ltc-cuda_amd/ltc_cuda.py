@@ -57,7 +57,10 @@ class CApi:
         "ltc_full_backward", "ltc_module_saved_floats", "ltc_module_fwd_workspace_bytes",
         "ltc_module_bwd_workspace_bytes", "ltc_module_forward", "ltc_module_backward",
         "ltc_launch_plan", "ltc_timing_enable", "ltc_timing_read", "ltc_kernel_count",
-        "ltc_kernel_name",
+        "ltc_kernel_name", "ltc_sensory_fwd_workspace_bytes", "ltc_sensory_fwd",
+        "ltc_ode_unfold_fwd_workspace_bytes", "ltc_ode_unfold_fwd",
+        "ltc_sensory_bwd_workspace_bytes", "ltc_sensory_bwd",
+        "ltc_ode_unfold_bwd_workspace_bytes", "ltc_ode_unfold_bwd",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
@@ -107,6 +110,27 @@ class CApi:
             + [_f32p, _i64, _i64, _i64, _f32p]
             + [_int, _int, _int, _int, _int, _flt, _flt, _flt]
             + [_f32p] * 17 + [_f32p, _i64, ctypes.c_void_p])
+        for name in ("ltc_sensory_fwd_workspace_bytes", "ltc_sensory_bwd_workspace_bytes",
+                     "ltc_ode_unfold_fwd_workspace_bytes", "ltc_ode_unfold_bwd_workspace_bytes"):
+            fn = getattr(lib, name)
+            fn.restype = _i64
+            fn.argtypes = [_int, _int, _int]
+        lib.ltc_sensory_fwd.restype = _int
+        lib.ltc_sensory_fwd.argtypes = (
+            [_f32p, _i64, _i64] + [_f32p] * 4 + [_int, _int, _int] + [_f32p, _f32p]
+            + [_f32p, _i64, ctypes.c_void_p])
+        lib.ltc_ode_unfold_fwd.restype = _int
+        lib.ltc_ode_unfold_fwd.argtypes = (
+            [_f32p] * 10 + [_int, _int, _int, _flt, _int] + [_f32p, _f32p]
+            + [_f32p, _i64, ctypes.c_void_p])
+        lib.ltc_sensory_bwd.restype = _int
+        lib.ltc_sensory_bwd.argtypes = (
+            [_f32p, _f32p, _f32p, _i64, _i64] + [_f32p] * 4 + [_int, _int, _int]
+            + [_f32p] * 5 + [_f32p, _i64, ctypes.c_void_p])
+        lib.ltc_ode_unfold_bwd.restype = _int
+        lib.ltc_ode_unfold_bwd.argtypes = (
+            [_f32p] * 11 + [_int, _int, _int, _flt] + [_f32p] * 10
+            + [_f32p, _i64, ctypes.c_void_p])
         lib.ltc_launch_plan.restype = _int
         lib.ltc_launch_plan.argtypes = [_int, _int, _int, _int, _int,
                                         ctypes.POINTER(ctypes.c_longlong), _int]
@@ -130,7 +154,11 @@ class CApi:
                   "bwd_ws": lambda: self.lib.ltc_bwd_workspace_bytes(B, T, D, H, U),
                   "msaved": lambda: self.lib.ltc_module_saved_floats(B, T, D, H, U),
                   "mfwd_ws": lambda: self.lib.ltc_module_fwd_workspace_bytes(B, T, D, H, U),
-                  "mbwd_ws": lambda: self.lib.ltc_module_bwd_workspace_bytes(B, T, D, H, U)}[kind]
+                  "mbwd_ws": lambda: self.lib.ltc_module_bwd_workspace_bytes(B, T, D, H, U),
+                  "sfwd_ws": lambda: self.lib.ltc_sensory_fwd_workspace_bytes(B, D, H),
+                  "sbwd_ws": lambda: self.lib.ltc_sensory_bwd_workspace_bytes(B, D, H),
+                  "ufwd_ws": lambda: self.lib.ltc_ode_unfold_fwd_workspace_bytes(B, H, U),
+                  "ubwd_ws": lambda: self.lib.ltc_ode_unfold_bwd_workspace_bytes(B, H, U)}[kind]
             v = int(fn())
             if v < 0:
                 raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
@@ -283,6 +311,132 @@ class _HipModule:
                 B, T, D, H, U, float(epsilon),
                 *[_ptr(g) for g in grads], _aligned(ws), int(need), _stream_handle(dev))
         self.capi.check(rc, "ltc_full_backward")
+        return grads
+
+
+    # -- per-step entry points (csrc/ltc_kernels.cu:675-950, bound at :1308-1311) --------
+
+    @staticmethod
+    def _check_f32(dev, *tensors):
+        for t in tensors:
+            if t.device != dev or not t.is_cuda:
+                raise ValueError("all LTC tensors must be on the same CUDA (HIP) device")
+            if t.dtype != torch.float32:
+                raise TypeError(f"LTC HIP kernels are fp32-only, got {t.dtype}")
+
+    @staticmethod
+    def _check_shapes(pairs):
+        for t, shp in pairs:
+            if tuple(t.shape) != tuple(shp):
+                raise ValueError(f"tensor shape {tuple(t.shape)} != expected {tuple(shp)}")
+
+    def ltc_sensory_fwd(self, inputs, sensory_sigma, sensory_mu, sensory_w_pos, sensory_erev):
+        """One step's sensory sums -> [w_num_sensory (B,H), w_den_sensory (B,H)]."""
+        if inputs.dim() != 2:
+            raise ValueError(f"inputs must be (B, D), got {tuple(inputs.shape)}")
+        B, D = inputs.shape
+        H = sensory_sigma.shape[-1]
+        params = [sensory_sigma, sensory_mu, sensory_w_pos, sensory_erev]
+        self._check_shapes([(p, (D, H)) for p in params])
+        dev = inputs.device
+        self._check_f32(dev, inputs, *params)
+        params = [p.contiguous() for p in params]
+        f32 = dict(device=dev, dtype=torch.float32)
+        wn, wd = torch.empty(B, H, **f32), torch.empty(B, H, **f32)
+        need = self.capi.sizes("sfwd_ws", B, 1, D, H, 1)
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            si = inputs.stride()
+            rc = self.capi.lib.ltc_sensory_fwd(
+                _ptr(inputs), si[0], si[1], *[_ptr(p) for p in params], B, D, H,
+                _ptr(wn), _ptr(wd), _aligned(ws), int(need), _stream_handle(dev))
+        self.capi.check(rc, "ltc_sensory_fwd")
+        return [wn, wd]
+
+    def ltc_ode_unfold_fwd(self, state, w_pos, w_erev, mu, sigma, w_num_sensory,
+                           w_den_sensory, cm_t, gleak_pos, vleak, ode_unfolds, epsilon,
+                           save_intermediates):
+        """One step's unfolds -> [state_new (B,H), v_buffer (U,B,H) or None]."""
+        if state.dim() != 2:
+            raise ValueError(f"state must be (B, H), got {tuple(state.shape)}")
+        B, H = state.shape
+        U = int(ode_unfolds)
+        ins = [w_pos, w_erev, mu, sigma, w_num_sensory, w_den_sensory, cm_t, gleak_pos, vleak]
+        self._check_shapes(list(zip(ins, [(H, H)] * 4 + [(B, H)] * 2 + [(H,)] * 3)))
+        dev = state.device
+        self._check_f32(dev, state, *ins)
+        state_c = state.contiguous()
+        ins = [t.contiguous() for t in ins]
+        f32 = dict(device=dev, dtype=torch.float32)
+        out = torch.empty(B, H, **f32)
+        vbuf = torch.empty(U, B, H, **f32) if save_intermediates else None
+        need = self.capi.sizes("ufwd_ws", B, 1, 1, H, U)
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            rc = self.capi.lib.ltc_ode_unfold_fwd(
+                _ptr(state_c), *[_ptr(t) for t in ins], B, H, U, float(epsilon),
+                1 if save_intermediates else 0, _ptr(out), _ptr(vbuf), _aligned(ws), int(need),
+                _stream_handle(dev))
+        self.capi.check(rc, "ltc_ode_unfold_fwd")
+        return [out, vbuf]
+
+    def ltc_sensory_bwd(self, grad_w_num, grad_w_den, inputs, sensory_sigma, sensory_mu,
+                        sensory_w_pos, sensory_erev):
+        """-> [grad_inputs (B,D), grad_sigma, grad_mu, grad_w_pos, grad_erev (D,H)]."""
+        if inputs.dim() != 2:
+            raise ValueError(f"inputs must be (B, D), got {tuple(inputs.shape)}")
+        B, D = inputs.shape
+        H = sensory_sigma.shape[-1]
+        params = [sensory_sigma, sensory_mu, sensory_w_pos, sensory_erev]
+        self._check_shapes([(p, (D, H)) for p in params]
+                           + [(grad_w_num, (B, H)), (grad_w_den, (B, H))])
+        dev = inputs.device
+        self._check_f32(dev, inputs, grad_w_num, grad_w_den, *params)
+        params = [p.contiguous() for p in params]
+        gn, gd = grad_w_num.contiguous(), grad_w_den.contiguous()
+        f32 = dict(device=dev, dtype=torch.float32)
+        grads = [torch.empty(B, D, **f32)] + [torch.empty(D, H, **f32) for _ in range(4)]
+        need = self.capi.sizes("sbwd_ws", B, 1, D, H, 1)
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            si = inputs.stride()
+            rc = self.capi.lib.ltc_sensory_bwd(
+                _ptr(gn), _ptr(gd), _ptr(inputs), si[0], si[1], *[_ptr(p) for p in params],
+                B, D, H, *[_ptr(g) for g in grads], _aligned(ws), int(need),
+                _stream_handle(dev))
+        self.capi.check(rc, "ltc_sensory_bwd")
+        return grads
+
+    def ltc_ode_unfold_bwd(self, v_buffer, w_pos, w_erev, mu, sigma, w_num_sensory,
+                           w_den_sensory, cm_t, gleak_pos, vleak, grad_output, ode_unfolds,
+                           epsilon):
+        """-> [grad_v, grad_w_num_sensory, grad_w_den_sensory (B,H), grad_w_pos,
+        grad_w_erev, grad_mu, grad_sigma (H,H), grad_cm, grad_gleak, grad_vleak (H)]."""
+        if v_buffer.dim() != 3:
+            raise ValueError(f"v_buffer must be (U, B, H), got {tuple(v_buffer.shape)}")
+        U = int(ode_unfolds)
+        _, B, H = v_buffer.shape
+        if v_buffer.shape[0] < 1:
+            raise ValueError("v_buffer holds no unfold")
+        ins = [w_pos, w_erev, mu, sigma, w_num_sensory, w_den_sensory, cm_t, gleak_pos, vleak,
+               grad_output]
+        self._check_shapes(list(zip(ins, [(H, H)] * 4 + [(B, H)] * 2 + [(H,)] * 3
+                                    + [(B, H)])))
+        dev = v_buffer.device
+        self._check_f32(dev, v_buffer, *ins)
+        v0 = v_buffer[0].contiguous()
+        ins = [t.contiguous() for t in ins]
+        f32 = dict(device=dev, dtype=torch.float32)
+        grads = [torch.empty(B, H, **f32) for _ in range(3)]
+        grads += [torch.empty(H, H, **f32) for _ in range(4)]
+        grads += [torch.empty(H, **f32) for _ in range(3)]
+        need = self.capi.sizes("ubwd_ws", B, 1, 1, H, U)
+        with torch.cuda.device(dev):
+            ws = _workspace(need, dev)
+            rc = self.capi.lib.ltc_ode_unfold_bwd(
+                _ptr(v0), *[_ptr(t) for t in ins], B, H, U, float(epsilon),
+                *[_ptr(g) for g in grads], _aligned(ws), int(need), _stream_handle(dev))
+        self.capi.check(rc, "ltc_ode_unfold_bwd")
         return grads
 
 

@@ -6,6 +6,8 @@ this file. It restates, in this build's own code:
   * the module init and its RNG consumption order    ltc.py:149-231
   * the pre-transforms (LayerNorm, affine, softplus)  ltc.py:249-288
   * one implicit-Euler ODE step with U unfolds        ltc.py:19-65
+    (as its two halves, sensory_sums and unfolds, which are also the
+    reference's per-step entry points, csrc/ltc_kernels.cu:675-777)
   * the outer T loop                                  ltc.py:68-106
   * the return convention (out, (h, h))               ltc.py:326
 
@@ -32,6 +34,8 @@ __all__ = [
     "PARAM_KEYS",
     "init_params",
     "transforms",
+    "sensory_sums",
+    "unfolds",
     "ode_step",
     "forward_loop",
     "forward_loop_scripted",
@@ -110,25 +114,48 @@ def transforms(p: dict, dt: float, ode_unfolds: int):
     return w_pos, w_erev, cm_t, gleak_pos, sensory_w_pos
 
 
+def sensory_sums(inputs, sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos):
+    """One step's sensory numerator and denominator sums (ltc.py:44-48).
+
+    inputs (B, D); the sums reduce over D (dim 1 of the (B, D, H) product).
+    Returns (num_s, den_s), each (B, H). The reference's per-step entry point
+    ltc_sensory_fwd computes the same pair (csrc/ltc_kernels.cu:675-713).
+    """
+    s_act = torch.sigmoid(sensory_sigma * (inputs.unsqueeze(-1) - sensory_mu))
+    s_wact = sensory_w_pos * s_act
+    return (s_wact * sensory_erev).sum(dim=1), s_wact.sum(dim=1)
+
+
+def unfolds(state, w_pos, w_erev, mu, sigma, num_s, den_s, cm_t, gleak_pos, vleak,
+            ode_unfolds: int, epsilon: float):
+    """U implicit-Euler unfolds of one step (ltc.py:50-63).
+
+    The recurrent sums reduce over the presynaptic index i (dim 1 of the
+    (B, H, H) product). Returns (v after the last unfold, [pre-state of every
+    unfold]); the reference's ltc_ode_unfold_fwd returns the same pair
+    (csrc/ltc_kernels.cu:716-777).
+    """
+    v = state
+    pre = []
+    for _ in range(ode_unfolds):
+        pre.append(v)
+        act = torch.sigmoid(sigma * (v.unsqueeze(-1) - mu))
+        num = (act * w_erev).sum(dim=1) + num_s
+        den = (w_pos * act).sum(dim=1) + den_s
+        v = (cm_t * v + gleak_pos * vleak + num) / (cm_t + gleak_pos + den + epsilon)
+    return v, pre
+
+
 def ode_step(inputs, state, w_pos, w_erev, mu, sigma,
              sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos,
              cm_t, gleak_pos, vleak, ode_unfolds: int, epsilon: float):
     """One time step: sensory reduction, then U implicit-Euler unfolds.
 
-    Follows ltc.py:42-65. inputs (B, D), state (B, H). The sensory sums
-    reduce over D (dim 1 of the (B, D, H) product); the recurrent sums reduce
-    over the presynaptic index i (dim 1 of the (B, H, H) product).
+    Follows ltc.py:42-65. inputs (B, D), state (B, H).
     """
-    s_act = torch.sigmoid(sensory_sigma * (inputs.unsqueeze(-1) - sensory_mu))
-    s_wact = sensory_w_pos * s_act
-    num_s = (s_wact * sensory_erev).sum(dim=1)
-    den_s = s_wact.sum(dim=1)
-    v = state
-    for _ in range(ode_unfolds):
-        act = torch.sigmoid(sigma * (v.unsqueeze(-1) - mu))
-        num = (act * w_erev).sum(dim=1) + num_s
-        den = (w_pos * act).sum(dim=1) + den_s
-        v = (cm_t * v + gleak_pos * vleak + num) / (cm_t + gleak_pos + den + epsilon)
+    num_s, den_s = sensory_sums(inputs, sensory_mu, sensory_sigma, sensory_erev, sensory_w_pos)
+    v, _ = unfolds(state, w_pos, w_erev, mu, sigma, num_s, den_s, cm_t, gleak_pos, vleak,
+                   ode_unfolds, epsilon)
     return v
 
 

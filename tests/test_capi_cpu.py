@@ -101,6 +101,59 @@ def test_backward_rejects_bad_arguments_before_launch(capi):
     assert rc == 1 and "workspace" in capi.last_error()
 
 
+def test_step_entry_point_sizes(capi):
+    lib = capi.lib
+    for fn in (lib.ltc_sensory_fwd_workspace_bytes, lib.ltc_sensory_bwd_workspace_bytes):
+        a, b = fn(24, 128, 64), fn(48, 128, 64)
+        assert 0 < a < b and a % 256 == 0
+        assert fn(1, 0, 8) == -1 and fn(1, 8, 0) == -1 and fn(-1, 8, 8) == -1
+        assert fn(1, 8, 2000) == -1
+    for fn in (lib.ltc_ode_unfold_fwd_workspace_bytes, lib.ltc_ode_unfold_bwd_workspace_bytes):
+        a, b = fn(24, 64, 6), fn(48, 64, 6)
+        assert 0 < a < b and a % 256 == 0
+        assert fn(1, 8, 0) == -1 and fn(1, 0, 6) == -1 and fn(1, 2000, 6) == -1
+    # the backward also recomputes the forward, so it needs more
+    assert lib.ltc_ode_unfold_bwd_workspace_bytes(24, 64, 6) > \
+        lib.ltc_ode_unfold_fwd_workspace_bytes(24, 64, 6)
+
+
+def test_step_entry_points_reject_bad_arguments_before_launch(capi):
+    """Fake non-NULL addresses: every case fails validation, so nothing runs."""
+    lib = capi.lib
+    big = 1 << 30
+    # ltc_sensory_fwd(inputs, sib, sid, sigma, mu, w_pos, erev, B, D, H, wn, wd, ws, wsb, s)
+    assert lib.ltc_sensory_fwd(1, 4, 1, 1, 1, 1, 1, 2, 0, 5, 1, 1, 256, big, None) == 1
+    assert lib.ltc_sensory_fwd(1, 4, 1, 1, None, 1, 1, 2, 4, 5, 1, 1, 256, big, None) == 1
+    assert "NULL" in capi.last_error()
+    assert lib.ltc_sensory_fwd(1, 4, 1, 1, 1, 1, 1, 2, 4, 5, None, 1, 256, big, None) == 1
+    assert lib.ltc_sensory_fwd(1, 4, 1, 1, 1, 1, 1, 2, 4, 5, 1, 1, 256, 64, None) == 1
+    assert "workspace too small" in capi.last_error()
+    assert lib.ltc_sensory_fwd(1, 4, 1, 1, 1, 1, 1, 2, 4, 5, 1, 1, 264, big, None) == 1
+    assert "aligned" in capi.last_error()
+    # ltc_sensory_bwd(gn, gd, inputs, sib, sid, sigma, mu, w_pos, erev, B, D, H, 5 grads, ...)
+    assert lib.ltc_sensory_bwd(1, 1, 1, 4, 1, 1, 1, 1, 1, 2, 4, 5, 1, 1, 1, None, 1,
+                               256, big, None) == 1
+    assert "gradient output" in capi.last_error()
+    assert lib.ltc_sensory_bwd(1, 1, 1, 4, 1, 1, 1, 1, 1, 2, 4, 5, 1, 1, 1, 1, 1,
+                               256, 16, None) == 1
+    # ltc_ode_unfold_fwd(state, 9 tensors, B, H, U, eps, save, out, vbuf, ws, wsb, s)
+    t9 = [1] * 9
+    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 5, 0, 1e-8, 0, 1, None, 256, big, None) == 1
+    assert "ode_unfolds" in capi.last_error()
+    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 5, 6, 1e-8, 1, 1, None, 256, big, None) == 1
+    assert "v_buffer" in capi.last_error()
+    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 1025, 6, 1e-8, 0, 1, None, 256, big, None) == 2
+    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 5, 6, 1e-8, 0, 1, None, 256, 16, None) == 1
+    # ltc_ode_unfold_bwd(vbuf, 9 tensors, grad_out, B, H, U, eps, 10 grads, ws, wsb, s)
+    g10 = [1] * 10
+    assert lib.ltc_ode_unfold_bwd(1, *t9, None, 2, 5, 6, 1e-8, *g10, 256, big, None) == 1
+    assert "NULL" in capi.last_error()
+    assert lib.ltc_ode_unfold_bwd(1, *t9, 1, 2, 5, 6, 1e-8, *g10[:9], None, 256, big,
+                                  None) == 1
+    assert lib.ltc_ode_unfold_bwd(1, *t9, 1, 2, 5, 6, 1e-8, *g10, 256, 16, None) == 1
+    assert "workspace too small" in capi.last_error()
+
+
 def test_timing_surface(capi):
     n = capi.lib.ltc_kernel_count()
     names = [capi.lib.ltc_kernel_name(k).decode() for k in range(n)]

@@ -205,3 +205,36 @@ def test_gradcheck_tiny():
     leaves = tuple(t.clone().requires_grad_(True) for t in a)
     fn = lambda *ts: O.forward_loop(*ts, U, 1e-8)
     assert torch.autograd.gradcheck(fn, leaves, eps=1e-6, atol=1e-6, rtol=1e-4)
+
+
+def test_step_halves_pre_states_and_sensory_sums():
+    """`unfolds` returns the pre-state of every unfold: pre[k] is the state after
+    k unfolds, so an off-by-one in the saved list fails; `sensory_sums` agrees
+    with a scalar loop over (b, d, h) on a tiny case."""
+    torch.manual_seed(3)
+    B, D, H, U = 2, 3, 4, 6
+    p = O.init_params(D, H)
+    w_pos, w_erev, cm_t, gleak_pos, s_wpos = O.transforms(p, 1.0 / 30.0, U)
+    x = torch.randn(B, D, dtype=torch.float64)
+    h0 = torch.randn(B, H, dtype=torch.float64) * 0.2
+    d = {k: v.double() for k, v in p.items()}
+    sn, sd = O.sensory_sums(x, d["sensory_mu"], d["sensory_sigma"], d["sensory_erev"],
+                            s_wpos.double())
+    for b in range(B):
+        for h in range(H):
+            num = den = 0.0
+            for i in range(D):
+                z = d["sensory_sigma"][i, h].item() * (x[b, i].item() - d["sensory_mu"][i, h].item())
+                a = 1.0 / (1.0 + math.exp(-z)) * s_wpos[i, h].item()
+                num += a * d["sensory_erev"][i, h].item()
+                den += a
+            assert abs(sn[b, h].item() - num) < 1e-12 and abs(sd[b, h].item() - den) < 1e-12
+    args = (w_pos.double(), w_erev.double(), d["mu"], d["sigma"], sn, sd, cm_t.double(),
+            gleak_pos.double(), d["vleak"])
+    v6, pre = O.unfolds(h0, *args, U, 1e-8)
+    assert len(pre) == U and torch.equal(pre[0], h0)
+    for k in range(1, U):
+        vk, _ = O.unfolds(h0, *args, k, 1e-8)
+        assert torch.equal(pre[k], vk)
+    v1, _ = O.unfolds(pre[U - 1], *args, 1, 1e-8)
+    assert torch.equal(v1, v6)
