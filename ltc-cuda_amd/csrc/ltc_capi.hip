@@ -52,21 +52,23 @@ int device_cus() {
 // Dynamic LDS of a cluster member, leaving room for its static flag word.
 constexpr long long kClusterLds = 60 * 1024;
 
-// Hp = 256: the chain runs as clusters of 8 members of 32 columns with 512
-// threads, 16 register-resident synapses per thread and their four gradient
-// sums in registers, which removes the separate parameter-gradient pass.
+// Hp = 256 and 512: the chain runs as clusters of Hp/32 members of 32
+// columns with 512 threads, each thread holding the four gradient sums of its
+// Hp/16 synapses in registers (operands register-resident at Hp = 256,
+// streamed at 512), which removes the separate parameter-gradient pass.
 void plan_fused_chain(ltc::Plan& p, int ncu) {
-  if (p.Hp != 256) return;
+  if (p.Hp != 256 && p.Hp != 512) return;
   const int cp = p.Hp / 32, slots = ncu / cp;
   for (int nb : {1, 2, 4, 8}) {
     const int ncl = (p.B + nb - 1) / nb;
     if (ncl > slots) continue;
+    if ((long long)nb * p.Hp * 8 + 16LL * nb * 32 * 4 > kClusterLds) continue;
     p.CPB = cp;
     p.JWB = 32;
     p.NBB = nb;
     p.NCLB = ncl;
     p.KSB = 16;
-    p.RCB = 16;
+    p.RCB = p.Hp / 16;
     p.FUSE = true;
     return;
   }

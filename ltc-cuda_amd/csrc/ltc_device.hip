@@ -1412,6 +1412,51 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   }
 }
 
+// Fused chain synapse phase with streamed operands (RCS rows per thread,
+// fully unrolled so that each row's four gradient sums stay in registers).
+// Members are 32 columns wide, so a wave holds two reduction chunks: its
+// lower half reads rows [srow0, srow0 + RCS), its upper half the RCS rows
+// after them. The upper half's row offset rides in its per-lane byte offset,
+// so the row walk stays a scalar offset. Rows come four at a time, the next
+// four requested while the current four are evaluated; the prefetch past the
+// chunk reads the next chunk's rows or the image's slack rows.
+//   jrow0  this thread's first postsynaptic row (for alpha/beta in LDS)
+template <int NB, int RCS>
+__device__ __forceinline__ void chain_fused_stream(__amdgpu_buffer_rsrc_t rs, int lane_bytes,
+                                                   int srow0, int jrow0, int Hp,
+                                                   const float2* ab, const float* vi,
+                                                   float* acc, float4 (&gacc)[RCS]) {
+  static_assert(RCS % 8 == 0, "rows come in groups of eight");
+  const int rowb = Hp * 16;
+  const int sb = srow0 * rowb;
+  float4 pa[4], pb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + q * rowb);
+#pragma unroll
+  for (int rr = 0; rr < RCS; rr += 8) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pb[q] = image_load(rs, lane_bytes, sb + (rr + 4 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bwd_synapse<NB, true>(pa[q], ab, Hp, jrow0 + rr + q, vi, acc, gacc[rr + q]);
+      asm volatile("" : "+v"(gacc[rr + q].x), "+v"(gacc[rr + q].y), "+v"(gacc[rr + q].z),
+                   "+v"(gacc[rr + q].w));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + (rr + 8 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bwd_synapse<NB, true>(pb[q], ab, Hp, jrow0 + rr + 4 + q, vi, acc, gacc[rr + 4 + q]);
+      asm volatile("" : "+v"(gacc[rr + 4 + q].x), "+v"(gacc[rr + 4 + q].y),
+                   "+v"(gacc[rr + 4 + q].z), "+v"(gacc[rr + 4 + q].w));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 struct BwdCK {
   const float4* recB;  // [Hp][Hp] (+ slack rows)
   const float* neuron;
@@ -1436,18 +1481,21 @@ struct BwdCK {
 // members' columns are then rebuilt from the published dL/dv_j and the saved
 // den_j, v_j, so only one value per (row, column) crosses the cluster.
 // Thread (o, ks): column i = p*JW + o, postsynaptic rows [ks*RC, ks*RC + RC).
-// FUSE (JW = 32, RCP register-resident operands of the unfolded image): the
-// thread also accumulates the four recurrent parameter-gradient sums of its
-// RCP synapses over all rows and unfolds, and writes one partial per cluster,
-// so the separate parameter-gradient pass and its gate evaluation go away.
-template <int NB, int JW, int RCP, bool FUSE>
+// FUSE (JW = 32, the unfolded image): the thread also accumulates the four
+// recurrent parameter-gradient sums of its synapses over all rows and
+// unfolds, and writes one partial per cluster, so the separate
+// parameter-gradient pass and its gate evaluation go away. Its operands are
+// register-resident (RCP rows) or streamed (RCS rows, chain_fused_stream).
+template <int NB, int JW, int RCP, bool FUSE, int RCS = 0>
 __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) {
-  static_assert(!FUSE || RCP > 0, "the fused chain keeps its operands in registers");
+  static_assert(!FUSE || RCP > 0 || RCS > 0, "the fused chain needs a compile-time row count");
+  static_assert(RCS == 0 || (FUSE && JW == 32 && RCP == 0), "streamed fusion: 32-column members");
+  constexpr int NACC = FUSE ? (RCP > 0 ? RCP : RCS) : 1;  // synapses with gradient sums
   constexpr int PER = NB * JW;
   extern __shared__ float4 lds4[];
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
-  const int RC = RCP > 0 ? RCP : k.RC;
+  const int RC = RCP > 0 ? RCP : (RCS > 0 ? RCS : k.RC);
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
   const int tid = threadIdx.x, nthr = blockDim.x;
@@ -1472,10 +1520,10 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + c];
   }
-  float4 gacc[FUSE ? RCP : 1];
+  float4 gacc[NACC];
   if constexpr (FUSE) {
 #pragma unroll
-    for (int rr = 0; rr < RCP; ++rr) gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int rr = 0; rr < NACC; ++rr) gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (tid == 0) gave_up = 0;
 
@@ -1556,7 +1604,13 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     float acc[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[b] = 0.f;
-    if constexpr (FUSE) {
+    if constexpr (FUSE && RCS > 0) {
+      // Wave w holds chunks 2w (lower half) and 2w + 1 (upper half).
+      const int srow0 = __builtin_amdgcn_readfirstlane((tid >> 6) * 2 * RCS);
+      const int lane_bytes = c * 16 + ((tid >> 5) & 1) * RCS * Hp * 16;
+      const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
+      chain_fused_stream<NB, RCS>(rsB, lane_bytes, srow0, r0, Hp, ab, cvi, acc, gacc);
+    } else if constexpr (FUSE) {
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) {
         bwd_synapse<NB, true>(preg[rr], ab, Hp, r0 + rr, cvi, acc, gacc[rr]);
@@ -1660,7 +1714,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     const long long HH = (long long)Hp * Hp;
     float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp + r0;
 #pragma unroll
-    for (int rr = 0; rr < RCP; ++rr) {
+    for (int rr = 0; rr < NACC; ++rr) {
       out[rr] = gacc[rr].x;
       out[HH + rr] = gacc[rr].y;
       out[2 * HH + rr] = gacc[rr].z;
@@ -1761,9 +1815,15 @@ hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
   const dim3 grid(p.NCLB * p.CPB), block(p.JWB * p.KSB);
   const size_t lds = bwd_cl_lds_bytes(p);
   if (p.FUSE) {
-    // 32-column members, 512 threads, 16 register-resident synapses each.
-    if (p.JWB != 32 || p.RCB != 16 || p.KSB != 16) return hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
+    // 32-column members, 512 threads: 16 register-resident synapses each
+    // (Hp = 256) or 32 streamed ones (Hp = 512).
+    if (p.JWB != 32 || p.KSB != 16) return hipErrorInvalidConfiguration;
+    if (p.RCB == 16)
+      hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
+    else if (p.RCB == 32)
+      hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 0, true, 32>), grid, block, lds, s, a);
+    else
+      return hipErrorInvalidConfiguration;
   } else {
     // Streamed operands (a register-resident form spilled at 1024 threads
     // and measured slower).

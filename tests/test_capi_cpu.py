@@ -205,9 +205,10 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         assert p["ode_workgroups_bwd"] == p["CPB"] * -(-B // p["NBB"])
         assert p["KSB"] >= p["NBB"] and p["lds_bwd"] <= 65536
         if p["fuse"]:
-            # Hp = 256 chain: 8 members of 32 columns, 512 threads, 16
-            # register-resident synapses per thread, one partial per cluster.
-            assert p["Hp"] == 256 and p["CPB"] == 8 and p["KSB"] == 16 and p["RCB"] == 16
+            # Hp = 256 / 512 chain: Hp/32 members of 32 columns, 512 threads,
+            # Hp/16 synapses per thread, one partial per cluster.
+            assert p["Hp"] in (256, 512) and p["CPB"] == p["Hp"] // 32
+            assert p["KSB"] == 16 and p["RCB"] == p["Hp"] // 16
             assert p["threads_bwd"] == 512
             assert p["NCH"] == p["ode_workgroups_bwd"] // p["CPB"]
         else:
@@ -238,6 +239,7 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     assert (c3["fuse"], c3["CPB"], c3["NBB"], c3["NCH"]) == (1, 8, 8, 32)
     c4 = capi.plan(128, 32, 512, 512, 6)
     assert (c4["CP"], c4["NB"], c4["NCL"], c4["RC"]) == (8, 4, 32, 32)
+    assert (c4["fuse"], c4["CPB"], c4["NBB"], c4["NCH"], c4["RCB"]) == (1, 16, 8, 16, 32)
     assert capi.plan(24, 8, 128, 64, 6)["CP"] == 0      # C1: one workgroup per row
     assert capi.plan(4096, 4, 64, 64, 6)["CP"] == 0     # C5
 

@@ -165,8 +165,8 @@ def test_cluster_path_forward_matches_oracle(shape):
 
 
 @pytest.mark.parametrize("shape", [CLUSTER_SHAPES[0], CLUSTER_SHAPES[3], CLUSTER_SHAPES[4],
-                                   CLUSTER_SHAPES[6], (9, 2, 8, 256, 4, 1),
-                                   (250, 1, 4, 256, 4, 4)],
+                                   CLUSTER_SHAPES[5], CLUSTER_SHAPES[6], (9, 2, 8, 256, 4, 1),
+                                   (250, 1, 4, 256, 4, 4), (9, 2, 8, 500, 8, 1)],
                          ids=lambda s: "B%dT%dD%dH%d" % s[:4])
 def test_cluster_path_backward_matches_oracle(shape):
     B, T, D, H, _, _ = shape
