@@ -47,10 +47,33 @@ int device_cus() {
 // Cluster path (H > 192): CP = Hp/64 workgroups share NB rows, one 64-column
 // slice each, so every operand serves NB rows while up to one workgroup per
 // CU runs. The whole grid must be resident at once (members wait on each
-// other), so it is used only when NCL * CP <= CUs, with 1024 threads and at
-// most 64 KiB of LDS per workgroup (one workgroup fits on any CU).
-// Dynamic LDS of a cluster member, leaving room for its static flag word.
+// other), so it is used only when NCL * CP <= CUs, with at most 1024 threads
+// and at most one CU's LDS per workgroup (one workgroup fits on any CU).
+// Dynamic LDS of a forward cluster member, leaving room for its static flag word.
 constexpr long long kClusterLds = 60 * 1024;
+
+// LDS one workgroup may allocate on the current device (cached per device),
+// less 1 KiB for static variables. Without a device the plan is made for
+// MI355X's 160 KiB.
+long long chain_lds_limit() {
+  constexpr int kMaxDev = 64;
+  static int cache[kMaxDev] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) {
+    (void)hipGetLastError();
+    return 159 * 1024;
+  }
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        n < 65536) {
+      (void)hipGetLastError();
+      n = 65536;
+    }
+    cache[dev] = n;
+  }
+  return cache[dev] - 1024;
+}
 
 // Hp = 256 and 512: the chain runs as clusters of Hp/32 members of 32
 // columns with 512 threads, each thread holding the four gradient sums of its
@@ -62,7 +85,7 @@ void plan_fused_chain(ltc::Plan& p, int ncu) {
   for (int nb : {1, 2, 4, 8}) {
     const int ncl = (p.B + nb - 1) / nb;
     if (ncl > slots) continue;
-    if ((long long)nb * p.Hp * 8 + 16LL * nb * 32 * 4 > kClusterLds) continue;
+    if (ltc::cluster_chain_lds(nb, p.Hp, 16, 32, p.Hp == 256) > chain_lds_limit()) continue;
     p.CPB = cp;
     p.JWB = 32;
     p.NBB = nb;
@@ -84,8 +107,8 @@ bool plan_cluster(ltc::Plan& p, int ncu) {
     for (int ks = 16; ks >= nb && ks >= 8; ks >>= 1) {
       if ((p.Hp / ks) % 8 != 0) continue;  // streamed operands come eight rows at a time
       const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
-      const long long lb = (long long)nb * p.Hp * 8 + (long long)ks * nb * 64 * 4;
-      if (lf > kClusterLds || lb > kClusterLds) continue;
+      if (lf > kClusterLds || ltc::cluster_chain_lds(nb, p.Hp, ks, 64, false) > chain_lds_limit())
+        continue;
       p.CP = cp;
       p.NCL = ncl;
       p.NB = nb;
@@ -1161,7 +1184,8 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8,
-      nbb * p.Hp * 8 + (long long)p.KSB * nbb * colsb * 4,
+      p.CP > 0 ? ltc::cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, ltc::chain_prefetches(p))
+               : nbb * p.Hp * 8 + (long long)p.KSB * nbb * colsb * 4,
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB};

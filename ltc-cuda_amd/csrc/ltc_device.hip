@@ -75,6 +75,13 @@ __device__ __forceinline__ V ks_sum(const V* base, int stride, int KS) {
   return acc;
 }
 
+// KS = 8 or 16 (the cluster kernels): all KS reads in flight together, one
+// LDS round trip, then a fixed pairwise tree.
+template <class V>
+__device__ __forceinline__ V ks_sum_wide(const V* base, int stride, int KS) {
+  return KS == 16 ? tree_sum<16>(base, stride) : tree_sum<8>(base, stride);
+}
+
 // Operand images read through a buffer resource: the wave-uniform row offset
 // is the scalar offset and the lane's column the vector offset, so no
 // per-load address arithmetic runs on the VALU. Reads past `bytes` return 0.
@@ -1250,10 +1257,9 @@ __device__ __forceinline__ unsigned long long xch_get(unsigned long long* w) {
 // x its index in the batch. Returns false if a wait ran out.
 constexpr int kXchBatch = 2;
 
-template <int PER, class Pre, class Deliver>
+template <int PER, int XB = kXchBatch, class Pre, class Deliver>
 __device__ __forceinline__ bool xch_gather(unsigned long long* slot, int p, int nwords, int tid,
                                            int nthr, unsigned tag, Pre&& pre, Deliver&& deliver) {
-  constexpr int XB = kXchBatch;
   for (int e0 = tid; e0 < nwords; e0 += XB * nthr) {
     unsigned long long w[XB];
     int at[XB];
@@ -1374,7 +1380,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
       const unsigned tag = (unsigned)(t * U + u + 1);
       unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
       if (owner) {
-        const float2 nq = ks_sum(red + bo * kClW + o, NB * kClW, KS);
+        const float2 nq = ks_sum_wide(red + bo * kClW + o, NB * kClW, KS);
         const float vold = vs[bo * Hp + c];
         const float den = CG + (nq.y + sdr) + k.eps;
         const float num = C * vold + GL + (nq.x + snr);
@@ -1418,8 +1424,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
 // lower half reads rows [srow0, srow0 + RCS), its upper half the RCS rows
 // after them. The upper half's row offset rides in its per-lane byte offset,
 // so the row walk stays a scalar offset. Rows come four at a time, the next
-// four requested while the current four are evaluated; the prefetch past the
-// chunk reads the next chunk's rows or the image's slack rows.
+// four requested while the current four are evaluated; nothing is requested
+// past the chunk, so no load is left in flight when the phase ends.
 //   jrow0  this thread's first postsynaptic row (for alpha/beta in LDS)
 template <int NB, int RCS>
 __device__ __forceinline__ void chain_fused_stream(__amdgpu_buffer_rsrc_t rs, int lane_bytes,
@@ -1444,8 +1450,10 @@ __device__ __forceinline__ void chain_fused_stream(__amdgpu_buffer_rsrc_t rs, in
                    "+v"(gacc[rr + q].w));
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (rr + 8 < RCS) {  // no prefetch past the chunk: nothing would use it
 #pragma unroll
-    for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + (rr + 8 + q) * rowb);
+      for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + (rr + 8 + q) * rowb);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -1456,6 +1464,31 @@ __device__ __forceinline__ void chain_fused_stream(__amdgpu_buffer_rsrc_t rs, in
     __builtin_amdgcn_sched_barrier(0);
   }
 }
+
+// Copies rows [b0, b0 + NB) of one [B][HP] slice (rows < B only) into LDS
+// [NB][HP] with direct global-to-LDS loads, 16 bytes per lane; a wave fills
+// 1 KiB of LDS per instruction. NT threads take part. Nothing waits here:
+// the caller waits for vmcnt(0) and then a workgroup barrier before it reads
+// the block.
+template <int NB, int HP, int NT>
+__device__ __forceinline__ void rows_to_lds_fixed(const float* slice, int b0, int B, float* dst,
+                                                  int tid) {
+  constexpr int units = NB * HP / 4, upr = HP / 4;
+  const int lane = tid & 63;
+#pragma unroll
+  for (int i = 0; i < (units + NT - 1) / NT; ++i) {
+    const int u0 = i * NT + (tid & ~63);
+    const int u = u0 + lane;
+    if (u < units && b0 + u / upr < B)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(slice + (long long)b0 * HP + 4LL * u),
+          (__attribute__((address_space(3))) void*)(dst + 4 * u0), 16, 0, 0);
+  }
+}
+
+// Waits for this wave's outstanding global loads (and stores), including
+// the direct-to-LDS ones; LDS and export counters are not waited on.
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 struct BwdCK {
   const float4* recB;  // [Hp][Hp] (+ slack rows)
@@ -1492,12 +1525,21 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   static_assert(RCS == 0 || (FUSE && JW == 32 && RCP == 0), "streamed fusion: 32-column members");
   constexpr int NACC = FUSE ? (RCP > 0 ? RCP : RCS) : 1;  // synapses with gradient sums
   constexpr int PER = NB * JW;
+  // Saved forward values through LDS prefetch: only where the synapse phase
+  // issues no loads of its own (register-resident operands), since the load
+  // counter is in order and the prefetch would delay the operands' waits.
+  constexpr bool PF = FUSE && RCP > 0;
+  constexpr int HPC = 16 * NACC;  // Hp of the fused forms (512 threads, 16 chunks)
   extern __shared__ float4 lds4[];
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
   const int RC = RCP > 0 ? RCP : (RCS > 0 ? RCS : k.RC);
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
+  // PF: saved forward values of the cluster's rows, fetched one synapse
+  // phase ahead of use: den of unfold n-1, and v of slots n and n-1.
+  float* pden = red + KS * NB * JW;                     // [NB][Hp]
+  float* pv = pden + NB * Hp;                           // [2][NB][Hp]
   const int tid = threadIdx.x, nthr = blockDim.x;
   // With JW = 64 ks is uniform across each wave; with JW = 32 a wave holds two.
   const int ks = JW == 64 ? __builtin_amdgcn_readfirstlane(tid / JW) : tid / JW;
@@ -1589,6 +1631,10 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     }
     ab[b * Hp + col] = make_float2(al, be);
   }
+  // v of slot n_last, the post-unfold state of unfold n_last - 1.
+  if constexpr (PF)
+    rows_to_lds_fixed<NB, HPC, 512>(k.vsave + n_last * BHp, b0, B, pv + (n_last & 1) * NB * HPC,
+                                    tid);
   lds_barrier();
 
   float cvi[NB];
@@ -1598,6 +1644,15 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
 
   for (long long n = n_last; n >= 0; --n) {
     const int t = (int)(n / U), u = (int)(n - (long long)t * U);
+    // PF: the saved values that unfold n-1's alpha/beta need, in flight
+    // during the synapse phase (v of slot n is already resident).
+    if constexpr (PF) {
+      if (n > 0) {
+        rows_to_lds_fixed<NB, HPC, 512>(k.densave + (n - 1) * BHp, b0, B, pden, tid);
+        rows_to_lds_fixed<NB, HPC, 512>(k.vsave + (n - 1) * BHp, b0, B,
+                                        pv + ((n - 1) & 1) * NB * HPC, tid);
+      }
+    }
     // Output gradient entering at this step boundary (owner only).
     float gnext = 0.f;
     if (n > 0 && u == 0 && live && c < H) gnext = gout_at(bo, t - 1, c);
@@ -1624,16 +1679,19 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     } else {
       static_assert(FUSE || RCP > 0 || JW == 64, "streamed operands need wave-uniform rows");
       const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
-      stream_rows(rsB, c * 16, r0, RC, Hp, [&](const float4 pv, int r) {
-        bwd_synapse_folded<NB>(pv, ab, Hp, r, cvi, acc);
+      stream_rows(rsB, c * 16, r0, RC, Hp, [&](const float4 pw, int r) {
+        bwd_synapse_folded<NB>(pw, ab, Hp, r, cvi, acc);
       });
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) red[(ks * NB + b) * JW + o] = acc[b];
-    // Saved values of unfold n-1, requested now and consumed after the
-    // exchange, whose wait covers their latency.
+    // Without PF: the saved values of unfold n-1, requested now and consumed
+    // after the exchange, whose wait covers their latency.
     float nden = 1.f, nvk = 0.f, nvk1 = 0.f;
-    if (n > 0) {
+    if constexpr (PF) {
+      // The prefetched blocks have long arrived; make them visible to all waves.
+      wait_vm();
+    } else if (n > 0) {
 #pragma unroll
       for (int b = 0; b < NB; ++b)
         acc[b] = b0 + b < B ? k.vsave[((n - 1) * B + b0 + b) * Hp + c] : 0.f;
@@ -1650,7 +1708,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     const unsigned tag = (unsigned)n;
     unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
     if (owner) {
-      const float s = ks_sum(red + bo * JW + o, NB * JW, KS);
+      const float s = ks_sum_wide(red + bo * JW + o, NB * JW, KS);
       g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
       if (u == 0 && live) {
         const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
@@ -1663,18 +1721,41 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
         xch_put(slot + p * PER + bo * JW + o, g, tag);
       }
     }
-    if (n > 0) {
-      float pden[kXchBatch], pvk1[kXchBatch];
-      const bool ok = xch_gather<PER>(
+    if (n > 0 && PF) {
+      const float* vn = pv + (n & 1) * NB * Hp;         // v of slot n
+      const float* vm = pv + ((n - 1) & 1) * NB * Hp;   // v of slot n-1
+      const bool ok = xch_gather<PER, kXchBatch>(
+          slot, p, nwords, tid, nthr, tag, [](int, int) {},
+          [&](int, int a, float gg) {
+            int b, col;
+            word_rc(a, b, col);
+            float al = 0.f, be = 0.f;
+            if (b0 + b < B && col < H) {
+              const float rden = 1.0f / pden[b * Hp + col];
+              al = gg * rden;
+              be = -gg * vn[b * Hp + col] * rden;
+            }
+            ab[b * Hp + col] = make_float2(al, be);
+          });
+      if (!ok) gave_up = 1;
+      if (owner) own_ab(n - 1, pden[bo * Hp + c], vm[bo * Hp + c], vn[bo * Hp + c]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) cvi[b] = b0 + b < B ? vm[b * Hp + c] : 0.f;
+    } else if (n > 0) {
+      // Words in flight per thread: 4 for the streamed fused chain (7.5 words
+      // per thread at Hp = 512; two poll rounds instead of four), else 2.
+      constexpr int XB = (FUSE && RCS > 0) ? 4 : kXchBatch;
+      float pden_[XB], pvk1[XB];
+      const bool ok = xch_gather<PER, XB>(
           slot, p, nwords, tid, nthr, tag,
           [&](int x, int a) {
             int b, col;
             word_rc(a, b, col);
-            pden[x] = 1.f;
+            pden_[x] = 1.f;
             pvk1[x] = 0.f;
             if (b0 + b < B) {
               const long long ee = ((n - 1) * B + b0 + b) * Hp + col;
-              pden[x] = k.densave[ee];
+              pden_[x] = k.densave[ee];
               pvk1[x] = k.vsave[ee + BHp];
             }
           },
@@ -1683,7 +1764,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
             word_rc(a, b, col);
             float al = 0.f, be = 0.f;
             if (b0 + b < B && col < H) {
-              const float rden = 1.0f / pden[x];
+              const float rden = 1.0f / pden_[x];
               al = gg * rden;
               be = -gg * pvk1[x] * rden;
             }
@@ -1789,7 +1870,7 @@ size_t fwd_cl_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * 64 * 8;
 }
 size_t bwd_cl_lds_bytes(const Plan& p) {
-  return (size_t)p.NBB * p.Hp * 8 + (size_t)p.KSB * p.NBB * p.JWB * 4;
+  return (size_t)cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, chain_prefetches(p));
 }
 
 hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s) {

@@ -162,6 +162,16 @@ inline long long cluster_words_bwd(const Plan& p) {
 // Rows of slack after the [Hp][Hp] operand images that the cluster kernels'
 // streamed prefetch may read.
 constexpr int kImageSlackRows = 8;
+// LDS bytes of one cluster chain member: alpha/beta [NB][Hp] float2, the
+// reduction partials [KS][NB][JW], and with `pf` three [NB][Hp] blocks of
+// saved forward values (den of one unfold, v of two slots) prefetched ahead
+// of use.
+inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
+  return (long long)nb * hp * 8 + (long long)ks * nb * jw * 4 + (pf ? 12LL * nb * hp : 0);
+}
+// The cluster chain prefetches saved values when its operands are
+// register-resident: the fused form at Hp = 256.
+inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
 
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
                           const float* state0, float eps, float* out, float* hfin,

@@ -188,7 +188,9 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     p = capi.plan(B, T, D, H, U)
     assert p["Hp"] % 64 == 0 and p["Hp"] >= H and p["Hp"] - H < 64
     assert p["Dp"] % 64 == 0 and p["Dp"] >= D and p["Dp"] - D < 64
-    assert p["lds_fwd"] <= 65536 and p["lds_bwd"] <= 65536
+    assert p["lds_fwd"] <= 65536
+    # the cluster chain may use up to one CU's LDS (160 KiB on MI355X, less 1 KiB)
+    assert p["lds_bwd"] <= (159 * 1024 if p["CP"] > 0 else 65536)
     assert 1 <= p["NRC"] <= 64
     if p["CP"] > 0:
         # Cluster path: CP members of 64 columns each, the whole grid resident
@@ -203,7 +205,7 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         assert p["threads"] == 64 * p["KS"] <= 1024
         assert p["ode_workgroups_bwd"] <= 256 and p["NBB"] in (1, 2, 4, 8)
         assert p["ode_workgroups_bwd"] == p["CPB"] * -(-B // p["NBB"])
-        assert p["KSB"] >= p["NBB"] and p["lds_bwd"] <= 65536
+        assert p["KSB"] >= p["NBB"]
         if p["fuse"]:
             # Hp = 256 / 512 chain: Hp/32 members of 32 columns, 512 threads,
             # Hp/16 synapses per thread, one partial per cluster.
