@@ -15,7 +15,7 @@ Printed: one JSON line with the contract fields, plus
                 its launch stream, against the 157.3 TFLOP/s FP32 peak;
   cpu_baseline  the CPU oracle's TorchScript restatement of the reference path,
                 same module and shapes, timed on this host's cores;
-  large_configs BASELINE configs 3-5 at full size on the GPU (kernel times).
+  large_configs BASELINE configs 2-5 at full size on the GPU (kernel times).
 
 Only rank 0 at N=1 runs; more GPUs are not part of this build.
 """
@@ -44,6 +44,7 @@ REF_GTX1080_MS = 12.7
 
 C1 = dict(B=24, T=8, D=128, H=64, U=6, sparsity=0.5, loss="sum", x="randn")
 LARGE = {
+    "C2": dict(B=32, T=16, D=128, H=128, U=6, sparsity=0.5, loss="sum", x="randn"),
     "C3": dict(B=256, T=64, D=256, H=256, U=6, sparsity=0.5, loss="mse", x="randn"),
     "C4": dict(B=128, T=32, D=512, H=512, U=6, sparsity=1.0, loss="sum", x="uniform3"),
     "C5": dict(B=4096, T=4, D=64, H=64, U=6, sparsity=0.5, loss=None, x="strided"),
@@ -328,7 +329,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-large", action="store_true")
-    ap.add_argument("--profile-pass", choices=["C1", "C3", "C4", "C5"], default=None,
+    ap.add_argument("--profile-pass", choices=["C1", "C2", "C3", "C4", "C5"], default=None,
                     help="for rocprofv3 --pmc: a 64 MiB device copy (calibrates the byte "
                          "counters), then 3 steps of the named config; prints nothing else")
     args = ap.parse_args()

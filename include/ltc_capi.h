@@ -55,8 +55,8 @@ const char* ltc_last_error(void);
 int ltc_device_count(void);
 
 /* Floats in the `saved` buffer that ltc_full_forward fills for backward:
- * the pre-state of every unfold plus the final state, and every unfold's
- * denominator. It replaces the reference's v_buffers_stacked (T,U,B,H) and
+ * the pre-state of every unfold plus the final state, and the reciprocal of
+ * every unfold's denominator. It replaces the reference's v_buffers_stacked (T,U,B,H) and
  * w_num/w_den_sens_stacked (T,B,H) (csrc/ltc_kernels.cu:1207-1211). */
 long long ltc_saved_floats(int B, int T, int H, int ode_unfolds);
 

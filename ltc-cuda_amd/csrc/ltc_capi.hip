@@ -330,7 +330,7 @@ LnWs carve_ln(const ltc::Plan& p, Carver& c) {
 }
 
 long long saved_floats(const ltc::Plan& p) {
-  // vsave: T*U+1 slots of (B,Hp); densave: T*U slots of (B,Hp).
+  // vsave: T*U+1 slots of (B,Hp); densave (1/den): T*U slots of (B,Hp).
   return ((long long)p.T * p.U + 1) * p.B * p.Hp + (long long)p.T * p.U * p.B * p.Hp;
 }
 
@@ -1143,7 +1143,7 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
   e = ltc::launch_copy_rows(w_num_sensory, H, w.f.sn, p.Hp, B, H, s);
   if (e == hipSuccess) e = ltc::launch_copy_rows(w_den_sensory, H, w.f.sd, p.Hp, B, H, s);
   if (e != hipSuccess) return hip_fail("copy launch", e);
-  // The unfold states and denominators, recomputed from v_buffer[0] (the
+  // The unfold states and reciprocal denominators, recomputed from v_buffer[0] (the
   // reference's backward kernels recompute each unfold from its saved
   // pre-state, csrc/ltc_kernels.cu:549-668).
   e = timed(ltc::K_ODE_FWD, s, [&] {

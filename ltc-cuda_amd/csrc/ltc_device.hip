@@ -82,6 +82,19 @@ __device__ __forceinline__ V ks_sum_wide(const V* base, int stride, int KS) {
   return KS == 16 ? tree_sum<16>(base, stride) : tree_sum<8>(base, stride);
 }
 
+// Any KS (a power of two <= 16) in one LDS round trip: for the kernels whose
+// threads finish one or two rows, where the extra registers are free.
+template <class V>
+__device__ __forceinline__ V ks_sum_1r(const V* base, int stride, int KS) {
+  switch (KS) {
+    case 16: return tree_sum<16>(base, stride);
+    case 8: return tree_sum<8>(base, stride);
+    case 4: return tree_sum<4>(base, stride);
+    case 2: return base[0] + base[stride];
+    default: return base[0];
+  }
+}
+
 // Operand images read through a buffer resource: the wave-uniform row offset
 // is the scalar offset and the lane's column the vector offset, so no
 // per-load address arithmetic runs on the VALU. Reads past `bytes` return 0.
@@ -355,17 +368,22 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
-          const float2 nq = ks_sum(red + b * Hp + o, NB * Hp, KS);
+          const float2 nq = NB <= 2 ? ks_sum_1r(red + b * Hp + o, NB * Hp, KS)
+                                    : ks_sum(red + b * Hp + o, NB * Hp, KS);
           const float n = nq.x, q = nq.y;
           const float vold = vs[b * Hp + o];
           const float den = CG + (q + sdr[m]) + k.eps;
           const float num = C * vold + GL + (n + snr[m]);
-          const float vnew = o < H ? num / den : 0.f;
+          // 1/den from v_rcp_f32 (within 1 ulp): the new state is num/den to
+          // about 2 ulp, and the reciprocal is what the backward multiplies
+          // by, so it is saved in place of den.
+          const float rden = __builtin_amdgcn_rcpf(den);
+          const float vnew = o < H ? num * rden : 0.f;
           const bool live = b0 + b < B;
           if (k.vsave != nullptr && live) {
             const long long e = ((long long)(t * U + u) * B + b0 + b) * Hp + o;
             k.vsave[e] = vold;
-            k.densave[e] = den;
+            k.densave[e] = rden;
           }
           vs[b * Hp + o] = vnew;
           if (u == U - 1 && live && o < H) k.out[((long long)(b0 + b) * T + t) * H + o] = vnew;
@@ -453,7 +471,7 @@ __device__ __forceinline__ void bwd_synapse_folded(const float4 p, const float2*
 }
 
 // Operands of unfold n for the synapse phase (all rows, column o) and for the
-// rows this thread finishes (den, v^k, v^{k+1}).
+// rows this thread finishes (1/den, v^k, v^{k+1}).
 template <int NB, int MO>
 __device__ __forceinline__ void bwd_load_unfold(const BwdK& k, long long n, int b0, int ks, int o,
                                                 float (&vi)[NB], float (&den)[MO],
@@ -555,7 +573,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
           float al = 0.f, be = 0.f;
           const bool live = b0 + b < B;
           if (live && o < H) {
-            const float rden = 1.0f / cden[m];
+            const float rden = cden[m];  // saved 1/den
             al = g[m] * rden;
             be = -g[m] * cvk1[m] * rden;
             accA[m] += al;
@@ -593,7 +611,8 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
       for (int m = 0; m < MO; ++m) {
         const int b = ks + m * KS;
         if (b < NB) {
-          const float s = ks_sum(red + b * Hp + o, NB * Hp, KS);
+          const float s = NB <= 2 ? ks_sum_1r(red + b * Hp + o, NB * Hp, KS)
+                                  : ks_sum(red + b * Hp + o, NB * Hp, KS);
           g[m] = o < H ? fmaf(kNegLn2, s, gdir[m]) : 0.f;
         }
       }
@@ -1384,11 +1403,12 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         const float vold = vs[bo * Hp + c];
         const float den = CG + (nq.y + sdr) + k.eps;
         const float num = C * vold + GL + (nq.x + snr);
-        const float vnew = c < H ? num / den : 0.f;
+        const float rden = __builtin_amdgcn_rcpf(den);
+        const float vnew = c < H ? num * rden : 0.f;
         if (k.vsave != nullptr && live) {
           const long long e = ((long long)(t * U + u) * B + b0 + bo) * Hp + c;
           k.vsave[e] = vold;
-          k.densave[e] = den;
+          k.densave[e] = rden;
         }
         vs[bo * Hp + c] = vnew;
         if (u == U - 1 && live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
@@ -1512,7 +1532,7 @@ struct BwdCK {
 // Cluster chain: member p forms dL/dv_i for its JW columns i (reduction over
 // every postsynaptic j) and publishes them; alpha_j/beta_j of the other
 // members' columns are then rebuilt from the published dL/dv_j and the saved
-// den_j, v_j, so only one value per (row, column) crosses the cluster.
+// 1/den_j, v_j, so only one value per (row, column) crosses the cluster.
 // Thread (o, ks): column i = p*JW + o, postsynaptic rows [ks*RC, ks*RC + RC).
 // FUSE (JW = 32, the unfolded image): the thread also accumulates the four
 // recurrent parameter-gradient sums of its synapses over all rows and
@@ -1537,7 +1557,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
   // PF: saved forward values of the cluster's rows, fetched one synapse
-  // phase ahead of use: den of unfold n-1, and v of slots n and n-1.
+  // phase ahead of use: 1/den of unfold n-1, and v of slots n and n-1.
   float* pden = red + KS * NB * JW;                     // [NB][Hp]
   float* pv = pden + NB * Hp;                           // [2][NB][Hp]
   const int tid = threadIdx.x, nthr = blockDim.x;
@@ -1577,7 +1597,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     float al = 0.f, be = 0.f;
     gdir = 0.f;
     if (live && c < H) {
-      const float rden = 1.0f / den;
+      const float rden = den;  // saved 1/den
       al = g * rden;
       be = -g * vk1 * rden;
       accA += al;
@@ -1625,7 +1645,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       float gg = gout_at(b, T - 1, col);
       if (k.ghfin != nullptr) gg += k.ghfin[(long long)(b0 + b) * H + col];
       const long long ee = (n_last * B + b0 + b) * Hp + col;
-      const float rden = 1.0f / k.densave[ee];
+      const float rden = k.densave[ee];  // saved 1/den
       al = gg * rden;
       be = -gg * k.vsave[ee + BHp] * rden;
     }
@@ -1731,7 +1751,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
             word_rc(a, b, col);
             float al = 0.f, be = 0.f;
             if (b0 + b < B && col < H) {
-              const float rden = 1.0f / pden[b * Hp + col];
+              const float rden = pden[b * Hp + col];  // saved 1/den
               al = gg * rden;
               be = -gg * vn[b * Hp + col] * rden;
             }
@@ -1764,7 +1784,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
             word_rc(a, b, col);
             float al = 0.f, be = 0.f;
             if (b0 + b < B && col < H) {
-              const float rden = 1.0f / pden_[x];
+              const float rden = pden_[x];  // saved 1/den
               al = gg * rden;
               be = -gg * pvk1[x] * rden;
             }

@@ -164,7 +164,7 @@ inline long long cluster_words_bwd(const Plan& p) {
 constexpr int kImageSlackRows = 8;
 // LDS bytes of one cluster chain member: alpha/beta [NB][Hp] float2, the
 // reduction partials [KS][NB][JW], and with `pf` three [NB][Hp] blocks of
-// saved forward values (den of one unfold, v of two slots) prefetched ahead
+// saved forward values (1/den of one unfold, v of two slots) prefetched ahead
 // of use.
 inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
   return (long long)nb * hp * 8 + (long long)ks * nb * jw * 4 + (pf ? 12LL * nb * hp : 0);

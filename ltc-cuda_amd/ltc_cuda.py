@@ -11,7 +11,7 @@ stream.
 Differences from the reference, all deliberate:
   * `_cuda_module.ltc_full_forward/backward` keep the reference's argument
     lists and return lists of tensors, but the saved-for-backward set is one
-    opaque `saved` tensor (unfold states and denominators) instead of the
+    opaque `saved` tensor (unfold states and reciprocal denominators) instead of the
     transposed parameter copies and sensory stacks (ltc_cuda.py:281-299).
   * Inputs are validated (device, dtype, shape) and a failing launch raises
     RuntimeError with the library's message; the reference checks nothing.
