@@ -29,10 +29,17 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def command(out: str = LIB_PATH) -> list:
+def source_files() -> list:
+    """Every file the library and the torch extension are built from."""
+    inc = os.path.join(os.path.dirname(HERE), "include", "ltc_capi.h")
+    return [os.path.join(CSRC, s) for s in SOURCES] + [
+        os.path.join(CSRC, "ltc_internal.h"), os.path.join(CSRC, "ltc_torch_ext.cpp"), inc]
+
+
+def command(out: str = LIB_PATH, arch: str = ARCH) -> list:
     return [
         hipcc_path(),
-        f"--offload-arch={ARCH}",
+        f"--offload-arch={arch}",
         "-O3",
         "-std=c++17",
         "-fPIC",
@@ -113,9 +120,11 @@ def build_ext(verbose: bool = False) -> str:
     return out
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, arch: str = ARCH, probe: bool = True) -> str:
+    """Compile libltc_hip.so for `arch`, then the torch extension (and the
+    issue-rate probe unless probe is False); returns the library path."""
     tmp = LIB_PATH + ".tmp"
-    cmd = command(tmp)
+    cmd = command(tmp, arch)
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -127,7 +136,8 @@ def build(verbose: bool = False) -> str:
         print("\n".join(msgs), flush=True)
     os.replace(tmp, LIB_PATH)
     build_ext(verbose)
-    build_probe(verbose)
+    if probe:
+        build_probe(verbose)
     return LIB_PATH
 
 

@@ -15,15 +15,20 @@ Differences from the reference, all deliberate:
     transposed parameter copies and sensory stacks (ltc_cuda.py:281-299).
   * Inputs are validated (device, dtype, shape) and a failing launch raises
     RuntimeError with the library's message; the reference checks nothing.
-  * The library is prebuilt in-tree (`python ltc-cuda_amd/build.py`); a
-    missing or unloadable library leaves `_HAS_CUDA_KERNELS = False` with the
-    reason in `_LOAD_ERROR`, and `ltc.py` then raises for CUDA inputs instead
-    of silently switching paths.
+  * The library is built in-tree (`python ltc-cuda_amd/build.py`). Like the
+    reference, which JIT-compiles with an mtime-checked cache
+    (ltc_cuda.py:138-234), a missing library is built on first use for the
+    visible device (gfx950 only), and a library older than its sources is
+    reported, and rebuilt when LTC_JIT=1 (LTC_JIT=0 never builds). A library
+    that cannot be built or loaded leaves `_HAS_CUDA_KERNELS = False` with
+    the reason in `_LOAD_ERROR`, and `ltc.py` then raises for CUDA inputs
+    instead of silently switching paths.
 """
 
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import logging
 import os
 
@@ -39,8 +44,11 @@ _LOAD_ERROR: str | None = None
 _torch_ext = None
 
 LIB_NAME = "libltc_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ABI_VERSION = 1
+# The one GPU target the kernels are written for.
+TARGET_ARCH = "gfx950"
 
 _f32p = ctypes.c_void_p
 _i64 = ctypes.c_longlong
@@ -573,10 +581,43 @@ def load_capi(path: str = LIB_PATH) -> CApi:
     return capi
 
 
+def device_arch(props) -> str:
+    """gfx target of a device from torch's device properties: the part of
+    `gcnArchName` before its feature flags ('gfx950:sramecc+:xnack-' -> 'gfx950')."""
+    return (getattr(props, "gcnArchName", "") or "").split(":")[0]
+
+
+def _build_script():
+    spec = importlib.util.spec_from_file_location("ltc_build", os.path.join(PKG_DIR, "build.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def stale_sources(lib_path: str, sources) -> list:
+    """Sources modified after the library was built (the reference's cache
+    check compares the same mtimes, ltc_cuda.py:150-160)."""
+    lib_t = os.path.getmtime(lib_path)
+    return [s for s in sources if os.path.isfile(s) and os.path.getmtime(s) > lib_t]
+
+
+def load_action(lib_exists: bool, stale: bool, jit: str) -> str:
+    """What the loader does: 'load', 'build' (none built yet), 'rebuild'
+    (stale and LTC_JIT=1), 'warn' (stale, load it anyway) or 'missing'
+    (none built and LTC_JIT=0)."""
+    if not lib_exists:
+        return "missing" if jit == "0" else "build"
+    if stale:
+        return "rebuild" if jit == "1" else "warn"
+    return "load"
+
+
 def _try_load_hip_kernels() -> bool:
     """Load libltc_hip.so when a HIP device is present (ltc_cuda.py:138-234).
 
-    Never compiles at import time: the library is built in-tree beforehand.
+    A missing library is compiled here (hipcc for the device's gfx target,
+    about a minute) unless LTC_JIT=0; a library older than its sources is
+    rebuilt only when LTC_JIT=1, else loaded with a warning.
     """
     global _HAS_CUDA_KERNELS, _cuda_module, _LOAD_ERROR
     _HAS_CUDA_KERNELS = False
@@ -584,11 +625,36 @@ def _try_load_hip_kernels() -> bool:
     if not torch.cuda.is_available():
         _LOAD_ERROR = "no HIP device visible to torch"
         return False
-    if not os.path.isfile(LIB_PATH):
-        _LOAD_ERROR = (f"{LIB_PATH} not found; build it with "
-                       f"`python {os.path.join(os.path.dirname(LIB_PATH), 'build.py')}`")
+    arch = device_arch(torch.cuda.get_device_properties(torch.cuda.current_device()))
+    if arch and arch != TARGET_ARCH:
+        _LOAD_ERROR = f"device is {arch}; libltc_hip.so is written for {TARGET_ARCH} only"
         logger.warning("LTC HIP kernels unavailable: %s", _LOAD_ERROR)
         return False
+    jit = os.environ.get("LTC_JIT", "")
+    exists = os.path.isfile(LIB_PATH)
+    stale = []
+    if exists:
+        try:
+            stale = stale_sources(LIB_PATH, _build_script().source_files())
+        except (OSError, ImportError) as exc:
+            logger.info("LTC source freshness check skipped: %s", exc)
+    action = load_action(exists, bool(stale), jit)
+    if action == "missing":
+        _LOAD_ERROR = (f"{LIB_PATH} not found (LTC_JIT=0); build it with "
+                       f"`python {os.path.join(PKG_DIR, 'build.py')}`")
+        logger.warning("LTC HIP kernels unavailable: %s", _LOAD_ERROR)
+        return False
+    if action == "warn":
+        logger.warning("LTC: %s is older than %s; rebuild with build.py or set LTC_JIT=1",
+                       LIB_PATH, ", ".join(os.path.basename(p) for p in stale))
+    if action in ("build", "rebuild"):
+        logger.warning("LTC: building %s for %s (first use)", LIB_PATH, arch or TARGET_ARCH)
+        try:
+            _build_script().build(arch=arch or TARGET_ARCH, probe=False)
+        except (OSError, RuntimeError) as exc:
+            _LOAD_ERROR = f"building {LIB_PATH} failed: {exc}"
+            logger.warning("LTC HIP kernels unavailable: %s", _LOAD_ERROR)
+            return False
     try:
         capi = load_capi(LIB_PATH)
         if capi.lib.ltc_device_count() < 1:
