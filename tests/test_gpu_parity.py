@@ -232,6 +232,20 @@ def test_cluster_path_graph_replay_matches_eager():
         torch.cuda.synchronize()
 
 
+def test_long_sequence_backward_matches_oracle():
+    """480 unfolds (T = 80): the chain's one-unfold-ahead operand pipeline and
+    the per-step output-gradient loads over a long reverse walk."""
+    B, T, D, H = 4, 80, 8, 16
+    args = boundary(B, T, D, H, seed=9)
+    dev_args, (out, h, saved) = gpu_forward(args, save=True)
+    g = torch.Generator().manual_seed(10)
+    g_out = torch.randn(B, T, H, generator=g) / T
+    g_h = torch.randn(B, H, generator=g)
+    got = gpu_backward(dev_args, saved, g_out.to(DEV), g_h.to(DEV))
+    ref = oracle_grads(args, g_out, g_h)
+    assert_grads_close(got, ref, "long-sequence backward")
+
+
 def test_backward_expanded_grad_and_no_grad_state():
     """loss = out.sum() hands an expanded (stride-0) gradient and no dL/dh."""
     B, T, D, H = 4, 5, 12, 20
