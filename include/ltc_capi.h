@@ -137,6 +137,8 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
  * (ltc.py:259-307). D <= 1024; larger inputs use ltc_full_forward.
  * `saved` holds ltc_module_saved_floats() floats: the boundary's saved
  * buffer followed by the normalised input and its row statistics.
+ * `state` may be NULL for a zero initial state (the module's default when no
+ * h0 is given), and `grad_state` may then be NULL too (nothing is written).
  */
 long long ltc_module_saved_floats(int B, int T, int D, int H, int ode_unfolds);
 long long ltc_module_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unfolds);

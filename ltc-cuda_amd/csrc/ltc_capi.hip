@@ -672,7 +672,7 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
                            ln_weight, ln_bias, (float)((double)dt / ode_unfolds), ln_eps};
   rc = check_leaves(lp);
   if (rc != LTC_OK) return rc;
-  if (B > 0 && (!state || !h_final)) return fail(LTC_EINVAL, "state/h_final pointer is NULL");
+  if (B > 0 && !h_final) return fail(LTC_EINVAL, "h_final pointer is NULL");
   if ((long long)B * T > 0 && (!x || !out)) return fail(LTC_EINVAL, "x/out pointer is NULL");
   if (save_intermediates && !saved) return fail(LTC_EINVAL, "saved pointer is NULL");
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
@@ -686,9 +686,10 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   if (B == 0) return LTC_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T == 0) {
-    hipError_t e = hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
-                                  hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
+    hipError_t e = state ? hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
+                                          hipMemcpyDeviceToDevice, s)
+                         : hipMemsetAsync(h_final, 0, (size_t)B * H * sizeof(float), s);
+    if (e != hipSuccess) return hip_fail("initial state copy", e);
     return LTC_OK;
   }
   Carver c{static_cast<char*>(workspace)};
@@ -754,7 +755,6 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
       !lg.s_sigma || !lg.gleak || !lg.vleak || !lg.cm || !lg.input_w || !lg.input_b ||
       !lg.ln_w || !lg.ln_b)
     return fail(LTC_EINVAL, "gradient output pointer is NULL");
-  if (B > 0 && !grad_state) return fail(LTC_EINVAL, "grad_state pointer is NULL");
   if ((long long)B * T > 0 && (!x || !grad_out || !grad_x || !saved))
     return fail(LTC_EINVAL, "x/grad_out/grad_x/saved pointer is NULL");
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
@@ -787,7 +787,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
       hipError_t e = hipMemsetAsync(z, 0, (size_t)D * sizeof(float), s);
       if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
     }
-    if (B > 0) {
+    if (B > 0 && grad_state) {
       hipError_t e = grad_h_final
                          ? hipMemcpyAsync(grad_state, grad_h_final, (size_t)B * H * sizeof(float),
                                           hipMemcpyDeviceToDevice, s)

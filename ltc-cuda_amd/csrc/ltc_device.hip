@@ -327,7 +327,8 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
 
   for (int e = tid; e < NB * Hp; e += blockDim.x) {
     const int b = e / Hp, j = e - b * Hp;
-    vs[e] = (b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j] : 0.f;
+    vs[e] = (k.state0 != nullptr && b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j]
+                                                          : 0.f;
   }
   lds_barrier();
 
@@ -642,7 +643,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   for (int m = 0; m < MO; ++m) {
     const int b = ks + m * KS;
     if (b < NB && b0 + b < B) {
-      if (o < H) k.gstate[(long long)(b0 + b) * H + o] = g[m];
+      if (k.gstate != nullptr && o < H) k.gstate[(long long)(b0 + b) * H + o] = g[m];
       float* np = k.npart + (long long)(b0 + b) * 3 * Hp + o;
       np[0] = pC[m];
       np[Hp] = pGv[m];
@@ -1366,7 +1367,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   if (tid == 0) gave_up = 0;
   for (int e = tid; e < NB * Hp; e += nthr) {
     const int b = e / Hp, j = e - b * Hp;
-    vs[e] = (b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j] : 0.f;
+    vs[e] = (k.state0 != nullptr && b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j]
+                                                          : 0.f;
   }
   lds_barrier();
 
@@ -1797,13 +1799,14 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     }
     lds_barrier();
     if (gave_up) {
-      if (live && c < H) k.gstate[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
+      if (k.gstate != nullptr && live && c < H)
+        k.gstate[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
       if (tid == 0) __hip_atomic_store(k.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
   }
   if (live) {
-    if (c < H) k.gstate[(long long)(b0 + bo) * H + c] = g;
+    if (k.gstate != nullptr && c < H) k.gstate[(long long)(b0 + bo) * H + c] = g;
     float* np = k.npart + (long long)(b0 + bo) * 3 * Hp + c;
     np[0] = pC;
     np[Hp] = pGv;

@@ -44,11 +44,15 @@ Workspace workspace(long long bytes, const Tensor& like) {
   return w;
 }
 
+// `state` may be undefined: a zero initial state, read by no kernel.
 void check_inputs(const Tensor& x, const Tensor& state, const std::array<Tensor, kLeaves>& lv) {
-  TORCH_CHECK(x.dim() == 3 && state.dim() == 2 && state.size(0) == x.size(0),
-              "x must be (B, T, D) and state (B, H)");
+  TORCH_CHECK(x.dim() == 3, "x must be (B, T, D)");
   TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat, "LTC HIP kernels are fp32-only");
-  const int64_t D = x.size(2), H = state.size(1);
+  TORCH_CHECK(lv[0].dim() == 2, "w must be (H, H)");
+  const int64_t D = x.size(2), H = lv[0].size(0);
+  TORCH_CHECK(!state.defined() ||
+                  (state.dim() == 2 && state.size(0) == x.size(0) && state.size(1) == H),
+              "state must be (B, H)");
   const int64_t shapes[kLeaves][2] = {{H, H}, {H, H}, {H, H}, {H, H}, {H, H}, {D, H},
                                       {D, H}, {D, H}, {D, H}, {D, H}, {H, -1}, {H, -1},
                                       {H, -1}, {D, -1}, {D, -1}, {D, -1}, {D, -1}};
@@ -61,12 +65,13 @@ void check_inputs(const Tensor& x, const Tensor& state, const std::array<Tensor,
                                         t.size(1) == shapes[i][1]);
     TORCH_CHECK(ok, "LTC parameter ", i, " has shape ", t.sizes());
   }
-  TORCH_CHECK(state.scalar_type() == at::kFloat && state.device() == x.device(),
+  TORCH_CHECK(!state.defined() ||
+                  (state.scalar_type() == at::kFloat && state.device() == x.device()),
               "state must be fp32 on the device of x");
 }
 
 struct LTCModuleFn : public torch::autograd::Function<LTCModuleFn> {
-  static variable_list forward(AutogradContext* ctx, Tensor x, Tensor state, Tensor w,
+  static variable_list forward(AutogradContext* ctx, Tensor x, Tensor state_in, Tensor w,
                                Tensor erev, Tensor mask, Tensor mu, Tensor sigma, Tensor s_w,
                                Tensor s_erev, Tensor s_mask, Tensor s_mu, Tensor s_sigma,
                                Tensor gleak, Tensor vleak, Tensor cm, Tensor input_w,
@@ -75,10 +80,15 @@ struct LTCModuleFn : public torch::autograd::Function<LTCModuleFn> {
     std::array<Tensor, kLeaves> lv = {w,   erev,  mask,  mu,    sigma,   s_w,     s_erev,
                                       s_mask, s_mu, s_sigma, gleak, vleak, cm, input_w,
                                       input_b, ln_w, ln_b};
+    // A 1-d empty state stands for "no initial state" (zeros): autograd
+    // Functions take only defined tensors.
+    const Tensor state = state_in.dim() == 1 && state_in.numel() == 0 ? Tensor() : state_in;
     check_inputs(x, state, lv);
+    // Undefined output gradients stay undefined (no zero-filled tensors).
+    ctx->set_materialize_grads(false);
     for (auto& t : lv) t = contig(t);
-    const Tensor st = contig(state);
-    const int B = (int)x.size(0), T = (int)x.size(1), D = (int)x.size(2), H = (int)st.size(1);
+    const Tensor st = state.defined() ? contig(state) : Tensor();
+    const int B = (int)x.size(0), T = (int)x.size(1), D = (int)x.size(2), H = (int)lv[0].size(0);
     const auto opts = x.options();
     Tensor out = at::empty({B, T, H}, opts);
     Tensor h = at::empty({B, H}, opts);
@@ -122,29 +132,40 @@ struct LTCModuleFn : public torch::autograd::Function<LTCModuleFn> {
     const int U = (int)ctx->saved_data["U"].toInt();
     const double eps = ctx->saved_data["eps"].toDouble();
     const double ln_eps = ctx->saved_data["ln_eps"].toDouble();
-    const int B = (int)x.size(0), T = (int)x.size(1), D = (int)x.size(2), H = (int)st.size(1);
+    const int B = (int)x.size(0), T = (int)x.size(1), D = (int)x.size(2);
+    const int H = (int)sv[2].size(0);
     const auto opts = x.options();
     Tensor go = grads[0].defined() ? grads[0] : at::zeros({B, T, H}, opts);
     if (go.scalar_type() != at::kFloat) go = go.to(at::kFloat);
     Tensor gh;
     if (grads[1].defined()) gh = contig(grads[1].to(at::kFloat));
-    // All gradients in one allocation: x, state, 4 (H,H), 4 (D,H), 3 (H), 4 (D).
-    const int64_t nx = (int64_t)B * T * D, nst = (int64_t)B * H, nhh = (int64_t)H * H,
-                  ndh = (int64_t)D * H;
+    // All gradients in one allocation: x, state (when it was given), 4 (H,H),
+    // 4 (D,H), 3 (H), 4 (D), each a contiguous view (as_strided: one op each).
+    const int64_t nx = (int64_t)B * T * D, nst = st.defined() ? (int64_t)B * H : 0,
+                  nhh = (int64_t)H * H, ndh = (int64_t)D * H;
     Tensor flat = at::empty({nx + nst + 4 * nhh + 4 * ndh + 3 * H + 4 * D}, opts);
     int64_t off = 0;
-    auto take = [&](at::IntArrayRef shape, int64_t n) {
-      Tensor t = flat.narrow(0, off, n).view(shape);
-      off += n;
+    auto take3 = [&](int64_t a, int64_t b, int64_t c) {
+      Tensor t = flat.as_strided({a, b, c}, {b * c, c, 1}, off);
+      off += a * b * c;
       return t;
     };
-    Tensor gx = take({B, T, D}, nx), gst = take({B, H}, nst);
-    Tensor gw = take({H, H}, nhh), gerev = take({H, H}, nhh), gmu = take({H, H}, nhh),
-           gsig = take({H, H}, nhh);
-    Tensor gsw = take({D, H}, ndh), gserev = take({D, H}, ndh), gsmu = take({D, H}, ndh),
-           gssig = take({D, H}, ndh);
-    Tensor ggl = take({H}, H), gvl = take({H}, H), gcm = take({H}, H);
-    Tensor giw = take({D}, D), gib = take({D}, D), glw = take({D}, D), glb = take({D}, D);
+    auto take2 = [&](int64_t a, int64_t b) {
+      Tensor t = flat.as_strided({a, b}, {b, 1}, off);
+      off += a * b;
+      return t;
+    };
+    auto take1 = [&](int64_t a) {
+      Tensor t = flat.as_strided({a}, {1}, off);
+      off += a;
+      return t;
+    };
+    Tensor gx = take3(B, T, D);
+    Tensor gst = st.defined() ? take2(B, H) : Tensor();
+    Tensor gw = take2(H, H), gerev = take2(H, H), gmu = take2(H, H), gsig = take2(H, H);
+    Tensor gsw = take2(D, H), gserev = take2(D, H), gsmu = take2(D, H), gssig = take2(D, H);
+    Tensor ggl = take1(H), gvl = take1(H), gcm = take1(H);
+    Tensor giw = take1(D), gib = take1(D), glw = take1(D), glb = take1(D);
     const Workspace ws = workspace(ltc_module_bwd_workspace_bytes(B, T, D, H, U), x);
     const hipStream_t stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
     const Tensor* lv = &sv[2];
@@ -165,12 +186,14 @@ struct LTCModuleFn : public torch::autograd::Function<LTCModuleFn> {
 };
 
 // Whole-layer fused call: leaves in the order of kLeaves above.
-std::vector<Tensor> module_apply(const Tensor& x, const Tensor& state,
+// `state` None means a zero initial state (passed on as a 1-d empty tensor).
+std::vector<Tensor> module_apply(const Tensor& x, const c10::optional<Tensor>& state,
                                  const std::vector<Tensor>& lv, double dt, int64_t U,
                                  double eps, double ln_eps) {
   TORCH_CHECK(lv.size() == kLeaves, "expected ", kLeaves, " LTC leaves");
   const bool needs_grad = torch::GradMode::is_enabled();
-  auto r = LTCModuleFn::apply(x, state, lv[0], lv[1], lv[2], lv[3], lv[4], lv[5], lv[6], lv[7],
+  const Tensor st = state.has_value() ? *state : at::empty({0}, x.options());
+  auto r = LTCModuleFn::apply(x, st, lv[0], lv[1], lv[2], lv[3], lv[4], lv[5], lv[6], lv[7],
                               lv[8], lv[9], lv[10], lv[11], lv[12], lv[13], lv[14], lv[15],
                               lv[16], dt, U, eps, ln_eps, needs_grad);
   return {r[0], r[1]};

@@ -214,17 +214,15 @@ class TrueLiquidTimeConstant(nn.Module):
         h0 is an (h, c) pair for LSTM API compatibility; only h is used.
         """
         B, T, D = x_seq.shape
-        state = torch.zeros(B, self.hidden_dim, device=x_seq.device, dtype=x_seq.dtype)
-        if h0 is not None:
-            state = h0[0]
-
         force_ts = getattr(self, "_force_torchscript", False)
         on_hip = x_seq.is_cuda and x_seq.dtype == torch.float32 and not force_ts
         if on_hip and self.training and self._module_path_ok(D):
             # Whole layer in two library calls: LayerNorm, affine and the
-            # positivity transforms run inside the fused kernels.
+            # positivity transforms run inside the fused kernels. Without h0
+            # the library starts from a zero state itself (state None).
             ltc_cuda.require_kernels()
-            if state.dtype != x_seq.dtype:
+            state = None if h0 is None else h0[0]
+            if state is not None and state.dtype != x_seq.dtype:
                 state = state.to(x_seq.dtype)
             leaves = [self.w, self.erev, self.sparsity_mask, self.mu, self.sigma,
                       self.sensory_w, self.sensory_erev, self.sensory_sparsity_mask,
@@ -235,6 +233,9 @@ class TrueLiquidTimeConstant(nn.Module):
                 self.input_norm.eps)
             return outputs, (state, state)
 
+        state = torch.zeros(B, self.hidden_dim, device=x_seq.device, dtype=x_seq.dtype)
+        if h0 is not None:
+            state = h0[0]
         x_seq = self.input_norm(x_seq)
         if state.dtype != x_seq.dtype:
             state = state.to(x_seq.dtype)

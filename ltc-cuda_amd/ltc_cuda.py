@@ -557,7 +557,8 @@ class LTCModuleFunction(torch.autograd.Function):
 
 
 def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
-    """Whole-layer fused call; `leaves` in MODULE_LEAVES order.
+    """Whole-layer fused call; `leaves` in MODULE_LEAVES order, `state` None
+    for a zero initial state.
 
     Runs through the C++ autograd Function when the torch extension is built
     (no Python in the per-step forward or backward), else through
@@ -567,6 +568,9 @@ def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
     if _torch_ext is not None:
         return tuple(_torch_ext.module_apply(x_seq, state, list(leaves), float(dt),
                                              int(ode_unfolds), float(epsilon), float(ln_eps)))
+    if state is None:
+        state = torch.zeros(x_seq.shape[0], leaves[0].shape[0], device=x_seq.device,
+                            dtype=torch.float32)
     needs_grad = torch.is_grad_enabled()
     return LTCModuleFunction.apply(x_seq, state, *leaves, float(dt), int(ode_unfolds),
                                    float(epsilon), float(ln_eps), needs_grad)

@@ -190,3 +190,15 @@ def test_fused_path_fails_loudly_without_kernels(monkeypatch):
     z = torch.zeros(1)
     with pytest.raises(RuntimeError, match="not loaded"):
         ltc_cuda.LTCCudaForward.apply(*([z] * 13), 6, 1e-8, False)
+
+
+def test_module_apply_takes_absent_state_to_its_own_checks():
+    """The C++ Function receives no initial state as None (a zero state in the library):
+    autograd must accept it and the call must reach the extension's own input checks."""
+    ext = pytest.importorskip("_ltc_torch")
+    x = torch.randn(2, 3, 4)
+    lv = ([torch.randn(5, 5)] * 5 + [torch.randn(4, 5)] * 5 + [torch.randn(5)] * 3
+          + [torch.randn(4)] * 4)
+    for grad in (False, True):
+        with torch.set_grad_enabled(grad), pytest.raises(RuntimeError, match="fp32-only"):
+            ext.module_apply(x, None, lv, 0.1, 6, 1e-8, 1e-5)

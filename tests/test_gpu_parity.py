@@ -565,6 +565,34 @@ def test_cpp_and_python_module_functions_agree_bitwise():
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("use_ext", [True, False], ids=["cpp", "python"])
+def test_module_path_without_h0_equals_zero_h0(use_ext):
+    """Without h0 the module path passes no state and the library starts from zeros;
+    outputs and leaf gradients must equal those of an explicit zero h0 bitwise."""
+    B, T, D, H = 6, 4, 40, 24
+    m = _perturbed_module(D, H, seed=13).to(DEV)
+    x = torch.randn(B, T, D, device=DEV)
+    G = torch.randn(B, T, H, device=DEV)
+    saved_ext = ltc_cuda._torch_ext
+    if not use_ext:
+        ltc_cuda._torch_ext = None
+    res = []
+    try:
+        for h0 in (None, torch.zeros(B, H, device=DEV)):
+            m.zero_grad(set_to_none=True)
+            out, (h, _) = m(x, None if h0 is None else (h0, h0))
+            ((out * G).sum() + h.sum()).backward()
+            res.append([out.detach(), h.detach()] + [p.grad for p in m.parameters()])
+    finally:
+        ltc_cuda._torch_ext = saved_ext
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+    r_out, r_h, _, _, _ = _oracle_module_grads(m, x.cpu(), torch.zeros(B, H), G.cpu(),
+                                               torch.ones(B, H))
+    assert (res[0][0].cpu().double() - r_out).abs().max().item() <= 1e-3
+    assert (res[0][1].cpu().double() - r_h).abs().max().item() <= 1e-3
+
+
 def test_eval_mode_uses_cached_transforms_like_the_reference():
     """Eval mode keeps the reference's cache semantics: stale after an in-place edit."""
     torch.manual_seed(42)
