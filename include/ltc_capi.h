@@ -136,7 +136,9 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
  * module runs these steps as separate PyTorch ops around the fused call
  * (ltc.py:259-307). D <= 1024; larger inputs use ltc_full_forward.
  * `saved` holds ltc_module_saved_floats() floats: the boundary's saved
- * buffer followed by the normalised input and its row statistics.
+ * buffer followed by the normalised input, its row statistics and the
+ * parameter images built from the leaves at forward time (the backward reads
+ * them instead of rebuilding them, so the leaves must not change in between).
  * `state` may be NULL for a zero initial state (the module's default when no
  * h0 is given), and `grad_state` may then be NULL too (nothing is written).
  */

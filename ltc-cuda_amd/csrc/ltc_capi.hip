@@ -295,12 +295,16 @@ struct BwdWs {
   ltc::PresumBuf ps;
 };
 
-BwdWs carve_bwd(const ltc::Plan& p, Carver& c) {
+// images = false: the caller brings the parameter images (the module path
+// keeps them in its saved buffer).
+BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
   BwdWs w{};
-  w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
-  w.pp.recB = c.take<float4>(image_rows(p) * p.Hp);
-  w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
-  w.pp.neuron = c.take<float>(3LL * p.Hp);
+  if (images) {
+    w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
+    w.pp.recB = c.take<float4>(image_rows(p) * p.Hp);
+    w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
+    w.pp.neuron = c.take<float>(3LL * p.Hp);
+  }
   w.absave = p.FUSE ? nullptr : c.take<float2>(p.N * p.Hp);
   w.dsn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.dsd = c.take<float>((long long)p.B * p.T * p.Hp);
@@ -334,11 +338,25 @@ long long saved_floats(const ltc::Plan& p) {
   return ((long long)p.T * p.U + 1) * p.B * p.Hp + (long long)p.T * p.U * p.B * p.Hp;
 }
 
+// Every parameter image of a training step: the forward builds them all in
+// one launch and the backward reads them from the saved buffer.
+ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
+  ltc::Prepped pp{};
+  pp.recF = c.take<float4>(image_rows(p) * p.Hp);
+  pp.recB = c.take<float4>(image_rows(p) * p.Hp);
+  pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
+  pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
+  pp.neuron = c.take<float>(3LL * p.Hp);
+  return pp;
+}
+
 long long module_saved_floats(const ltc::Plan& p) {
-  // boundary saved buffer, then xa and stats at 64-float (256-byte) alignment
+  // boundary saved buffer, then xa and stats, then the parameter images, each
+  // at 64-float (256-byte) alignment
   Carver c{nullptr};
   c.take<float>(saved_floats(p));
   carve_ln(p, c);
+  carve_images(p, c);
   return (c.off + 3) / 4;
 }
 
@@ -634,7 +652,7 @@ long long ltc_module_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unf
   if (check_dims(B, T, D, H, ode_unfolds) != LTC_OK || D > ltc::kModuleMaxD) return -1;
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
   Carver c{nullptr};
-  carve_bwd(p, c);
+  carve_bwd(p, c, false);
   c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
   return round_up(c.off, 256);
 }
@@ -695,25 +713,31 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   Carver c{static_cast<char*>(workspace)};
   const FwdWs wfw = carve_fwd(p, c);
   LnWs lw = carve_ln(p, c);
+  ltc::Prepped pp = wfw.pp;
+  int images = ltc::kLeafFwdImages;
   float* vsave = nullptr;
   float* densave = nullptr;
   if (save_intermediates) {
+    // Training: LayerNorm rows and every parameter image go to the saved
+    // buffer, so the backward starts with the chain (no image launch).
     vsave = saved;
     densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
     Carver sc{reinterpret_cast<char*>(saved)};
     sc.take<float>(saved_floats(p));
     lw = carve_ln(p, sc);
+    pp = carve_images(p, sc);
+    images |= ltc::kLeafBwdImages;
   }
   const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
   const ltc::Strides3 xas{(long long)T * D, D, 1};
   hipError_t e;
-  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, wfw.pp, false, &ln, s); });
+  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s); });
   if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_SENS_FWD, s,
-            [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, wfw.pp, wfw.sn, wfw.sd, s); });
+            [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, pp, wfw.sn, wfw.sd, s); });
   if (e != hipSuccess) return hip_fail("sensory forward launch", e);
   e = timed(ltc::K_ODE_FWD, s, [&] {
-    return ltc::launch_ode_fwd(p, wfw.pp, wfw.sn, wfw.sd, state, epsilon, out, h_final, vsave,
+    return ltc::launch_ode_fwd(p, pp, wfw.sn, wfw.sd, state, epsilon, out, h_final, vsave,
                                densave, wfw.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
@@ -759,7 +783,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     return fail(LTC_EINVAL, "x/grad_out/grad_x/saved pointer is NULL");
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
   Carver need{nullptr};
-  carve_bwd(p, need);
+  carve_bwd(p, need, false);
   need.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
   if (workspace_bytes < need.off || (need.off > 0 && !workspace))
     return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
@@ -797,19 +821,18 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     return LTC_OK;
   }
   Carver c{static_cast<char*>(workspace)};
-  const BwdWs wb = carve_bwd(p, c);
+  BwdWs wb = carve_bwd(p, c, false);
   float* lnpart = c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
   Carver sc{const_cast<char*>(reinterpret_cast<const char*>(saved))};
   sc.take<float>(saved_floats(p));
   const LnWs lw = carve_ln(p, sc);
+  wb.pp = carve_images(p, sc);  // built by the forward (ltc_module_forward)
   const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
   const ltc::Strides3 xas{(long long)T * D, D, 1};
   const ltc::Strides3 gs{sgb, sgt, sgh};
   const float* vsave = saved;
   const float* densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
   hipError_t e;
-  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, wb.pp, true, nullptr, s); });
-  if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_ODE_BWD, s, [&] {
     return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.absave,
                                wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, wb.cb, s);

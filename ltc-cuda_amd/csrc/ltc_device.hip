@@ -983,9 +983,13 @@ constexpr int kLnPerLane = kModuleMaxD / 64;  // row values each lane keeps
 // LayerNorm + affine of the (b,t) rows in trailing blocks of the same launch:
 // one wave per row, the row held in registers (D <= kModuleMaxD), two-pass
 // mean/variance, xa = ((x - mean)*rstd*ln_w + ln_b)*input_w + input_b.
+// recb: 0 no chain image, 1 plain {S', c', WE, WP} (fused chain), 2 folded
+// {S', c', S'*WE, S'*WP}; sensf / sensb: write the forward / backward
+// sensory image. recF and the neuron vector are always written.
 __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
-                                                        int Hp, int Dp, int bwd, int nprep_blocks,
-                                                        LnBuf ln, int T, int BT) {
+                                                        int Hp, int Dp, int recb, int sensf,
+                                                        int sensb, int nprep_blocks, LnBuf ln,
+                                                        int T, int BT) {
   if ((int)blockIdx.x >= nprep_blocks) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int row = ((int)blockIdx.x - nprep_blocks) * 4 + w;
@@ -1037,9 +1041,10 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
       v = make_float4(-S * kLog2e, S * M * kLog2e, wp * lp.erev[e], wp);
     }
     pp.recF[tid] = v;
-    // bwd == 2: the chain's image carries S'*WE and S'*WP (folded; see
-    // bwd_synapse_folded); bwd == 1 keeps WE, WP for the fused chain.
-    if (bwd) pp.recB[(long long)j * Hp + i] = bwd == 2 ? make_float4(v.x, v.y, v.x * v.z, v.x * v.w) : v;
+    // recb == 2: the chain's image carries S'*WE and S'*WP (folded; see
+    // bwd_synapse_folded); recb == 1 keeps WE, WP for the fused chain.
+    if (recb)
+      pp.recB[(long long)j * Hp + i] = recb == 2 ? make_float4(v.x, v.y, v.x * v.z, v.x * v.w) : v;
     return;
   }
   tid -= nrec;
@@ -1053,10 +1058,8 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
       f = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * Es, Ws);
       g = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Es, Ws * Ss);
     }
-    if (bwd)
-      pp.sensB[(long long)h * Dp + d] = g;
-    else
-      pp.sensF[tid] = f;
+    if (sensb) pp.sensB[(long long)h * Dp + d] = g;
+    if (sensf) pp.sensF[tid] = f;
     return;
   }
   tid -= nsens;
@@ -2115,15 +2118,17 @@ hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpar
   return hipGetLastError();
 }
 
-hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, bool bwd,
+hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
                             const LnBuf* ln, hipStream_t s) {
   const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
   const int nprep = (int)((total + 255) / 256);
   const int BT = p.B * p.T;
   const int nln = ln ? (BT + 3) / 4 : 0;
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
+  const bool bwd = (images & kLeafBwdImages) != 0;
   hipLaunchKernelGGL(prep_leaf_kernel, dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, p.D,
-                     p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, nprep, lb, p.T, BT);
+                     p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, (images & kLeafFwdImages) ? 1 : 0,
+                     bwd ? 1 : 0, nprep, lb, p.T, BT);
   return hipGetLastError();
 }
 

@@ -143,8 +143,11 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
 hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long long dst_ld,
                             long long rows, int cols, hipStream_t s);
 // Module path: images from the leaves; with ln != nullptr the same launch
-// also normalises every (b,t) row of x.
-hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, bool bwd,
+// also normalises every (b,t) row of x. `images` selects the forward
+// (sensF) and backward (recB, sensB) images; recF and neuron are always built.
+constexpr int kLeafFwdImages = 1;
+constexpr int kLeafBwdImages = 2;
+hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
                             const LnBuf* ln, hipStream_t s);
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
