@@ -1115,6 +1115,9 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, co
       if (d < D) {
         float gxa = 0.f;
         const float* pp = dxpart + (long long)row * Dp + d;
+        // Unrolled so that the partials' loads are in flight together (the
+        // adds keep their fixed order).
+#pragma unroll 4
         for (int hb = 0; hb < HB; ++hb) gxa += pp[hb * hstride];
         xh[c] = (xr[d * ln.xs.c] - mean) * rstd;
         const float xn = xh[c] * lw[c] + lb[c];
@@ -2132,9 +2135,9 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   return hipGetLastError();
 }
 
-// Rows per LayerNorm-backward block: one per wave while B*T is small (more
-// blocks in flight), four per wave otherwise (fewer column partials).
-int ln_rows_per_block(const Plan& p) { return (long long)p.B * p.T >= 4096 ? 16 : 4; }
+// Rows per LayerNorm-backward block: one per wave up to 1024 blocks (more
+// loads in flight), four per wave beyond (fewer column partials).
+int ln_rows_per_block(const Plan& p) { return (long long)p.B * p.T > 4096 ? 16 : 4; }
 
 int ln_bwd_blocks(const Plan& p) {
   const int rpb = ln_rows_per_block(p);
