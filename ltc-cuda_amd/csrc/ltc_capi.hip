@@ -1208,7 +1208,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
       (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8,
       p.CP > 0 ? ltc::cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, ltc::chain_prefetches(p))
-               : nbb * p.Hp * 8 + (long long)p.KSB * nbb * colsb * 4,
+               : ltc::chain_lds(p),
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB};

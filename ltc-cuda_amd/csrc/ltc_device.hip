@@ -653,14 +653,26 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   if constexpr (FUSE) {
     // This workgroup's share of the recurrent parameter gradients, synapse
     // (i = o, j = r0 + rr), layout [workgroup][4][i][j] as rec_grad_kernel's.
+    // A thread holds RCP consecutive j of one i, so each plane goes through a
+    // padded [Hp][Hp+1] LDS tile and leaves in whole rows (scattered 16-byte
+    // pieces cost one cache line each).
     const long long HH = (long long)Hp * Hp;
-    float* out = k.rpart + (long long)blockIdx.x * 4 * HH + (long long)o * Hp + r0;
+    float* tile = reinterpret_cast<float*>(lds4);
+    float* out = k.rpart + (long long)blockIdx.x * 4 * HH;
+    const int nthr = blockDim.x;
 #pragma unroll
-    for (int rr = 0; rr < RCP; ++rr) {
-      out[rr] = gacc[rr].x;
-      out[HH + rr] = gacc[rr].y;
-      out[2 * HH + rr] = gacc[rr].z;
-      out[3 * HH + rr] = gacc[rr].w;
+    for (int pl = 0; pl < 4; ++pl) {
+      __syncthreads();  // the LDS is free (chain buffers or the previous plane)
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) {
+        const float4 v = gacc[rr];
+        tile[o * (Hp + 1) + r0 + rr] = pl == 0 ? v.x : pl == 1 ? v.y : pl == 2 ? v.z : v.w;
+      }
+      __syncthreads();
+      for (int e = tid; e < Hp * Hp; e += nthr) {
+        const int i = e / Hp, j = e - i * Hp;
+        out[pl * HH + e] = tile[i * (Hp + 1) + j];
+      }
     }
   }
 }
@@ -1849,9 +1861,7 @@ __global__ __launch_bounds__(256) void clear_words_kernel(unsigned long long* w,
 size_t fwd_lds_bytes(const Plan& p) {
   return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * p.Hp * 8;
 }
-size_t bwd_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 8 + (size_t)p.KSB * p.NB * p.Hp * 4;
-}
+size_t bwd_lds_bytes(const Plan& p) { return (size_t)chain_lds(p); }
 
 template <int NB>
 hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {

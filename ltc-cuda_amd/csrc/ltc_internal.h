@@ -175,6 +175,14 @@ inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.
 inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
+// Dynamic LDS of the single-workgroup chain (ode_bwd_kernel): alpha/beta rows
+// and the KS partials; with FUSE at least one padded [Hp][Hp+1] plane, through
+// which the recurrent-gradient partials are transposed for coalesced stores.
+inline long long chain_lds(const Plan& p) {
+  const long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
+  const long long plane = p.FUSE ? (long long)p.Hp * (p.Hp + 1) * 4 : 0;
+  return base > plane ? base : plane;
+}
 
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,
                           const float* state0, float eps, float* out, float* hfin,

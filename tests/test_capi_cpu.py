@@ -189,8 +189,17 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
     assert p["Hp"] % 64 == 0 and p["Hp"] >= H and p["Hp"] - H < 64
     assert p["Dp"] % 64 == 0 and p["Dp"] >= D and p["Dp"] - D < 64
     assert p["lds_fwd"] <= 65536
-    # the cluster chain may use up to one CU's LDS (160 KiB on MI355X, less 1 KiB)
-    assert p["lds_bwd"] <= (159 * 1024 if p["CP"] > 0 else 65536)
+    # the cluster chain may use up to one CU's LDS (160 KiB on MI355X, less 1 KiB);
+    # the single-workgroup chain its partials under 64 KiB, or with FUSE one padded
+    # [Hp][Hp+1] plane for the transposed gradient stores
+    if p["CP"] > 0:
+        assert p["lds_bwd"] <= 159 * 1024
+    else:
+        Hp, NB, KSB = p["Hp"], p["NB"], p["KSB"]
+        base = NB * Hp * 8 + KSB * NB * Hp * 4
+        assert base <= 65536
+        plane = Hp * (Hp + 1) * 4 if p["fuse"] else 0
+        assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
     assert 1 <= p["NRC"] <= 64
     if p["CP"] > 0:
         # Cluster path: CP members of 64 columns each, the whole grid resident
