@@ -887,6 +887,31 @@ __device__ __forceinline__ float sum_partials(const float* p, long long stride, 
   return acc;
 }
 
+// sum_partials of P planes (plane q at p + q*pstep) with the loads of all
+// planes in flight together; each plane's sum keeps the same order.
+template <int P>
+__device__ __forceinline__ void sum_partials_planes(const float* p, long long pstep,
+                                                    long long stride, int n, float (&acc)[P]) {
+#pragma unroll
+  for (int q = 0; q < P; ++q) acc[q] = 0.f;
+  int z = 0;
+  for (; z + 8 <= n; z += 8) {
+    float v[P][8];
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[q][i] = p[q * pstep + (long long)(z + i) * stride];
+#pragma unroll
+    for (int q = 0; q < P; ++q)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[q] += v[q][i];
+  }
+  for (; z < n; ++z) {
+#pragma unroll
+    for (int q = 0; q < P; ++q) acc[q] += p[q * pstep + (long long)z * stride];
+  }
+}
+
 // First pass of a long partial sum: dst[r][n] = sum of src rows
 // [r*rpb, min(M, (r+1)*rpb)) at column n (row stride `stride`), in row order.
 __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ src,
@@ -909,10 +934,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
     const long long HH = (long long)Hp * Hp;
     const float* src = k.rpart + (long long)i * Hp + j;
-    const float s0 = sum_partials(src, 4 * HH, k.NCH);
-    const float s1 = sum_partials(src + HH, 4 * HH, k.NCH);
-    const float s2 = sum_partials(src + 2 * HH, 4 * HH, k.NCH);
-    const float s3 = sum_partials(src + 3 * HH, 4 * HH, k.NCH);
+    float sp[4];
+    sum_partials_planes<4>(src, HH, 4 * HH, k.NCH, sp);
+    const float s0 = sp[0], s1 = sp[1], s2 = sp[2], s3 = sp[3];
     k.g.w_erev[tid] = s0;
     k.g.w_pos[tid] = s1;
     k.g.mu[tid] = -k.rp.sigma[tid] * s2;
@@ -923,9 +947,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
   if (tid < H) {
     const int j = (int)tid;
     const float* src = k.npart + j;
-    const float c = sum_partials(src, 3LL * Hp, k.B);
-    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
-    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
+    float sp[3];
+    sum_partials_planes<3>(src, Hp, 3LL * Hp, k.B, sp);
+    const float c = sp[0], gv = sp[1], ga = sp[2];
     k.g.cm[j] = c;
     k.g.gleak[j] = k.rp.vleak[j] * ga - gv;
     k.g.vleak[j] = k.rp.gleak[j] * ga;
@@ -937,10 +961,9 @@ __global__ __launch_bounds__(256) void finalize_kernel(FinK k) {
     const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
     const long long DH = (long long)Dp * Hp;
     const float* src = k.spart + (long long)h * Dp + d;
-    const float s1 = sum_partials(src, 4 * DH, k.NRC);
-    const float s2 = sum_partials(src + DH, 4 * DH, k.NRC);
-    const float s3 = sum_partials(src + 2 * DH, 4 * DH, k.NRC);
-    const float s4 = sum_partials(src + 3 * DH, 4 * DH, k.NRC);
+    float sp[4];
+    sum_partials_planes<4>(src, DH, 4 * DH, k.NRC, sp);
+    const float s1 = sp[0], s2 = sp[1], s3 = sp[2], s4 = sp[3];
     const long long e = (long long)d * H + h;
     const float Ws = k.rp.s_wpos[e], Ss = k.rp.s_sigma[e], Ms = k.rp.s_mu[e];
     k.g.s_wpos[e] = s1;
@@ -1201,10 +1224,9 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
     const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
     const long long HH = (long long)Hp * Hp;
     const float* src = k.rpart + (long long)i * Hp + j;
-    const float dwe = sum_partials(src, 4 * HH, k.NCH);
-    const float dwp = sum_partials(src + HH, 4 * HH, k.NCH);
-    const float sd = sum_partials(src + 2 * HH, 4 * HH, k.NCH);
-    const float sdv = sum_partials(src + 3 * HH, 4 * HH, k.NCH);
+    float sp[4];
+    sum_partials_planes<4>(src, HH, 4 * HH, k.NCH, sp);
+    const float dwe = sp[0], dwp = sp[1], sd = sp[2], sdv = sp[3];
     const float wv = k.lp.w[tid], mk = k.lp.mask[tid], ev = k.lp.erev[tid];
     const float wpos = softplus_t(wv) * mk;
     // w_pos feeds the synapse directly and through w_erev = w_pos * erev.
@@ -1219,10 +1241,9 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
     const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
     const long long DH = (long long)Dp * Hp;
     const float* src = k.spart + (long long)h * Dp + d;
-    const float s1 = sum_partials(src, 4 * DH, k.NRC);
-    const float s2 = sum_partials(src + DH, 4 * DH, k.NRC);
-    const float s3 = sum_partials(src + 2 * DH, 4 * DH, k.NRC);
-    const float s4 = sum_partials(src + 3 * DH, 4 * DH, k.NRC);
+    float sp[4];
+    sum_partials_planes<4>(src, DH, 4 * DH, k.NRC, sp);
+    const float s1 = sp[0], s2 = sp[1], s3 = sp[2], s4 = sp[3];
     const long long e = (long long)d * H + h;
     const float sw = k.lp.s_w[e], mk = k.lp.s_mask[e];
     const float Ws = softplus_t(sw) * mk, Ss = k.lp.s_sigma[e], Ms = k.lp.s_mu[e];
@@ -1236,9 +1257,9 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
   if (tid < H) {
     const int j = (int)tid;
     const float* src = k.npart + j;
-    const float c = sum_partials(src, 3LL * Hp, k.B);
-    const float gv = sum_partials(src + Hp, 3LL * Hp, k.B);
-    const float ga = sum_partials(src + 2 * Hp, 3LL * Hp, k.B);
+    float sp[3];
+    sum_partials_planes<3>(src, Hp, 3LL * Hp, k.B, sp);
+    const float c = sp[0], gv = sp[1], ga = sp[2];
     const float gl = k.lp.gleak[j];
     k.g.cm[j] = c / k.lp.dtU * softplus_grad(k.lp.cm[j]);
     k.g.gleak[j] = (k.lp.vleak[j] * ga - gv) * softplus_grad(gl);
@@ -1249,10 +1270,12 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
   if (tid < D) {
     const int d = (int)tid;
     const float* src = k.lnpart + d;
-    k.g.input_w[d] = sum_partials(src, 4LL * Dp, k.NLN);
-    k.g.input_b[d] = sum_partials(src + Dp, 4LL * Dp, k.NLN);
-    k.g.ln_w[d] = sum_partials(src + 2 * Dp, 4LL * Dp, k.NLN);
-    k.g.ln_b[d] = sum_partials(src + 3 * Dp, 4LL * Dp, k.NLN);
+    float sp[4];
+    sum_partials_planes<4>(src, Dp, 4LL * Dp, k.NLN, sp);
+    k.g.input_w[d] = sp[0];
+    k.g.input_b[d] = sp[1];
+    k.g.ln_w[d] = sp[2];
+    k.g.ln_b[d] = sp[3];
   }
 }
 
