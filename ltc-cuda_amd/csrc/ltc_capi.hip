@@ -201,6 +201,12 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
   // the chain kernel also accumulates the recurrent parameter gradients and
   // writes one partial per workgroup.
   p.FUSE = ltc::ode_fuse_ok(p.NB, p.RCB);
+  // One row at Hp = 64: the single-row fused chain with 8 waves of 8 synapses.
+  if (p.NB == 1 && p.Hp == 64) {
+    p.KSB = 8;
+    p.RCB = 8;
+    p.FUSE = true;
+  }
   p.CP = p.NCL = 0;
   p.CPB = p.NBB = p.NCLB = 0;
   p.JWB = 64;
@@ -1206,7 +1212,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const long long nbb = p.CP > 0 ? p.NBB : p.NB;
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
-      (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8,
+      p.CP > 0 ? (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8 : ltc::fwd_lds(p),
       p.CP > 0 ? ltc::cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, ltc::chain_prefetches(p))
                : ltc::chain_lds(p),
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,

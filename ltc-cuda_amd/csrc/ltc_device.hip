@@ -678,6 +678,206 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 }
 
 // ---------------------------------------------------------------------------
+// Single-row kernels at Hp = 64 (NB = 1: one wave spans all columns).
+// Every wave keeps the row's per-column state in lane o and updates it from
+// the same KS partials in the same fixed order, so the copies agree bitwise;
+// a wave reads the values of its own synapse rows with v_readlane instead of
+// through LDS. That leaves one barrier per unfold: the partials alternate
+// between two LDS buffers by unfold parity, and a buffer is rewritten two
+// unfolds later, after every wave has passed the barrier that follows its
+// reads. The forward's results are bitwise those of ode_fwd_kernel; the
+// chain's match ode_bwd_kernel's to the rounding of the multiply-adds the
+// compiler contracts differently in the two bodies.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+template <int RCP>
+__global__ __launch_bounds__(1024) void ode_fwd_row_kernel(FwdK k) {
+  constexpr int HP = 64, KS = HP / RCP;
+  extern __shared__ float4 lds4[];
+  float2* red = reinterpret_cast<float2*>(lds4);  // [2][KS][64]
+  const int H = k.H, B = k.B, T = k.T, U = k.U;
+  const int tid = threadIdx.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  const int b0 = blockIdx.x;
+  const int r0 = ks * RCP;
+  const bool col = o < H;
+  const float C = k.neuron[o], G = k.neuron[HP + o], L = k.neuron[2 * HP + o];
+  const float GL = G * L, CG = C + G;
+  float4 preg[RCP];
+#pragma unroll
+  for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * HP + o];
+  float v = (k.state0 != nullptr && col) ? k.state0[(long long)b0 * H + o] : 0.f;
+  float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
+  auto load_sens = [&](int t, float& a, float& d) {
+    const long long e = ((long long)b0 * T + t) * HP + o;
+    a = k.sn[e];
+    d = k.sd[e];
+  };
+  if (T > 0) load_sens(0, snr, sdr);
+  int par = 0;
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) load_sens(t + 1, snn, sdn);
+    for (int u = 0; u < U; ++u) {
+      float na = 0.f, qa = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) {
+        const float4 p = preg[rr];
+        const float a = gate(fmaf(p.x, lane_value(v, r0 + rr), p.y));
+        na = fmaf(a, p.z, na);
+        qa = fmaf(a, p.w, qa);
+      }
+      float2* rb = red + par * KS * HP;
+      rb[ks * HP + o] = make_float2(na, qa);
+      lds_barrier();
+      const float2 nq = tree_sum<KS>(rb + o, HP);
+      const float den = CG + (nq.y + sdr) + k.eps;
+      const float num = C * v + GL + (nq.x + snr);
+      const float rden = __builtin_amdgcn_rcpf(den);
+      const float vnew = col ? num * rden : 0.f;
+      if (ks == 0) {
+        if (k.vsave != nullptr) {
+          const long long e = ((long long)(t * U + u) * B + b0) * HP + o;
+          k.vsave[e] = v;
+          k.densave[e] = rden;
+        }
+        if (u == U - 1 && col) k.out[((long long)b0 * T + t) * H + o] = vnew;
+      }
+      v = vnew;
+      par ^= 1;
+    }
+    snr = snn;
+    sdr = sdn;
+  }
+  if (ks == 0) {
+    if (col) k.hfin[(long long)b0 * H + o] = v;
+    if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0) * HP + o] = v;
+  }
+}
+
+// Fused chain (FUSE) of one row at Hp = 64: thread (ks, o) holds the RCP
+// synapses (i = o, j = ks*RCP + rr) with their four gradient sums. Launched
+// with RCP = 8 (8 waves): measured 44 us against 45.5 us at RCP = 4 (C1).
+template <int RCP>
+__global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
+  constexpr int HP = 64, KS = HP / RCP;
+  extern __shared__ float4 lds4[];
+  float* red = reinterpret_cast<float*>(lds4);  // [2][KS][64]
+  const int H = k.H, B = k.B, T = k.T, U = k.U;
+  const int tid = threadIdx.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  const int b0 = blockIdx.x;
+  const int r0 = ks * RCP;
+  const bool col = o < H;
+  const float C = k.neuron[o];
+  float4 preg[RCP], gacc[RCP];
+#pragma unroll
+  for (int rr = 0; rr < RCP; ++rr) {
+    preg[rr] = k.recB[(long long)(r0 + rr) * HP + o];
+    gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + o] : 0.f;
+  float pC = 0.f, pGv = 0.f, pA = 0.f;
+  if (T == 0) return;
+  const long long BHp = (long long)B * HP;
+  // Saved pre-state v^k (also v_i of the synapses), 1/den and v^{k+1} of
+  // column o for unfold n, software-pipelined one unfold ahead.
+  auto load = [&](long long n, float& vk, float& rd, float& vk1) {
+    const long long e = (n * B + b0) * HP + o;
+    vk = k.vsave[e];
+    rd = col ? k.densave[e] : 1.f;
+    vk1 = k.vsave[e + BHp];
+  };
+  auto gout = [&](int t) {
+    return col ? k.gout[(long long)b0 * k.gs.b + (long long)t * k.gs.t + (long long)o * k.gs.c]
+               : 0.f;
+  };
+  float cvk, crd, cvk1, nvk = 0.f, nrd = 1.f, nvk1 = 0.f;
+  load((long long)T * U - 1, cvk, crd, cvk1);
+  float gcur = gout(T - 1), gnext = 0.f;
+  int par = 0;
+  for (int t = T - 1; t >= 0; --t) {
+    if (t > 0) gnext = gout(t - 1);
+    float accA = 0.f, accB = 0.f;
+    g += gcur;
+    for (int u = U - 1; u >= 0; --u) {
+      const long long n = (long long)t * U + u;
+      if (n > 0) load(n - 1, nvk, nrd, nvk1);
+      float al = 0.f, be = 0.f;
+      if (col) {
+        al = g * crd;  // saved 1/den
+        be = -g * cvk1 * crd;
+      }
+      accA += al;
+      accB += be;
+      pC += al * (cvk - cvk1);
+      pGv += al * cvk1;
+      pA += al;
+      const float gdir = al * C;
+      float acc = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) {
+        const float4 p = preg[rr];
+        const float cx = lane_value(al, r0 + rr), cy = lane_value(be, r0 + rr);
+        const float a = gate(fmaf(p.x, cvk, p.y));
+        const float a2 = fmaf(-a, a, a);
+        const float dl = fmaf(cx, p.z, cy * p.w) * a2;
+        acc = fmaf(dl, p.x, acc);
+        gacc[rr].x = fmaf(cx, a, gacc[rr].x);
+        gacc[rr].y = fmaf(cy, a, gacc[rr].y);
+        gacc[rr].z += dl;
+        gacc[rr].w = fmaf(dl, cvk, gacc[rr].w);
+      }
+      float* rb = red + par * KS * HP;
+      rb[ks * HP + o] = acc;
+      lds_barrier();
+      const float s = tree_sum<KS>(rb + o, HP);
+      g = col ? fmaf(kNegLn2, s, gdir) : 0.f;
+      par ^= 1;
+      if (n > 0) {
+        cvk = nvk;
+        crd = nrd;
+        cvk1 = nvk1;
+      }
+    }
+    if (ks == 0) {
+      const long long e = ((long long)b0 * T + t) * HP + o;
+      k.dsn[e] = accA;
+      k.dsd[e] = accB;
+    }
+    gcur = gnext;
+  }
+  if (ks == 0) {
+    if (k.gstate != nullptr && col) k.gstate[(long long)b0 * H + o] = g;
+    float* np = k.npart + (long long)b0 * 3 * HP + o;
+    np[0] = pC;
+    np[HP] = pGv;
+    np[2 * HP] = pA;
+  }
+  // Recurrent-gradient partials through a padded [64][65] LDS tile, whole
+  // rows out (layout [workgroup][4][i][j], as ode_bwd_kernel's).
+  constexpr long long HH = (long long)HP * HP;
+  float* tile = reinterpret_cast<float*>(lds4);
+  float* out = k.rpart + (long long)blockIdx.x * 4 * HH;
+#pragma unroll
+  for (int pl = 0; pl < 4; ++pl) {
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const float4 w = gacc[rr];
+      tile[o * (HP + 1) + r0 + rr] = pl == 0 ? w.x : pl == 1 ? w.y : pl == 2 ? w.z : w.w;
+    }
+    __syncthreads();
+    for (int e = tid; e < HP * HP; e += blockDim.x) {
+      const int i = e >> 6, j = e & 63;
+      out[pl * HH + e] = tile[i * (HP + 1) + j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Recurrent parameter gradients, reduced over n = (t,k,b).
 // grid (Hp/64, Hp/32, NCH), block 256: lane -> j, wave w -> 8 presynaptic i.
 // Per synapse and n:  a = gate, a2 = a(1-a), h = alpha*WE + beta*WP,
@@ -1881,9 +2081,7 @@ __global__ __launch_bounds__(256) void clear_words_kernel(unsigned long long* w,
 // ---------------------------------------------------------------------------
 // Template dispatch helpers.
 // ---------------------------------------------------------------------------
-size_t fwd_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * p.Hp * 8;
-}
+size_t fwd_lds_bytes(const Plan& p) { return (size_t)fwd_lds(p); }
 size_t bwd_lds_bytes(const Plan& p) { return (size_t)chain_lds(p); }
 
 template <int NB>
@@ -1891,6 +2089,14 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KS);
   const size_t lds = fwd_lds_bytes(p);
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
+  if constexpr (NB == 1) {
+    if (row_kernels(p) && rcp > 0) {
+      if (rcp == 4) hipLaunchKernelGGL((ode_fwd_row_kernel<4>), grid, block, lds, s, a);
+      else if (rcp == 8) hipLaunchKernelGGL((ode_fwd_row_kernel<8>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((ode_fwd_row_kernel<16>), grid, block, lds, s, a);
+      return hipGetLastError();
+    }
+  }
   switch (rcp) {
     case 4: hipLaunchKernelGGL((ode_fwd_kernel<NB, 4>), grid, block, lds, s, a); break;
     case 8: hipLaunchKernelGGL((ode_fwd_kernel<NB, 8>), grid, block, lds, s, a); break;
@@ -1906,6 +2112,12 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   const size_t lds = bwd_lds_bytes(p);
   const int rcp = (p.RCB == 4 || p.RCB == 8 || p.RCB == 16) ? p.RCB : 0;
 #define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
+  if constexpr (NB == 1) {
+    if (row_kernels(p) && p.FUSE && rcp == 8) {
+      hipLaunchKernelGGL((ode_bwd_row_kernel<8>), grid, block, lds, s, a);
+      return hipGetLastError();
+    }
+  }
   if (p.FUSE) {
     // Only the spill-free pairs of ode_fuse_ok() are instantiated.
     if constexpr (ode_fuse_ok(NB, 8)) {

@@ -175,11 +175,25 @@ inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.
 inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
+// One row per workgroup at Hp = 64: the single-row kernels (every wave keeps
+// the row's state, one barrier per unfold, partials double-buffered).
+inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp == 64; }
+
+// Dynamic LDS of the single-workgroup forward: state rows and the KS
+// partials, or the single-row kernel's two partial buffers.
+inline long long fwd_lds(const Plan& p) {
+  const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8;
+  const long long row = row_kernels(p) ? 2LL * p.KS * p.Hp * 8 : 0;
+  return base > row ? base : row;
+}
+
 // Dynamic LDS of the single-workgroup chain (ode_bwd_kernel): alpha/beta rows
-// and the KS partials; with FUSE at least one padded [Hp][Hp+1] plane, through
-// which the recurrent-gradient partials are transposed for coalesced stores.
+// and the KS partials (two buffers in the single-row kernel); with FUSE at
+// least one padded [Hp][Hp+1] plane, through which the recurrent-gradient
+// partials are transposed for coalesced stores.
 inline long long chain_lds(const Plan& p) {
-  const long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
+  long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
+  if (row_kernels(p) && 2LL * p.KSB * p.Hp * 4 > base) base = 2LL * p.KSB * p.Hp * 4;
   const long long plane = p.FUSE ? (long long)p.Hp * (p.Hp + 1) * 4 : 0;
   return base > plane ? base : plane;
 }
