@@ -224,10 +224,16 @@ class TrueLiquidTimeConstant(nn.Module):
             state = None if h0 is None else h0[0]
             if state is not None and state.dtype != x_seq.dtype:
                 state = state.to(x_seq.dtype)
-            leaves = [self.w, self.erev, self.sparsity_mask, self.mu, self.sigma,
-                      self.sensory_w, self.sensory_erev, self.sensory_sparsity_mask,
-                      self.sensory_mu, self.sensory_sigma, self.gleak, self.vleak, self.cm,
-                      self.input_w, self.input_b, self.input_norm.weight, self.input_norm.bias]
+            # Straight from the registries (nn.Module attribute access costs a
+            # __getattr__ call per name, ~0.3 us each on this per-step path).
+            P, Bf = self._parameters, self._buffers
+            NP = self._modules["input_norm"]._parameters
+            leaves = [P["w"], P["erev"], Bf["sparsity_mask"], P["mu"], P["sigma"],
+                      P["sensory_w"], P["sensory_erev"], Bf["sensory_sparsity_mask"],
+                      P["sensory_mu"], P["sensory_sigma"], P["gleak"], P["vleak"], P["cm"],
+                      P["input_w"] if "input_w" in P else Bf["input_w"],
+                      P["input_b"] if "input_b" in P else Bf["input_b"],
+                      NP["weight"], NP["bias"]]
             outputs, state = ltc_cuda.ltc_module_forward(
                 x_seq, state, leaves, self.dt, self.ode_unfolds, self.epsilon,
                 self.input_norm.eps)
