@@ -21,10 +21,11 @@ constexpr int ode_owned_rows(int nb) { return nb <= 2 ? nb : nb / 4; }
 // (NB, RC) pairs whose chain kernel can also keep the four recurrent
 // gradient accumulators of every register-resident operand without spilling
 // at the register budget __launch_bounds__(ode_max_threads(NB)) leaves
-// (checked against the compiled code objects: zero scratch).
+// (checked against the compiled code objects: zero scratch). One row at
+// Hp = 64 uses the single-row chain instead (ode_bwd_row_kernel).
 constexpr bool ode_fuse_ok(int nb, int rc) {
-  return (nb == 1 && rc == 4) || (nb == 4 && (rc == 4 || rc == 8)) ||
-         (nb == 8 && (rc == 4 || rc == 8)) || (nb == 16 && rc == 4);
+  return (nb == 4 && (rc == 4 || rc == 8)) || (nb == 8 && (rc == 4 || rc == 8)) ||
+         (nb == 16 && rc == 4);
 }
 
 // Kernel ids for the optional event-timing facility.
