@@ -1648,6 +1648,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         const float num = C * vold + GL + (nq.x + snr);
         const float rden = __builtin_amdgcn_rcpf(den);
         const float vnew = c < H ? num * rden : 0.f;
+        // Publish first: the partners wait on it, the other stores on nothing.
+        xch_put(slot + p * PER + bo * kClW + o, vnew, tag);
         if (k.vsave != nullptr && live) {
           const long long e = ((long long)(t * U + u) * B + b0 + bo) * Hp + c;
           k.vsave[e] = vold;
@@ -1655,7 +1657,6 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         }
         vs[bo * Hp + c] = vnew;
         if (u == U - 1 && live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
-        xch_put(slot + p * PER + bo * kClW + o, vnew, tag);
       }
       const bool ok = xch_gather<PER>(
           slot, p, nwords, tid, nthr, tag, [](int, int) {},
@@ -1973,16 +1974,17 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     if (owner) {
       const float s = ks_sum_wide(red + bo * JW + o, NB * JW, KS);
       g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
+      // Publish first: the partners wait on it, the other stores on nothing.
+      if (n > 0) {
+        g += gnext;
+        xch_put(slot + p * PER + bo * JW + o, g, tag);
+      }
       if (u == 0 && live) {
         const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
         k.dsn[e] = accA;
         k.dsd[e] = accB;
       }
       if (u == 0) accA = accB = 0.f;
-      if (n > 0) {
-        g += gnext;
-        xch_put(slot + p * PER + bo * JW + o, g, tag);
-      }
     }
     if (n > 0 && PF) {
       const float* vn = pv + (n & 1) * NB * Hp;         // v of slot n
