@@ -212,18 +212,32 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
 #pragma unroll
   for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
 
-  for (int d0 = 0; d0 < D; d0 += 64) {
-    for (int e = threadIdx.x; e < 64 * ROWS; e += 256) {
+  // The x values of a 64-input chunk are loaded into registers one chunk
+  // ahead, so the loads travel while the previous chunk is evaluated.
+  constexpr int NXF = (64 * ROWS + 255) / 256;
+  float xv[NXF];
+  auto fetch = [&](int d0) {
+#pragma unroll
+    for (int i = 0; i < NXF; ++i) {
+      const int e = threadIdx.x + i * 256;
       const int r = e >> 6, dd = e & 63;
       const int row = row0 + r, d = d0 + dd;
-      float v = 0.f;
-      if (row < BT && d < D) {
+      xv[i] = 0.f;
+      if (e < 64 * ROWS && row < BT && d < D) {
         const int b = row / T, t = row - b * T;
-        v = x[b * xs.b + t * xs.t + d * xs.c];
+        xv[i] = x[b * xs.b + t * xs.t + d * xs.c];
       }
-      xsh[dd * XLD + r] = v;
+    }
+  };
+  fetch(0);
+  for (int d0 = 0; d0 < D; d0 += 64) {
+#pragma unroll
+    for (int i = 0; i < NXF; ++i) {
+      const int e = threadIdx.x + i * 256;
+      if (e < 64 * ROWS) xsh[(e & 63) * XLD + (e >> 6)] = xv[i];
     }
     __syncthreads();
+    if (d0 + 64 < D) fetch(d0 + 64);
     const int dn = min(64, D - d0);
     const int dlo = DS == 1 ? 0 : w * (64 / DS);
     const int dhi = DS == 1 ? dn : min(dn, dlo + 64 / DS);
@@ -993,29 +1007,51 @@ __global__ __launch_bounds__(256) void sens_bwd_kernel(SensBK k) {
 
   const int rb = blockIdx.z * k.rows_per;
   const int re = min(k.BT, rb + k.rows_per);
-  for (int r0 = rb; r0 < re; r0 += SB_RT) {
+  // A chunk's staged values (dL/dsn, dL/dsd of its rows for this block's 32
+  // neurons, and its x rows) are loaded into registers one chunk ahead, so
+  // the loads travel while the previous chunk is evaluated.
+  constexpr int NA = SB_RT * 32 / 256, NX = SB_RT * 64 / 256;
+  float2 na[NA];
+  float nx[NX];
+  auto fetch = [&](int r0) {
     const int cnt = min(SB_RT, re - r0);
-    for (int e = threadIdx.x; e < SB_RT * 32; e += 256) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int e = threadIdx.x + i * 256;
       const int rr = e >> 5, hh = e & 31;
-      const int row = r0 + rr;
-      float2 v = make_float2(0.f, 0.f);
+      na[i] = make_float2(0.f, 0.f);
       if (rr < cnt) {
-        const long long ix = (long long)row * Hp + hb * 32 + hh;
-        v = make_float2(k.dsn[ix], k.dsd[ix]);
+        const long long ix = (long long)(r0 + rr) * Hp + hb * 32 + hh;
+        na[i] = make_float2(k.dsn[ix], k.dsd[ix]);
       }
-      absh[rr][hh] = v;
     }
-    for (int e = threadIdx.x; e < SB_RT * 64; e += 256) {
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int e = threadIdx.x + i * 256;
       const int rr = e >> 6, dd = e & 63;
       const int row = r0 + rr, dg = db + dd;
-      float v = 0.f;
+      nx[i] = 0.f;
       if (rr < cnt && dg < k.D) {
         const int b = row / k.T, t = row - b * k.T;
-        v = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+        nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
       }
-      xsh[rr][dd] = v;
+    }
+  };
+  if (rb < re) fetch(rb);
+  for (int r0 = rb; r0 < re; r0 += SB_RT) {
+    const int cnt = min(SB_RT, re - r0);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int e = threadIdx.x + i * 256;
+      absh[e >> 5][e & 31] = na[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int e = threadIdx.x + i * 256;
+      xsh[e >> 6][e & 63] = nx[i];
     }
     __syncthreads();
+    if (r0 + SB_RT < re) fetch(r0 + SB_RT);
     for (int rr = 0; rr < cnt; ++rr) {
       const float xv = xsh[rr][lane];
       float dxp = 0.f;
