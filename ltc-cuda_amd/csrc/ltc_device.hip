@@ -925,18 +925,39 @@ __global__ __launch_bounds__(256) void rec_grad_kernel(RecGK k) {
 
   const long long nb = (long long)blockIdx.z * k.nper;
   const long long ne = min(k.N, nb + k.nper);
-  for (long long n0 = nb; n0 < ne; n0 += RG_NT) {
-    for (int e = threadIdx.x; e < RG_NT * 32; e += 256) {
-      const int nn = e >> 5, ii = e & 31;
-      const long long n = n0 + nn;
-      vsh[nn][ii] = n < ne ? k.vsave[n * Hp + ib + ii] : 0.f;
+  // A chunk's v_i and alpha/beta rows are loaded into registers one chunk
+  // ahead, so the loads travel while the previous chunk is evaluated.
+  constexpr int NV = RG_NT * 32 / 256, NA = RG_NT * 64 / 256;
+  float nv[NV];
+  float2 nab[NA];
+  auto fetch = [&](long long n0) {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int e = threadIdx.x + q * 256;
+      const long long n = n0 + (e >> 5);
+      nv[q] = n < ne ? k.vsave[n * Hp + ib + (e & 31)] : 0.f;
     }
-    for (int e = threadIdx.x; e < RG_NT * 64; e += 256) {
-      const int nn = e >> 6, jj = e & 63;
-      const long long n = n0 + nn;
-      absh[nn][jj] = n < ne ? k.absave[n * Hp + jb + jj] : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const int e = threadIdx.x + q * 256;
+      const long long n = n0 + (e >> 6);
+      nab[q] = n < ne ? k.absave[n * Hp + jb + (e & 63)] : make_float2(0.f, 0.f);
+    }
+  };
+  if (nb < ne) fetch(nb);
+  for (long long n0 = nb; n0 < ne; n0 += RG_NT) {
+#pragma unroll
+    for (int q = 0; q < NV; ++q) {
+      const int e = threadIdx.x + q * 256;
+      vsh[e >> 5][e & 31] = nv[q];
+    }
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+      const int e = threadIdx.x + q * 256;
+      absh[e >> 6][e & 63] = nab[q];
     }
     __syncthreads();
+    if (n0 + RG_NT < ne) fetch(n0 + RG_NT);
     const int cnt = (int)min((long long)RG_NT, ne - n0);
     for (int nn = 0; nn < cnt; ++nn) {
       const float2 c = absh[nn][lane];
