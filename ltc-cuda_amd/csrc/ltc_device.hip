@@ -213,31 +213,40 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
   for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
 
   // The x values of a 64-input chunk are loaded into registers one chunk
-  // ahead, so the loads travel while the previous chunk is evaluated.
-  constexpr int NXF = (64 * ROWS + 255) / 256;
+  // ahead, so the loads travel while the previous chunk is evaluated. Lane l
+  // of wave w stages input d0 + l of rows w, w + 4, ...; the row bases are
+  // wave-uniform and computed once.
+  constexpr int NXF = (ROWS + 3) / 4;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const float* xrow[NXF];
+#pragma unroll
+  for (int i = 0; i < NXF; ++i) {
+    const int r = wu + 4 * i, row = row0 + r;
+    xrow[i] = nullptr;
+    if (r < ROWS && row < BT) {
+      const int b = row / T, t = row - b * T;
+      xrow[i] = x + b * xs.b + t * xs.t;
+    }
+  }
+  // The loads are unconditional (a lane past the rows or past D reads x[0],
+  // and the stash writes 0 instead) so that none sits behind a branch and
+  // each waits only for its own data.
   float xv[NXF];
   auto fetch = [&](int d0) {
+    const int d = d0 + lane;
+    const long long off = (long long)d * xs.c;
 #pragma unroll
-    for (int i = 0; i < NXF; ++i) {
-      const int e = threadIdx.x + i * 256;
-      const int r = e >> 6, dd = e & 63;
-      const int row = row0 + r, d = d0 + dd;
-      xv[i] = 0.f;
-      if (e < 64 * ROWS && row < BT && d < D) {
-        const int b = row / T, t = row - b * T;
-        xv[i] = x[b * xs.b + t * xs.t + d * xs.c];
-      }
-    }
+    for (int i = 0; i < NXF; ++i) xv[i] = *((xrow[i] != nullptr && d < D) ? xrow[i] + off : x);
   };
-  fetch(0);
+  if (D > 0) fetch(0);
   for (int d0 = 0; d0 < D; d0 += 64) {
+    const bool dok = d0 + lane < D;
 #pragma unroll
-    for (int i = 0; i < NXF; ++i) {
-      const int e = threadIdx.x + i * 256;
-      if (e < 64 * ROWS) xsh[(e & 63) * XLD + (e >> 6)] = xv[i];
-    }
+    for (int i = 0; i < NXF; ++i)
+      if (wu + 4 * i < ROWS)
+        xsh[lane * XLD + wu + 4 * i] = (dok && xrow[i] != nullptr) ? xv[i] : 0.f;
     __syncthreads();
-    if (d0 + 64 < D) fetch(d0 + 64);
+    fetch(d0 + 64);
     const int dn = min(64, D - d0);
     const int dlo = DS == 1 ? 0 : w * (64 / DS);
     const int dhi = DS == 1 ? dn : min(dn, dlo + 64 / DS);
