@@ -247,19 +247,38 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
         xsh[lane * XLD + wu + 4 * i] = (dok && xrow[i] != nullptr) ? xv[i] : 0.f;
     __syncthreads();
     fetch(d0 + 64);
-    const int dn = min(64, D - d0);
-    const int dlo = DS == 1 ? 0 : w * (64 / DS);
-    const int dhi = DS == 1 ? dn : min(dn, dlo + 64 / DS);
     const float4* pcol = sensF + (long long)d0 * Hp + h;
+    if constexpr (DS == 1) {
+      const int dn = min(64, D - d0);
 #pragma unroll 4
-    for (int dd = dlo; dd < dhi; ++dd) {
-      const float4 p = pcol[(long long)dd * Hp];
-      const float* xr = xsh + dd * XLD + rw;
+      for (int dd = 0; dd < dn; ++dd) {
+        const float4 p = pcol[(long long)dd * Hp];
+        const float* xr = xsh + dd * XLD + rw;
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const float a = gate(fmaf(p.x, xr[r], p.y));
-        an[r] = fmaf(a, p.z, an[r]);
-        ad[r] = fmaf(a, p.w, ad[r]);
+        for (int r = 0; r < RPW; ++r) {
+          const float a = gate(fmaf(p.x, xr[r], p.y));
+          an[r] = fmaf(a, p.z, an[r]);
+          ad[r] = fmaf(a, p.w, ad[r]);
+        }
+      }
+    } else {
+      // The wave's 64/DS inputs of the chunk: all operand loads in flight at
+      // once. Rows past D are zero in the image and zero in xsh, so they add
+      // exact zeros.
+      constexpr int QD = 64 / DS;
+      const int dlo = w * QD;
+      float4 pq[QD];
+#pragma unroll
+      for (int i = 0; i < QD; ++i) pq[i] = pcol[(long long)(dlo + i) * Hp];
+#pragma unroll
+      for (int i = 0; i < QD; ++i) {
+        const float* xr = xsh + (dlo + i) * XLD + rw;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const float a = gate(fmaf(pq[i].x, xr[r], pq[i].y));
+          an[r] = fmaf(a, pq[i].z, an[r]);
+          ad[r] = fmaf(a, pq[i].w, ad[r]);
+        }
       }
     }
     __syncthreads();
