@@ -898,25 +898,33 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
     np[HP] = pGv;
     np[2 * HP] = pA;
   }
-  // Recurrent-gradient partials through a padded [64][65] LDS tile, whole
-  // rows out (layout [workgroup][4][i][j], as ode_bwd_kernel's).
-  constexpr long long HH = (long long)HP * HP;
+  // Recurrent-gradient partials through four padded [64][65] LDS planes at
+  // once, whole rows out (layout [workgroup][4][i][j], as ode_bwd_kernel's):
+  // one barrier pair, and each thread's reads all in flight before its stores.
+  constexpr int TLD = HP + 1, PL = HP * TLD;
+  constexpr int NT = KS * 64, PER = 4 * HP * HP / NT;
   float* tile = reinterpret_cast<float*>(lds4);
-  float* out = k.rpart + (long long)blockIdx.x * 4 * HH;
+  float* out = k.rpart + (long long)blockIdx.x * 4 * HP * HP;
+  __syncthreads();
 #pragma unroll
-  for (int pl = 0; pl < 4; ++pl) {
-    __syncthreads();
-#pragma unroll
-    for (int rr = 0; rr < RCP; ++rr) {
-      const float4 w = gacc[rr];
-      tile[o * (HP + 1) + r0 + rr] = pl == 0 ? w.x : pl == 1 ? w.y : pl == 2 ? w.z : w.w;
-    }
-    __syncthreads();
-    for (int e = tid; e < HP * HP; e += blockDim.x) {
-      const int i = e >> 6, j = e & 63;
-      out[pl * HH + e] = tile[i * (HP + 1) + j];
-    }
+  for (int rr = 0; rr < RCP; ++rr) {
+    const float4 w = gacc[rr];
+    const int e = o * TLD + r0 + rr;
+    tile[e] = w.x;
+    tile[PL + e] = w.y;
+    tile[2 * PL + e] = w.z;
+    tile[3 * PL + e] = w.w;
   }
+  __syncthreads();
+  float vals[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = tid + q * NT;
+    const int pl = e >> 12, i = (e >> 6) & 63, j = e & 63;
+    vals[q] = tile[pl * PL + i * TLD + j];
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
 }
 
 // ---------------------------------------------------------------------------

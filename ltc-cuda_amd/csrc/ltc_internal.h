@@ -190,12 +190,14 @@ inline long long fwd_lds(const Plan& p) {
 
 // Dynamic LDS of the single-workgroup chain (ode_bwd_kernel): alpha/beta rows
 // and the KS partials (two buffers in the single-row kernel); with FUSE at
-// least one padded [Hp][Hp+1] plane, through which the recurrent-gradient
-// partials are transposed for coalesced stores.
+// least one padded [Hp][Hp+1] plane (all four in the single-row kernel),
+// through which the recurrent-gradient partials are transposed for coalesced
+// stores.
 inline long long chain_lds(const Plan& p) {
   long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
   if (row_kernels(p) && 2LL * p.KSB * p.Hp * 4 > base) base = 2LL * p.KSB * p.Hp * 4;
-  const long long plane = p.FUSE ? (long long)p.Hp * (p.Hp + 1) * 4 : 0;
+  const long long plane =
+      p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;
   return base > plane ? base : plane;
 }
 
