@@ -736,7 +736,7 @@ __device__ __forceinline__ float lane_value(float v, int lane) {
 }
 
 template <int RCP>
-__global__ __launch_bounds__(1024) void ode_fwd_row_kernel(FwdK k) {
+__global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
   constexpr int HP = 64, KS = HP / RCP;
   extern __shared__ float4 lds4[];
   float2* red = reinterpret_cast<float2*>(lds4);  // [2][KS][64]
@@ -763,13 +763,21 @@ __global__ __launch_bounds__(1024) void ode_fwd_row_kernel(FwdK k) {
   for (int t = 0; t < T; ++t) {
     if (t + 1 < T) load_sens(t + 1, snn, sdn);
     for (int u = 0; u < U; ++u) {
+      // The gates of all RCP synapses in phases (arguments, exponentials,
+      // reciprocals), so that each transcendental's result is consumed
+      // several instructions later; the sums keep their order.
+      float z[RCP];
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) z[rr] = fmaf(preg[rr].x, lane_value(v, r0 + rr), preg[rr].y);
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
       float na = 0.f, qa = 0.f;
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) {
-        const float4 p = preg[rr];
-        const float a = gate(fmaf(p.x, lane_value(v, r0 + rr), p.y));
-        na = fmaf(a, p.z, na);
-        qa = fmaf(a, p.w, qa);
+        na = fmaf(z[rr], preg[rr].z, na);
+        qa = fmaf(z[rr], preg[rr].w, qa);
       }
       float2* rb = red + par * KS * HP;
       rb[ks * HP + o] = make_float2(na, qa);
