@@ -1313,7 +1313,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-constexpr int kLnPerLane = kModuleMaxD / 64;  // row values each lane keeps
 
 // Parameter images from the leaves (same flat segments as prep_kernel), plus
 // LayerNorm + affine of the (b,t) rows in trailing blocks of the same launch:
@@ -1322,6 +1321,8 @@ constexpr int kLnPerLane = kModuleMaxD / 64;  // row values each lane keeps
 // recb: 0 no chain image, 1 plain {S', c', WE, WP} (fused chain), 2 folded
 // {S', c', S'*WE, S'*WP}; sensf / sensb: write the forward / backward
 // sensory image. recF and the neuron vector are always written.
+// CPL: row values each lane keeps (D <= 64 * CPL <= kModuleMaxD).
+template <int CPL>
 __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
                                                         int Hp, int Dp, int recb, int sensf,
                                                         int sensb, int nprep_blocks, LnBuf ln,
@@ -1332,18 +1333,25 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
     if (row >= BT) return;
     const int b = row / T, t = row - b * T;
     const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
-    float xv[kLnPerLane];
+    // The row and the four per-column vectors load together, so one memory
+    // round trip precedes the two reductions.
+    float xv[CPL], lw[CPL], lb[CPL], iw[CPL], ib[CPL];
     float sum = 0.f;
 #pragma unroll
-    for (int c = 0; c < kLnPerLane; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       const int d = lane + 64 * c;
-      xv[c] = d < D ? xr[d * ln.xs.c] : 0.f;
+      const bool in = d < D;
+      xv[c] = in ? xr[d * ln.xs.c] : 0.f;
+      lw[c] = in ? lp.ln_w[d] : 0.f;
+      lb[c] = in ? lp.ln_b[d] : 0.f;
+      iw[c] = in ? lp.input_w[d] : 0.f;
+      ib[c] = in ? lp.input_b[d] : 0.f;
       sum += xv[c];
     }
     const float mean = wave_sum(sum) / (float)D;
     float sq = 0.f;
 #pragma unroll
-    for (int c = 0; c < kLnPerLane; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       const int d = lane + 64 * c;
       const float dv = d < D ? xv[c] - mean : 0.f;
       sq = fmaf(dv, dv, sq);
@@ -1351,11 +1359,11 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
     const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)D + lp.ln_eps);
     float* xo = ln.xa + (long long)row * D;
 #pragma unroll
-    for (int c = 0; c < kLnPerLane; ++c) {
+    for (int c = 0; c < CPL; ++c) {
       const int d = lane + 64 * c;
       if (d < D) {
-        const float xn = (xv[c] - mean) * rstd * lp.ln_w[d] + lp.ln_b[d];
-        xo[d] = xn * lp.input_w[d] + lp.input_b[d];
+        const float xn = (xv[c] - mean) * rstd * lw[c] + lb[c];
+        xo[d] = xn * iw[c] + ib[c];
       }
     }
     if (lane == 0) {
@@ -2477,9 +2485,16 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   const int nln = ln ? (BT + 3) / 4 : 0;
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   const bool bwd = (images & kLeafBwdImages) != 0;
-  hipLaunchKernelGGL(prep_leaf_kernel, dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, p.D,
-                     p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, (images & kLeafFwdImages) ? 1 : 0,
-                     bwd ? 1 : 0, nprep, lb, p.T, BT);
+#define LTC_PREPL(C)                                                                      \
+  hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, \
+                     p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                           \
+                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, lb, p.T, BT)
+  if (nln == 0 || p.D <= 64) LTC_PREPL(1);
+  else if (p.D <= 128) LTC_PREPL(2);
+  else if (p.D <= 256) LTC_PREPL(4);
+  else if (p.D <= 512) LTC_PREPL(8);
+  else LTC_PREPL(16);
+#undef LTC_PREPL
   return hipGetLastError();
 }
 
