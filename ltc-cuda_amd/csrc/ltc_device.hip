@@ -249,17 +249,28 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
     fetch(d0 + 64);
     const float4* pcol = sensF + (long long)d0 * Hp + h;
     if constexpr (DS == 1) {
-      const int dn = min(64, D - d0);
-#pragma unroll 4
-      for (int dd = 0; dd < dn; ++dd) {
-        const float4 p = pcol[(long long)dd * Hp];
-        const float* xr = xsh + dd * XLD + rw;
+      // All 64 inputs of the chunk (rows past D are zero in the image and in
+      // xsh, so they add exact zeros), operands loaded four at a time one
+      // group ahead (the last group reloads itself).
+      float4 pc[4], pn[4];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const float a = gate(fmaf(p.x, xr[r], p.y));
-          an[r] = fmaf(a, p.z, an[r]);
-          ad[r] = fmaf(a, p.w, ad[r]);
+      for (int i = 0; i < 4; ++i) pc[i] = pcol[(long long)i * Hp];
+      for (int gq = 0; gq < 16; ++gq) {
+        const int gn = gq < 15 ? gq + 1 : 15;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pn[i] = pcol[(long long)(gn * 4 + i) * Hp];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* xr = xsh + (gq * 4 + i) * XLD + rw;
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) {
+            const float a = gate(fmaf(pc[i].x, xr[r], pc[i].y));
+            an[r] = fmaf(a, pc[i].z, an[r]);
+            ad[r] = fmaf(a, pc[i].w, ad[r]);
+          }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pc[i] = pn[i];
       }
     } else {
       // The wave's 64/DS inputs of the chunk: all operand loads in flight at
