@@ -1471,8 +1471,10 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(LeafParams lp, LnBuf ln, co
         float gxa = 0.f;
         const float* pp = dxpart + (long long)row * Dp + d;
         // Unrolled so that the partials' loads are in flight together (the
-        // adds keep their fixed order).
-#pragma unroll 4
+        // adds keep their fixed order); less deep at the widest rows, whose
+        // registers already hold 16 columns.
+        constexpr int UNR = CPL <= 8 ? 8 : 4;
+#pragma unroll UNR
         for (int hb = 0; hb < HB; ++hb) gxa += pp[hb * hstride];
         xh[c] = (xr[d * ln.xs.c] - mean) * rstd;
         const float xn = xh[c] * lw[c] + lb[c];
