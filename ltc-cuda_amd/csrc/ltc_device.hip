@@ -911,12 +911,21 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
       pGv += al * cvk1;
       pA += al;
       const float gdir = al * C;
+      // The RCP gates depend on v^k only: evaluated in phases (arguments,
+      // exponentials, reciprocals) ahead of the alpha/beta products.
+      float ga[RCP];
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
+#pragma unroll
+      for (int rr = 0; rr < RCP; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
       float acc = 0.f;
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) {
         const float4 p = preg[rr];
         const float cx = lane_value(al, r0 + rr), cy = lane_value(be, r0 + rr);
-        const float a = gate(fmaf(p.x, cvk, p.y));
+        const float a = ga[rr];
         const float a2 = fmaf(-a, a, a);
         const float dl = fmaf(cx, p.z, cy * p.w) * a2;
         acc = fmaf(dl, p.x, acc);
