@@ -112,6 +112,30 @@ __device__ __forceinline__ float4 image_load(__amdgpu_buffer_rsrc_t r, int lane_
 // through a double buffer of four rows, calling f(operand, row) for each row.
 // r0 must be wave-uniform. The prefetch past the chunk reads the next chunk's
 // rows, or zeros past the image.
+// As stream_rows, calling f4(operands, row) once per group of four rows.
+template <class F4>
+__device__ __forceinline__ void stream_rows4(__amdgpu_buffer_rsrc_t rs, int lane_bytes, int r0,
+                                             int RC, int Hp, F4&& f4) {
+  const int rowb = Hp * 16;
+  const int sb = r0 * rowb;
+  float4 pa[4], pb[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, sb + q * rowb);
+  for (int rr = 0; rr < RC; rr += 8) {
+    const int s0 = sb + rr * rowb;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pb[q] = image_load(rs, lane_bytes, s0 + (4 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+    f4(pa, r0 + rr);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) pa[q] = image_load(rs, lane_bytes, s0 + (8 + q) * rowb);
+    __builtin_amdgcn_sched_barrier(0);
+    f4(pb, r0 + rr + 4);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 template <class F>
 __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_bytes, int r0,
                                             int RC, int Hp, F&& f) {
@@ -446,8 +470,14 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       } else {
         // Operands stream from L2, the next four requested while the current
         // four are evaluated.
-        stream_rows(rsF, o * 16, r0, RC, Hp,
-                    [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
+        if constexpr (kFwdGroup<NB> == 4) {
+          stream_rows4(rsF, o * 16, r0, RC, Hp, [&](const float4* p, int r) {
+            fwd_synapses<NB, 4>(p, vs, Hp, r, na, qa);
+          });
+        } else {
+          stream_rows(rsF, o * 16, r0, RC, Hp,
+                      [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
+        }
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
@@ -1799,8 +1829,14 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         for (int rr = 0; rr < RCP; rr += kFwdGroup<NB>)
           fwd_synapses<NB, kFwdGroup<NB>>(preg + rr, vs, Hp, r0 + rr, na, qa);
       } else {
-        stream_rows(rsF, c * 16, r0, RC, Hp,
-                    [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
+        if constexpr (kFwdGroup<NB> == 4) {
+          stream_rows4(rsF, c * 16, r0, RC, Hp, [&](const float4* p, int r) {
+            fwd_synapses<NB, 4>(p, vs, Hp, r, na, qa);
+          });
+        } else {
+          stream_rows(rsF, c * 16, r0, RC, Hp,
+                      [&](const float4 p, int r) { fwd_synapse<NB>(p, vs, Hp, r, na, qa); });
+        }
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = make_float2(na[b], qa[b]);
