@@ -258,9 +258,13 @@ def test_backward_expanded_grad_and_no_grad_state():
     assert_grads_close(got, ref, "expanded grad")
 
 
-def test_strided_input_matches_contiguous():
-    """C5-style x[:, :, 0::2] view is read in place and gives the same bits."""
-    B, T, D, H = 64, 4, 64, 64
+@pytest.mark.parametrize("shape", [(64, 4, 64, 64), (4100, 4, 70, 64)],
+                         ids=["split-D sensory form", "row-group sensory form, partial chunk"])
+def test_strided_input_matches_contiguous(shape):
+    """C5-style x[:, :, 0::2] view is read in place and gives the same bits:
+    the first shape takes the sensory kernels' split-D form, the second (16400
+    rows, D = 70) the row-group form with a partial second chunk of inputs."""
+    B, T, D, H = shape
     args = boundary(B, T, D, H, seed=9)
     torch.manual_seed(10)
     wide = torch.randn(B, T, 2 * D)
