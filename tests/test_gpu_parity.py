@@ -99,6 +99,7 @@ FWD_SHAPES = [
     (2, 4, 32, 65), (24, 8, 128, 64), (32, 16, 128, 128), (3, 2, 7, 192), (2, 2, 16, 256),
     (1, 2, 8, 320), (2, 2, 16, 512), (1, 1, 4, 1000), (1, 1, 1, 1), (600, 2, 8, 16),
     (1100, 2, 8, 24), (2100, 1, 4, 8), (4100, 1, 4, 8),
+    (600, 2, 8, 150),  # two rows per workgroup, operands streamed in groups of four rows
 ]
 
 
