@@ -100,6 +100,7 @@ FWD_SHAPES = [
     (1, 2, 8, 320), (2, 2, 16, 512), (1, 1, 4, 1000), (1, 1, 1, 1), (600, 2, 8, 16),
     (1100, 2, 8, 24), (2100, 1, 4, 8), (4100, 1, 4, 8),
     (600, 2, 8, 150),  # two rows per workgroup, operands streamed in groups of four rows
+    (2100, 1, 128, 8),  # row-group sensory form over two full input chunks
 ]
 
 
