@@ -123,6 +123,32 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
                       void* workspace, long long workspace_bytes, void* stream);
 
 /*
+ * ltc_full_forward without a workspace argument. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The kernels' scratch (parameter images, sensory sums, cluster exchange
+ * words) lives in a static device array of LTC_NOALLOC_SCRATCH_BYTES bytes,
+ * which the library holds on every GPU it runs on until the process ends.
+ * Sizes whose ltc_fwd_workspace_bytes() exceeds it return LTC_EUNSUPPORTED
+ * before anything is launched. The call allocates nothing and arguments
+ * mean what they mean for ltc_full_forward. Every call on one GPU shares
+ * that GPU's array, and each call rewrites what it reads, so a call does not
+ * depend on an earlier one; calls that overlap on one GPU (two streams, two
+ * host threads) race on the array and must be serialised by the caller.
+ */
+#define LTC_NOALLOC_SCRATCH_BYTES (64LL * 1024 * 1024)
+int ltc_full_forward_noalloc(const float* x, long long sxb, long long sxt, long long sxd,
+                             const float* state,
+                             const float* w_pos, const float* w_erev, const float* mu,
+                             const float* sigma,
+                             const float* sensory_mu, const float* sensory_sigma,
+                             const float* sensory_erev, const float* sensory_w_pos,
+                             const float* cm_t, const float* gleak_pos, const float* vleak,
+                             int B, int T, int D, int H, int ode_unfolds, float epsilon,
+                             int save_intermediates,
+                             float* out, float* h_final, float* saved, void* stream);
+
+/*
  * Module-level path: the whole TrueLiquidTimeConstant.forward
  * (reference ltc.py:249-326) and its backward in one call each. The caller
  * passes the module's leaves instead of the boundary tensors, and the

@@ -11,6 +11,12 @@
 #include "../../include/ltc_capi.h"
 #include "ltc_internal.h"
 
+// Scratch of the no-allocation forward (ltc_full_forward_noalloc): one array
+// per device, held until the process ends. In host code `scratch` names a
+// host-side shadow, never the device array: its device address comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+static __device__ __align__(256) unsigned char scratch[LTC_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_err;
@@ -451,6 +457,36 @@ int hip_fail(const char* what, hipError_t e) {
   return fail(LTC_EHIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Device address of this device's scratch array (looked up on the first call
+// on each device, with that device current); nullptr after a failed lookup,
+// with the message set.
+void* noalloc_scratch() {
+  constexpr int kMaxDev = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDev] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    hip_fail("hipGetDevice", e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDev) {
+    fail(LTC_EUNSUPPORTED, "device index " + std::to_string(dev) + " out of range");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> g(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      hip_fail("hipGetSymbolAddress(scratch)", e != hipSuccess ? e : hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -539,6 +575,33 @@ int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
   return LTC_OK;
+}
+
+int ltc_full_forward_noalloc(const float* x, long long sxb, long long sxt, long long sxd,
+                             const float* state, const float* w_pos, const float* w_erev,
+                             const float* mu, const float* sigma, const float* sensory_mu,
+                             const float* sensory_sigma, const float* sensory_erev,
+                             const float* sensory_w_pos, const float* cm_t,
+                             const float* gleak_pos, const float* vleak, int B, int T, int D,
+                             int H, int ode_unfolds, float epsilon, int save_intermediates,
+                             float* out, float* h_final, float* saved, void* stream) {
+  g_err.clear();
+  const int rc = check_dims(B, T, D, H, ode_unfolds);
+  if (rc != LTC_OK) return rc;
+  Carver need{nullptr};
+  carve_fwd(make_plan(B, T, D, H, ode_unfolds), need);
+  if (need.off > LTC_NOALLOC_SCRATCH_BYTES)
+    return fail(LTC_EUNSUPPORTED,
+                "these sizes need " + std::to_string(need.off) +
+                    " bytes of scratch; the no-allocation forward holds " +
+                    std::to_string(LTC_NOALLOC_SCRATCH_BYTES) +
+                    " (use ltc_full_forward with a workspace)");
+  void* ws = noalloc_scratch();
+  if (ws == nullptr) return LTC_EHIP;
+  return ltc_full_forward(x, sxb, sxt, sxd, state, w_pos, w_erev, mu, sigma, sensory_mu,
+                          sensory_sigma, sensory_erev, sensory_w_pos, cm_t, gleak_pos, vleak, B,
+                          T, D, H, ode_unfolds, epsilon, save_intermediates, out, h_final, saved,
+                          ws, LTC_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sxd,

@@ -69,6 +69,7 @@ class CApi:
         "ltc_ode_unfold_fwd_workspace_bytes", "ltc_ode_unfold_fwd",
         "ltc_sensory_bwd_workspace_bytes", "ltc_sensory_bwd",
         "ltc_ode_unfold_bwd_workspace_bytes", "ltc_ode_unfold_bwd",
+        "ltc_full_forward_noalloc",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
@@ -96,6 +97,11 @@ class CApi:
             [_f32p, _i64, _i64, _i64, _f32p] + [_f32p] * 11
             + [_int, _int, _int, _int, _int, _flt, _int]
             + [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.c_void_p])
+        lib.ltc_full_forward_noalloc.restype = _int
+        lib.ltc_full_forward_noalloc.argtypes = (
+            [_f32p, _i64, _i64, _i64, _f32p] + [_f32p] * 11
+            + [_int, _int, _int, _int, _int, _flt, _int]
+            + [_f32p, _f32p, _f32p, ctypes.c_void_p])
         lib.ltc_full_backward.restype = _int
         lib.ltc_full_backward.argtypes = (
             [_f32p, _i64, _i64, _i64] + [_f32p] * 11 + [_f32p]
