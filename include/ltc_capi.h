@@ -303,6 +303,30 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*
+ * Cluster give-up. For H > 192 the ODE kernels run as clusters of workgroups
+ * that exchange values every unfold and must all be resident at once (the
+ * plan asks for at most one workgroup per CU). Each wait is bounded; when a
+ * member runs out of its budget (another kernel held the CUs its partners
+ * needed), the whole cluster leaves early, and the call then overwrites
+ * every output it writes (out, h_final and saved for a forward; every
+ * gradient for a backward) with NaN and raises a sticky per-device fault flag.
+ * The call itself has already returned LTC_OK by then (it only queues work);
+ * ltc_device_status() waits for the current device, returns LTC_EHIP with a
+ * message when the flag is raised, and clears it when `clear` is nonzero.
+ * It synchronises the device, so it must not be called under graph capture.
+ * No counterpart in the reference, whose kernels have no inter-block waits.
+ */
+int ltc_device_status(int clear);
+
+/* Wait budget of every cluster exchange, in ticks of the GPU's 100 MHz wall
+ * clock (default 20000000 = 0.2 s), for calls made after it returns; returns
+ * the previous budget, or -1 for a negative argument. A budget of 0 makes
+ * every member give up at its first wait: a host-forced failure for tests of
+ * the give-up path (every kernel still exits normally). No counterpart in the
+ * reference. */
+long long ltc_set_cluster_spin_ticks(long long ticks);
+
+/*
  * Per-kernel event timing. No counterpart in the reference, whose bench
  * times with torch.cuda.Event around whole calls (bench_ltc.py:39-96).
  * While enabled, every kernel this library launches is bracketed by HIP

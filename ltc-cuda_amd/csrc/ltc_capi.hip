@@ -4,6 +4,7 @@
 // stream. Allocates no device memory.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -267,8 +268,11 @@ struct Carver {
 // rows past the end.
 long long image_rows(const ltc::Plan& p) { return p.Hp + (p.CP > 0 ? ltc::kImageSlackRows : 0); }
 
+// Wait budget of the cluster exchanges (ltc_set_cluster_spin_ticks).
+std::atomic<long long> g_spin{ltc::kDefaultSpinTicks};
+
 ltc::ClusterBuf carve_cluster(const ltc::Plan& p, Carver& c, bool bwd) {
-  ltc::ClusterBuf cb{nullptr, nullptr};
+  ltc::ClusterBuf cb{nullptr, nullptr, g_spin.load(std::memory_order_relaxed)};
   if (p.CP > 0) {
     cb.xch = c.take<unsigned long long>(bwd ? ltc::cluster_words_bwd(p) : ltc::cluster_words(p));
     cb.status = c.take<int>(1);
@@ -457,6 +461,29 @@ int hip_fail(const char* what, hipError_t e) {
   return fail(LTC_EHIP, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// Runs a fill list (zero-fills and copies of a degenerate call, or the NaN
+// fill after a cluster launch) and reports a failed launch.
+int run_fill(const ltc::FillList& fl, hipStream_t s) {
+  const hipError_t e = ltc::launch_fill(fl, s);
+  return e == hipSuccess ? LTC_OK : hip_fail("fill launch", e);
+}
+
+ltc::FillList zero_list() {
+  ltc::FillList fl{};
+  fl.value = 0.f;
+  return fl;
+}
+
+// After a call whose ODE kernels ran as clusters: every output listed is
+// overwritten with NaN, and the device's fault flag raised, when a member of
+// the call gave up waiting (its status word is set); otherwise nothing runs.
+ltc::FillList poison_list(const ltc::ClusterBuf& cb) {
+  ltc::FillList fl{};
+  fl.value = __builtin_nanf("");
+  fl.gate = cb.status;
+  return fl;
+}
+
 // Device address of this device's scratch array (looked up on the first call
 // on each device, with that device current); nullptr after a failed lookup,
 // with the message set.
@@ -550,10 +577,9 @@ int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T == 0) {
     // No steps: the final state is the initial state.
-    hipError_t e = hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
-                                  hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    ltc::fill_add(fl, h_final, state, (long long)B * H);
+    return run_fill(fl, s);
   }
 
   Carver c{static_cast<char*>(workspace)};
@@ -574,6 +600,13 @@ int ltc_full_forward(const float* x, long long sxb, long long sxt, long long sxd
                                w.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  if (p.CP > 0) {
+    ltc::FillList fl = poison_list(w.cb);
+    ltc::fill_add(fl, out, nullptr, (long long)B * T * H);
+    ltc::fill_add(fl, h_final, nullptr, (long long)B * H);
+    ltc::fill_add(fl, saved, nullptr, save_intermediates ? saved_floats(p) : 0);
+    return run_fill(fl, s);
+  }
   return LTC_OK;
 }
 
@@ -642,29 +675,14 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
 
   if ((long long)B * T == 0) {
     // No unfolds: parameter gradients are zero and dL/dh0 = dL/dh_final.
-    float* zs[] = {grad_w_pos, grad_w_erev, grad_mu, grad_sigma};
-    for (float* z : zs) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zd[] = {grad_sensory_mu, grad_sensory_sigma, grad_sensory_erev, grad_sensory_w_pos};
-    for (float* z : zd) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zh[] = {grad_cm_t, grad_gleak_pos, grad_vleak};
-    for (float* z : zh) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    if (B > 0) {
-      hipError_t e = grad_h_final
-                         ? hipMemcpyAsync(grad_state, grad_h_final, (size_t)B * H * sizeof(float),
-                                          hipMemcpyDeviceToDevice, s)
-                         : hipMemsetAsync(grad_state, 0, (size_t)B * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("grad_state copy", e);
-    }
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    for (float* z : {grad_w_pos, grad_w_erev, grad_mu, grad_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)H * H);
+    for (float* z : {grad_sensory_mu, grad_sensory_sigma, grad_sensory_erev, grad_sensory_w_pos})
+      ltc::fill_add(fl, z, nullptr, (long long)D * H);
+    for (float* z : {grad_cm_t, grad_gleak_pos, grad_vleak}) ltc::fill_add(fl, z, nullptr, H);
+    ltc::fill_add(fl, grad_state, grad_h_final, (long long)B * H);
+    return run_fill(fl, s);
   }
 
   Carver c{static_cast<char*>(workspace)};
@@ -700,6 +718,17 @@ int ltc_full_backward(const float* x, long long sxb, long long sxt, long long sx
     return ltc::launch_finalize(p, rp, w.rpart, w.spart, w.dxpart, w.npart, w.ps, go, s);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
+  if (p.CP > 0) {
+    ltc::FillList fl = poison_list(w.cb);
+    ltc::fill_add(fl, grad_x, nullptr, (long long)B * T * D);
+    ltc::fill_add(fl, grad_state, nullptr, (long long)B * H);
+    for (float* z : {grad_w_pos, grad_w_erev, grad_mu, grad_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)H * H);
+    for (float* z : {grad_sensory_mu, grad_sensory_sigma, grad_sensory_erev, grad_sensory_w_pos})
+      ltc::fill_add(fl, z, nullptr, (long long)D * H);
+    for (float* z : {grad_cm_t, grad_gleak_pos, grad_vleak}) ltc::fill_add(fl, z, nullptr, H);
+    return run_fill(fl, s);
+  }
   return LTC_OK;
 }
 
@@ -773,11 +802,9 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   if (B == 0) return LTC_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (T == 0) {
-    hipError_t e = state ? hipMemcpyAsync(h_final, state, (size_t)B * H * sizeof(float),
-                                          hipMemcpyDeviceToDevice, s)
-                         : hipMemsetAsync(h_final, 0, (size_t)B * H * sizeof(float), s);
-    if (e != hipSuccess) return hip_fail("initial state copy", e);
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    ltc::fill_add(fl, h_final, state, (long long)B * H);
+    return run_fill(fl, s);
   }
   Carver c{static_cast<char*>(workspace)};
   const FwdWs wfw = carve_fwd(p, c);
@@ -810,6 +837,13 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
                                densave, wfw.cb, s);
   });
   if (e != hipSuccess) return hip_fail("ODE forward launch", e);
+  if (p.CP > 0) {
+    ltc::FillList fl = poison_list(wfw.cb);
+    ltc::fill_add(fl, out, nullptr, (long long)B * T * H);
+    ltc::fill_add(fl, h_final, nullptr, (long long)B * H);
+    ltc::fill_add(fl, saved, nullptr, save_intermediates ? saved_floats(p) : 0);
+    return run_fill(fl, s);
+  }
   return LTC_OK;
 }
 
@@ -860,34 +894,16 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     return fail(LTC_EINVAL, "workspace must be 256-byte aligned");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if ((long long)B * T == 0) {
-    float* zs[] = {grad_w, grad_erev, grad_mu, grad_sigma};
-    for (float* z : zs) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zd[] = {grad_sensory_w, grad_sensory_erev, grad_sensory_mu, grad_sensory_sigma};
-    for (float* z : zd) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zh[] = {grad_gleak, grad_vleak, grad_cm};
-    for (float* z : zh) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zx[] = {grad_input_w, grad_input_b, grad_ln_weight, grad_ln_bias};
-    for (float* z : zx) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    if (B > 0 && grad_state) {
-      hipError_t e = grad_h_final
-                         ? hipMemcpyAsync(grad_state, grad_h_final, (size_t)B * H * sizeof(float),
-                                          hipMemcpyDeviceToDevice, s)
-                         : hipMemsetAsync(grad_state, 0, (size_t)B * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("grad_state copy", e);
-    }
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    for (float* z : {grad_w, grad_erev, grad_mu, grad_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)H * H);
+    for (float* z : {grad_sensory_w, grad_sensory_erev, grad_sensory_mu, grad_sensory_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)D * H);
+    for (float* z : {grad_gleak, grad_vleak, grad_cm}) ltc::fill_add(fl, z, nullptr, H);
+    for (float* z : {grad_input_w, grad_input_b, grad_ln_weight, grad_ln_bias})
+      ltc::fill_add(fl, z, nullptr, D);
+    ltc::fill_add(fl, grad_state, grad_h_final, (long long)B * H);
+    return run_fill(fl, s);
   }
   Carver c{static_cast<char*>(workspace)};
   BwdWs wb = carve_bwd(p, c, false);
@@ -923,6 +939,19 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
+  if (p.CP > 0) {
+    ltc::FillList fl = poison_list(wb.cb);
+    ltc::fill_add(fl, grad_x, nullptr, (long long)B * T * D);
+    ltc::fill_add(fl, grad_state, nullptr, (long long)B * H);
+    for (float* z : {grad_w, grad_erev, grad_mu, grad_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)H * H);
+    for (float* z : {grad_sensory_w, grad_sensory_erev, grad_sensory_mu, grad_sensory_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)D * H);
+    for (float* z : {grad_gleak, grad_vleak, grad_cm}) ltc::fill_add(fl, z, nullptr, H);
+    for (float* z : {grad_input_w, grad_input_b, grad_ln_weight, grad_ln_bias})
+      ltc::fill_add(fl, z, nullptr, D);
+    return run_fill(fl, s);
+  }
   return LTC_OK;
 }
 
@@ -1084,12 +1113,10 @@ int ltc_sensory_bwd(const float* grad_w_num, const float* grad_w_den, const floa
   if (rc != LTC_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (B == 0) {
-    float* zd[] = {grad_sensory_sigma, grad_sensory_mu, grad_sensory_w_pos, grad_sensory_erev};
-    for (float* z : zd) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)D * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    for (float* z : {grad_sensory_sigma, grad_sensory_mu, grad_sensory_w_pos, grad_sensory_erev})
+      ltc::fill_add(fl, z, nullptr, (long long)D * H);
+    return run_fill(fl, s);
   }
   Carver c{static_cast<char*>(workspace)};
   const SensWs w = carve_sens(p, c, true);
@@ -1167,6 +1194,12 @@ int ltc_ode_unfold_fwd(const float* state, const float* w_pos, const float* w_er
     e = ltc::launch_copy_rows(vsave, p.Hp, v_buffer, H, (long long)ode_unfolds * B, H, s);
     if (e != hipSuccess) return hip_fail("copy launch", e);
   }
+  if (p.CP > 0) {
+    ltc::FillList fl = poison_list(w.f.cb);
+    ltc::fill_add(fl, state_out, nullptr, (long long)B * H);
+    ltc::fill_add(fl, v_buffer, nullptr, save_intermediates ? (long long)ode_unfolds * B * H : 0);
+    return run_fill(fl, s);
+  }
   return LTC_OK;
 }
 
@@ -1198,17 +1231,11 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
   if (rc != LTC_OK) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (B == 0) {
-    float* zs[] = {grad_w_pos, grad_w_erev, grad_mu, grad_sigma};
-    for (float* z : zs) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    float* zh[] = {grad_cm_t, grad_gleak_pos, grad_vleak};
-    for (float* z : zh) {
-      hipError_t e = hipMemsetAsync(z, 0, (size_t)H * sizeof(float), s);
-      if (e != hipSuccess) return hip_fail("hipMemsetAsync", e);
-    }
-    return LTC_OK;
+    ltc::FillList fl = zero_list();
+    for (float* z : {grad_w_pos, grad_w_erev, grad_mu, grad_sigma})
+      ltc::fill_add(fl, z, nullptr, (long long)H * H);
+    for (float* z : {grad_cm_t, grad_gleak_pos, grad_vleak}) ltc::fill_add(fl, z, nullptr, H);
+    return run_fill(fl, s);
   }
   Carver c{static_cast<char*>(workspace)};
   const UnfoldWs w = carve_unfold(p, c, true);
@@ -1263,6 +1290,20 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
                                 ltc::kFinRec);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
+  if (p.CP > 0) {
+    // Either the recompute (forward) or the chain may have given up; both
+    // status words gate the same fill.
+    for (const ltc::ClusterBuf* cb : {&w.f.cb, &w.b.cb}) {
+      ltc::FillList fl = poison_list(*cb);
+      for (float* z : {grad_v, grad_w_num_sensory, grad_w_den_sensory})
+        ltc::fill_add(fl, z, nullptr, (long long)B * H);
+      for (float* z : {grad_w_pos, grad_w_erev, grad_mu, grad_sigma})
+        ltc::fill_add(fl, z, nullptr, (long long)H * H);
+      for (float* z : {grad_cm_t, grad_gleak_pos, grad_vleak}) ltc::fill_add(fl, z, nullptr, H);
+      const int rc = run_fill(fl, s);
+      if (rc != LTC_OK) return rc;
+    }
+  }
   return LTC_OK;
 }
 
@@ -1284,6 +1325,23 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;
+}
+
+int ltc_device_status(int clear) {
+  g_err.clear();
+  int v = 0;
+  const hipError_t e = ltc::device_fault(&v, clear != 0);
+  if (e != hipSuccess) return hip_fail("device status read", e);
+  if (v != 0)
+    return fail(LTC_EHIP,
+                "a cluster launch on this device gave up waiting for its partner workgroups "
+                "(the grid was not resident at once); every output of that call was set to NaN");
+  return LTC_OK;
+}
+
+long long ltc_set_cluster_spin_ticks(long long ticks) {
+  if (ticks < 0) return -1;
+  return g_spin.exchange(ticks);
 }
 
 int ltc_timing_enable(int on) {

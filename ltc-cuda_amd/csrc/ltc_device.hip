@@ -1687,14 +1687,15 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
 // read whole, so no fence or counter is involved. Two slots alternate by tag
 // parity: a member overwrites a slot only after all partners have published
 // the following unfold, which they do after they finished reading that slot.
-// Every wait is bounded (kSpinTicks of the 100 MHz wall clock). A member that
-// gives up sets *status, writes NaN into its final state and returns; its
-// partners then give up the same way, so the grid always drains.
+// Every wait is bounded (a budget of ticks of the 100 MHz wall clock, a
+// kernel argument). A member that gives up sets *status, writes NaN into its
+// final state and returns; its partners then give up the same way, so the
+// grid always drains. The host then overwrites every output of the call with
+// NaN and raises the device's fault flag (launch_fill with a gate).
 // Exchange layout: [cluster][2 slots][CP members][NB rows][64 columns] words,
 // cleared (tag 0) before every launch; tags start at 1.
 // ---------------------------------------------------------------------------
 constexpr int kClW = 64;                    // columns per cluster member
-constexpr long long kSpinTicks = 20000000;  // 0.2 s at 100 MHz
 
 __device__ __forceinline__ void xch_put(unsigned long long* w, float v, unsigned tag) {
   const unsigned long long word =
@@ -1710,12 +1711,15 @@ __device__ __forceinline__ unsigned long long xch_get(unsigned long long* w) {
 // thread at a time. For each word: pre(x, a) is called once before the first
 // poll (to start the loads its delivery needs), deliver(x, a, value) once the
 // tag is current; a = q*PER + b*64 + col is the word's offset in the slot and
-// x its index in the batch. Returns false if a wait ran out.
+// x its index in the batch. Returns false if a wait ran out; with a budget
+// of spin <= 0 ticks, at the first wait, before any word is read.
 constexpr int kXchBatch = 2;
 
 template <int PER, int XB = kXchBatch, class Pre, class Deliver>
 __device__ __forceinline__ bool xch_gather(unsigned long long* slot, int p, int nwords, int tid,
-                                           int nthr, unsigned tag, Pre&& pre, Deliver&& deliver) {
+                                           int nthr, unsigned tag, long long spin, Pre&& pre,
+                                           Deliver&& deliver) {
+  if (spin <= 0) return false;
   for (int e0 = tid; e0 < nwords; e0 += XB * nthr) {
     unsigned long long w[XB];
     int at[XB];
@@ -1745,7 +1749,7 @@ __device__ __forceinline__ bool xch_gather(unsigned long long* slot, int p, int 
         }
       }
       if (!any) break;
-      if (wall_clock64() - t0 > kSpinTicks) return false;
+      if (wall_clock64() - t0 > spin) return false;
 #pragma unroll
       for (int x = 0; x < XB; ++x)
         if (wait[x]) w[x] = xch_get(slot + at[x]);
@@ -1766,6 +1770,7 @@ struct FwdCK {
   float* densave;
   unsigned long long* xch;
   int* status;
+  long long spin;  // wait budget of each exchange, wall-clock ticks
   int B, T, H, Hp, U, KS, RC, CP;
   float eps;
 };
@@ -1861,7 +1866,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         if (u == U - 1 && live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
       }
       const bool ok = xch_gather<PER>(
-          slot, p, nwords, tid, nthr, tag, [](int, int) {},
+          slot, p, nwords, tid, nthr, tag, k.spin, [](int, int) {},
           [&](int, int a, float v) {
             const int q = a / PER, r = a - q * PER;
             vs[(r >> 6) * Hp + q * kClW + (r & 63)] = v;
@@ -1972,6 +1977,7 @@ struct BwdCK {
   float* rpart;  // FUSE: one recurrent-gradient partial per cluster, [NCL][4][Hp][Hp]
   unsigned long long* xch;
   int* status;
+  long long spin;  // wait budget of each exchange, wall-clock ticks
   int B, T, H, Hp, U, KS, RC, CP;
 };
 
@@ -2192,7 +2198,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       const float* vn = pv + (n & 1) * NB * Hp;         // v of slot n
       const float* vm = pv + ((n - 1) & 1) * NB * Hp;   // v of slot n-1
       const bool ok = xch_gather<PER, kXchBatch>(
-          slot, p, nwords, tid, nthr, tag, [](int, int) {},
+          slot, p, nwords, tid, nthr, tag, k.spin, [](int, int) {},
           [&](int, int a, float gg) {
             int b, col;
             word_rc(a, b, col);
@@ -2214,7 +2220,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       constexpr int XB = (FUSE && RCS > 0) ? 4 : kXchBatch;
       float pden_[XB], pvk1[XB];
       const bool ok = xch_gather<PER, XB>(
-          slot, p, nwords, tid, nthr, tag,
+          slot, p, nwords, tid, nthr, tag, k.spin,
           [&](int x, int a) {
             int b, col;
             word_rc(a, b, col);
@@ -2280,6 +2286,31 @@ __global__ __launch_bounds__(256) void clear_words_kernel(unsigned long long* w,
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) w[i] = 0ULL;
   if (i == 0 && status != nullptr) *status = 0;
+}
+
+// The device's sticky fault flag: raised by a gated fill after a cluster
+// member gave up, read and cleared by the host (device_fault).
+__device__ int g_fault;
+
+// Segment list fill/copy (see FillList). Grid-stride over the concatenated
+// segments; with a gate, every thread first reads it and leaves when it is 0.
+__global__ __launch_bounds__(256) void fill_list_kernel(FillList fl) {
+  if (fl.gate != nullptr) {
+    if (__hip_atomic_load(fl.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+      __hip_atomic_store(&g_fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  long long base = 0;
+  for (int sgi = 0; sgi < fl.nseg; ++sgi) {
+    const FillSeg sg = fl.seg[sgi];
+    for (; i < base + sg.n; i += stride) {
+      const long long e = i - base;
+      sg.dst[e] = sg.src != nullptr ? sg.src[e] : fl.value;
+    }
+    base += sg.n;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2405,6 +2436,34 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   return hipGetLastError();
 }
 
+hipError_t launch_fill(const FillList& fl, hipStream_t s) {
+  long long total = 0;
+  for (int i = 0; i < fl.nseg; ++i) total += fl.seg[i].n;
+  if (total == 0) return hipSuccess;
+  // A gated fill (after a cluster launch) usually does nothing: a small grid
+  // keeps its cost to one short launch.
+  const long long cap = fl.gate != nullptr ? 256 : 2048;
+  long long blocks = (total + 255) / 256;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(fill_list_kernel, dim3((unsigned)blocks), dim3(256), 0, s, fl);
+  return hipGetLastError();
+}
+
+hipError_t device_fault(int* value, bool clear) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  int v = 0;
+  e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_fault), sizeof(int), 0, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  if (clear && v != 0) {
+    const int zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_fault), &zero, sizeof(int), 0, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+  }
+  *value = v;
+  return hipSuccess;
+}
+
 hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long long dst_ld,
                             long long rows, int cols, hipStream_t s) {
   const long long n = rows * dst_ld;
@@ -2454,7 +2513,7 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
     hipError_t e = clear_cluster(p, cb, false, s);
     if (e != hipSuccess) return e;
     FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
-            p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, eps};
+            cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, eps};
     switch (p.NB) {
       case 8: return fwd_cl_by_rcp<8>(p, a, s);
       case 4: return fwd_cl_by_rcp<4>(p, a, s);
@@ -2482,7 +2541,8 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
     hipError_t e = clear_cluster(p, cb, true, s);
     if (e != hipSuccess) return e;
     BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
-            gstate, rpart, cb.xch, cb.status, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, p.CPB};
+            gstate, rpart, cb.xch, cb.status, cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB,
+            p.CPB};
     switch (p.NBB) {
       case 8: return bwd_cl_by_rcp<8>(p, a, s);
       case 4: return bwd_cl_by_rcp<4>(p, a, s);

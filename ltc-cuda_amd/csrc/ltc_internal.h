@@ -153,11 +153,44 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
 // Cluster path scratch: exchange words and a status word (nonzero after a
-// cluster member gave up waiting for its partners).
+// cluster member gave up waiting for its partners), plus the wait budget of
+// every exchange in ticks of the 100 MHz wall clock (<= 0: a member gives up
+// at its first wait, which the tests use to force the give-up path).
 struct ClusterBuf {
   unsigned long long* xch;
   int* status;
+  long long spin;
 };
+// Default wait budget: 0.2 s.
+constexpr long long kDefaultSpinTicks = 20000000;
+
+// Writes a list of contiguous float segments in one launch: each segment is
+// either copied from `src` or, with src == nullptr, filled with `value`. With
+// `gate` set, the launch does nothing unless *gate != 0, and then it also
+// raises the device's sticky fault flag (read by device_fault()): the
+// cluster paths use this to overwrite every output of a call with NaN after a
+// member gave up. A kernel, not hipMemsetAsync, so that a captured call
+// records kernel nodes only.
+struct FillSeg {
+  float* dst;
+  const float* src;
+  long long n;
+};
+constexpr int kMaxFillSegs = 20;
+struct FillList {
+  FillSeg seg[kMaxFillSegs];
+  int nseg;
+  float value;
+  const int* gate;
+};
+hipError_t launch_fill(const FillList& fl, hipStream_t s);
+// Adds a segment (ignored when dst is null or n is 0).
+inline void fill_add(FillList& fl, float* dst, const float* src, long long n) {
+  if (dst != nullptr && n > 0 && fl.nseg < kMaxFillSegs) fl.seg[fl.nseg++] = FillSeg{dst, src, n};
+}
+// The current device's sticky fault flag: reads it (after waiting for the
+// device) and clears it when `clear` is set. Returns the HIP status.
+hipError_t device_fault(int* value, bool clear);
 // Exchange words of one cluster launch (forward / chain).
 inline long long cluster_words(const Plan& p) { return 2LL * p.NCL * p.CP * p.NB * 64; }
 inline long long cluster_words_bwd(const Plan& p) {

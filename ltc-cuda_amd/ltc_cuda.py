@@ -69,7 +69,7 @@ class CApi:
         "ltc_ode_unfold_fwd_workspace_bytes", "ltc_ode_unfold_fwd",
         "ltc_sensory_bwd_workspace_bytes", "ltc_sensory_bwd",
         "ltc_ode_unfold_bwd_workspace_bytes", "ltc_ode_unfold_bwd",
-        "ltc_full_forward_noalloc",
+        "ltc_full_forward_noalloc", "ltc_device_status", "ltc_set_cluster_spin_ticks",
     )
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
@@ -145,6 +145,10 @@ class CApi:
         lib.ltc_ode_unfold_bwd.argtypes = (
             [_f32p] * 11 + [_int, _int, _int, _flt] + [_f32p] * 10
             + [_f32p, _i64, ctypes.c_void_p])
+        lib.ltc_device_status.restype = _int
+        lib.ltc_device_status.argtypes = [_int]
+        lib.ltc_set_cluster_spin_ticks.restype = _i64
+        lib.ltc_set_cluster_spin_ticks.argtypes = [_i64]
         lib.ltc_launch_plan.restype = _int
         lib.ltc_launch_plan.argtypes = [_int, _int, _int, _int, _int,
                                         ctypes.POINTER(ctypes.c_longlong), _int]
@@ -178,6 +182,12 @@ class CApi:
                 raise ValueError(f"unsupported LTC sizes B={B} T={T} D={D} H={H} U={U}")
             self._sizes[key] = v
         return v
+
+    def device_status(self, clear: bool = True) -> None:
+        """Raise RuntimeError if a cluster launch on the current device gave up
+        (its outputs were set to NaN); waits for the device. Clears the flag
+        unless clear is False."""
+        self.check(self.lib.ltc_device_status(1 if clear else 0), "ltc_device_status")
 
     def last_error(self) -> str:
         return self.lib.ltc_last_error().decode(errors="replace")
@@ -719,6 +729,13 @@ def require_kernels():
     if not _HAS_CUDA_KERNELS or _cuda_module is None:
         raise RuntimeError(f"LTC HIP extension is not loaded: {_LOAD_ERROR}")
     return _cuda_module
+
+
+def device_status(clear: bool = True) -> None:
+    """Raise RuntimeError if a cluster launch (H > 192) on the current device
+    gave up waiting for its partner workgroups since the last check; the
+    outputs of that call were set to NaN. Synchronises the device."""
+    require_kernels().capi.device_status(clear)
 
 
 class LTCCudaForward(torch.autograd.Function):

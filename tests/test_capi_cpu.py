@@ -288,3 +288,17 @@ def test_torch_extension_shares_the_library_and_validates_on_cpu():
     with pytest.raises(RuntimeError, match="17 LTC leaves"):
         ext.module_apply(torch.zeros(B, T, D), torch.zeros(B, H), leaves[:3], 0.1, 6, 1e-8,
                          1e-5)
+
+
+def test_cluster_wait_budget_and_status_without_gpu(capi):
+    """The budget setter needs no device; the status query reports the missing one."""
+    lib = capi.lib
+    prev = lib.ltc_set_cluster_spin_ticks(123)
+    try:
+        assert prev == 20000000
+        assert lib.ltc_set_cluster_spin_ticks(-1) == -1  # rejected, budget unchanged
+        assert lib.ltc_set_cluster_spin_ticks(0) == 123
+    finally:
+        lib.ltc_set_cluster_spin_ticks(prev)
+    if lib.ltc_device_count() == 0:
+        assert lib.ltc_device_status(0) == 3 and capi.last_error()

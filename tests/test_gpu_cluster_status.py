@@ -1,0 +1,93 @@
+"""A cluster member that gives up waiting is reported, and its call's outputs are NaN.
+
+The failure is forced from the host: a wait budget of 0 ticks makes every
+member leave at its first exchange (ltc_set_cluster_spin_ticks), so every
+kernel still exits normally. The call then overwrites every output it writes
+with NaN and raises the device's fault flag, which ltc_device_status()
+reports and clears.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import ltc_cuda
+from _gpu_common import DEV, _native, _perturbed_module, boundary, gpu_backward, gpu_forward  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+B, T, D, H = 16, 2, 8, 256
+DEFAULT_TICKS = 20000000
+
+
+@pytest.fixture()
+def capi():
+    c = ltc_cuda._cuda_module.capi
+    assert c.plan(B, T, D, H, 6)["CP"] > 0
+    c.device_status(clear=True)  # start clean
+    yield c
+    assert c.lib.ltc_set_cluster_spin_ticks(DEFAULT_TICKS) >= 0
+    c.lib.ltc_device_status(1)
+
+
+class _NoWait:
+    """Wait budget of 0 ticks inside the block, the default after it."""
+
+    def __init__(self, capi):
+        self.capi = capi
+
+    def __enter__(self):
+        assert self.capi.lib.ltc_set_cluster_spin_ticks(0) == DEFAULT_TICKS
+
+    def __exit__(self, *exc):
+        assert self.capi.lib.ltc_set_cluster_spin_ticks(DEFAULT_TICKS) == 0
+
+
+def _expect_fault(capi):
+    rc = capi.lib.ltc_device_status(1)
+    assert rc == 3 and "gave up" in capi.last_error(), (rc, capi.last_error())
+    assert capi.lib.ltc_device_status(0) == 0  # the first read cleared it
+
+
+def test_forward_give_up_sets_every_output_to_nan(capi):
+    args = boundary(B, T, D, H, seed=31)
+    with _NoWait(capi):
+        _, (out, h, saved) = gpu_forward(args, save=True)
+    assert torch.isnan(out).all() and torch.isnan(h).all() and torch.isnan(saved).all()
+    _expect_fault(capi)
+    # the default budget again: finite results and a clean status
+    _, (out, h, saved) = gpu_forward(args, save=True)
+    assert torch.isfinite(out).all() and torch.isfinite(h).all()
+    capi.device_status()
+
+
+def test_backward_give_up_sets_every_gradient_to_nan(capi):
+    args = boundary(B, T, D, H, seed=32)
+    dev_args, (out, h, saved) = gpu_forward(args, save=True)
+    assert torch.isfinite(out).all()
+    g_out = torch.randn(B, T, H, device=DEV)
+    g_h = torch.randn(B, H, device=DEV)
+    with _NoWait(capi):
+        grads = gpu_backward(dev_args, saved, g_out, g_h)
+    for g in grads:
+        assert torch.isnan(g).all()
+    _expect_fault(capi)
+    grads = gpu_backward(dev_args, saved, g_out, g_h)
+    for g in grads:
+        assert torch.isfinite(g).all()
+    capi.device_status()
+
+
+def test_module_path_give_up_is_reported_through_python(capi):
+    m = _perturbed_module(D, H, seed=33).to(DEV)
+    x = torch.randn(B, T, D, device=DEV)
+    with _NoWait(capi):
+        out, (h, _) = m(x)
+        out.sum().backward()
+    assert torch.isnan(out).all() and torch.isnan(h).all()
+    for n, p in m.named_parameters():
+        assert torch.isnan(p.grad).all(), n
+    with pytest.raises(RuntimeError, match="gave up"):
+        ltc_cuda.device_status()
+    ltc_cuda.device_status()  # cleared by the call that raised
