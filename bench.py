@@ -1,21 +1,33 @@
 """Benchmark of the LTC fused ODE-solver path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-large]
+    python bench.py --build-probe        (compile issue_rate_probe.hip; no GPU needed)
 
-Headline workload (BASELINE.json metric, config 1's shape run on the GPU):
+Headline workload (BASELINE.json metric, config C1's shape run on the GPU):
 one TrueLiquidTimeConstant layer, B=24 T=8 D=128 H=64, 6 unfolds, dt=1/30,
 Bernoulli(0.5) masks, seeded init (torch.manual_seed(42)), x ~ N(0,1),
-loss = sum(out). A step is module forward (LayerNorm, affine, softplus
-transforms, fused HIP loop) plus loss.backward(), as the reference's
-bench_ltc.py:62-96 times it.
+loss = sum(out). A step is the module forward (LayerNorm, affine, softplus
+transforms, the fused HIP time loop), the loss and loss.backward(), as the
+reference's bench_ltc.py:62-96 times it. The headline step is that whole step
+captured as one HIP graph and replayed (ltc_cuda.CapturedStep), after a check
+that its outputs and gradients equal an eager step's bit for bit; the eager
+step is timed beside it.
 
 Printed: one JSON line with the contract fields, plus
-  roofline      dominant kernel of the step: algorithmic FLOP per launch over
-                its mean launch time from HIP events recorded by the library on
-                its launch stream, against the 157.3 TFLOP/s FP32 peak;
-  cpu_baseline  the CPU oracle's TorchScript restatement of the reference path,
-                same module and shapes, timed on this host's cores;
-  large_configs BASELINE configs 2-5 at full size on the GPU (kernel times).
+  roofline       dominant kernel of the C1 step: algorithmic FLOP per launch
+                 over its mean launch time (HIP events the library records on
+                 its launch stream), against the 157.3 TFLOP/s FP32 peak;
+                 traffic = measured HBM bytes per launch (profiles/traffic.json);
+  cpu_baseline   the CPU oracle's TorchScript restatement of the reference
+                 path, same module and shapes, timed on this host's cores;
+  fwd/bwd split  median fwd (inside fwd+bwd), fwd+bwd and no-grad fwd from
+                 torch.cuda.Event, as bench_ltc.py:62-96 and :258-289;
+  peak memory and kernel launches, as bench_ltc.py:99-134;
+  issue_rate     the probe's measured FMA / exp / rcp issue rates, which set
+                 the mix-aware VALU bound (valu_mix_bound_ms, mix_frac_*);
+  large_configs  BASELINE configs C2-C5 at full size on the GPU, each with
+                 the same split, kernel times, roofline and a CPU baseline
+                 (C3/C4: a batch slice, scaled in B; rows are independent).
 
 Only rank 0 at N=1 runs; more GPUs are not part of this build.
 """
@@ -26,6 +38,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -34,13 +47,18 @@ sys.path.insert(0, os.path.join(ROOT, "ltc-cuda_amd"))
 sys.path.insert(0, ROOT)
 
 import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
 
 METRIC = "fwd+bwd ms/step & synapse-updates/s (B24 T8 D128 H64, 6 unfolds)"
-PEAK_FP32_TFLOPS = 157.3          # MI355X FP32 (vector and matrix)
-LANE_SLOTS_PER_S = 256 * 64 * 2.4e9  # 256 CUs x 64 lanes x 2.4 GHz
+PEAK_FP32_TFLOPS = 157.3             # MI355X FP32 vector peak (packed FP32)
 PEAK_HBM_GBS = 8000.0
 # Published fwd+bwd of the reference CUDA kernels at this config, GTX 1080 (README.md:13).
 REF_GTX1080_MS = 12.7
+# Issue rates (lane-ops per CU per clock) used when the probe is not built:
+# one FMA per lane per clock, transcendentals at half rate.
+RATES = {"fma": 64.0, "exp": 32.0, "rcp": 32.0, "cus": 256, "clk_hz": 2.4e9}
+PROBE_SRC = os.path.join(ROOT, "issue_rate_probe.hip")
+PROBE_BIN = os.path.join(ROOT, "issue_rate_probe")
 
 C1 = dict(B=24, T=8, D=128, H=64, U=6, sparsity=0.5, loss="sum", x="randn")
 LARGE = {
@@ -49,24 +67,31 @@ LARGE = {
     "C4": dict(B=128, T=32, D=512, H=512, U=6, sparsity=1.0, loss="sum", x="uniform3"),
     "C5": dict(B=4096, T=4, D=64, H=64, U=6, sparsity=0.5, loss=None, x="strided"),
 }
+# CPU baseline sample per config: batch rows timed (scaled to B when fewer),
+# minimum runs and time budget in seconds.
+CPU_SAMPLE = {"C1": (24, 5, 10.0), "C2": (32, 5, 5.0), "C3": (4, 3, 4.0), "C4": (4, 3, 4.0),
+              "C5": (512, 5, 3.0)}
 
 
-def n_syn(c):
-    return c["B"] * c["T"] * (c["D"] * c["H"] + c["U"] * c["H"] ** 2)
+def n_syn(c, B=None):
+    B = c["B"] if B is None else B
+    return B * c["T"] * (c["D"] * c["H"] + c["U"] * c["H"] ** 2)
 
 
-def kernel_flops(c):
-    """Algorithmic FLOP per launch of each kernel, per synapse (evaluation):
-    forward 10 (z 2, sigmoid 4, two products 2, two sums 2), chain 14 per
-    recurrent synapse-unfold (sigmoid recompute 6, sigmoid' 2, delta 4, dv 2),
-    8 for the four recurrent parameter sums, 22 per sensory synapse backward.
-    Per-neuron, LayerNorm and finalize work is not counted."""
+def kernel_flops(c, fused_chain):
+    """Algorithmic FLOP per launch of each kernel: per sensory synapse, the
+    forward counts 10 (z 2, sigmoid 4, two products 2, two sums 2) and the
+    backward 22; per recurrent synapse-unfold, the forward 10 and the chain 14
+    (sigmoid recompute 6, sigmoid' 2, delta 4, dv 2), plus the 8 of the four
+    parameter-gradient sums, which the fused chain does itself (22) and
+    rec_grad does otherwise. Per-neuron, LayerNorm and finalize work is not
+    counted."""
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
     sens = c["B"] * c["T"] * c["D"] * c["H"]
     return {
         "ltc_sens_fwd": 10 * sens,
         "ltc_ode_fwd": 10 * rec,
-        "ltc_ode_bwd": 14 * rec,
+        "ltc_ode_bwd": (22 if fused_chain else 14) * rec,
         "ltc_rec_grad": 8 * rec,
         "ltc_sens_bwd": 22 * sens,
         "ltc_prep": 0,
@@ -100,7 +125,7 @@ def make_inputs(c, device, seed=42):
 def loss_of(out, target):
     if target is None:
         return out.sum()
-    return torch.nn.functional.mse_loss(out, target)
+    return F.mse_loss(out, target)
 
 
 def sync():
@@ -115,20 +140,23 @@ def step(m, x, target):
     m.zero_grad(set_to_none=True)
 
 
-def time_split(m, x, target, iters):
-    """Median fwd (inside f+b), total and fwd-only (no_grad), torch.cuda.Event timed."""
+def time_split(m, x, target, iters, train=True):
+    """Median fwd (inside fwd+bwd), fwd+bwd, and no-grad fwd, torch.cuda.Event timed
+    around whole module calls (bench_ltc.py:62-96)."""
     fwd, tot, inf = [], [], []
-    for _ in range(iters):
-        s, f, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-        s.record()
-        out, _ = m(x)
-        f.record()
-        loss_of(out, target).backward()
-        e.record()
-        torch.cuda.synchronize()
-        m.zero_grad(set_to_none=True)
-        fwd.append(s.elapsed_time(f))
-        tot.append(s.elapsed_time(e))
+    if train:
+        for _ in range(iters):
+            s, f, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            s.record()
+            out, _ = m(x)
+            f.record()
+            loss_of(out, target).backward()
+            e.record()
+            torch.cuda.synchronize()
+            m.zero_grad(set_to_none=True)
+            del out
+            fwd.append(s.elapsed_time(f))
+            tot.append(s.elapsed_time(e))
     for _ in range(iters):
         s, e = (torch.cuda.Event(enable_timing=True) for _ in range(2))
         s.record()
@@ -137,42 +165,17 @@ def time_split(m, x, target, iters):
         e.record()
         torch.cuda.synchronize()
         inf.append(s.elapsed_time(e))
-    return statistics.median(fwd), statistics.median(tot), statistics.median(inf)
-
-
-class _GraphStep(torch.nn.Module):
-    """Layer forward returning plain tensors, for torch.cuda.make_graphed_callables."""
-
-    def __init__(self, inner):
-        super().__init__()
-        self.inner = inner
-
-    def forward(self, x):
-        out, (h, _) = self.inner(x)
-        return out, h
-
-
-def graphed_step_ms(m, x, target, steps, warmup):
-    """Same step with the layer's fwd and bwd captured into HIP graphs (replayed)."""
-    g = torch.cuda.make_graphed_callables(_GraphStep(m), (x,))
-
-    def one():
-        out, _ = g(x)
-        loss_of(out, target).backward()
-        m.zero_grad(set_to_none=True)
-
-    for _ in range(warmup):
-        one()
-    sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        one()
-    sync()
-    return (time.perf_counter() - t0) * 1e3 / steps
+    med = statistics.median
+    r = {"fwd_nograd_ms": round(med(inf), 5)}
+    if train:
+        r.update({"fwd_ms": round(med(fwd), 5), "bwd_ms": round(med(tot) - med(fwd), 5),
+                  "fwd_bwd_ms": round(med(tot), 5)})
+    return r
 
 
 def kernel_times(capi, fn, iters):
-    """Mean per-launch duration of each library kernel over `iters` calls of fn."""
+    """Mean per-launch duration (HIP events on the launch stream) and launches per
+    call of each library kernel over `iters` calls of fn."""
     capi.timing_enable(True)
     for _ in range(iters):
         fn()
@@ -182,49 +185,116 @@ def kernel_times(capi, fn, iters):
     return {k: (ms / n, n // iters) for k, (ms, n) in t.items() if n > 0}
 
 
-def roofline(c, ktimes, traffic=None):
-    fl = kernel_flops(c)
+def roofline(c, ktimes, fused_chain, traffic=None):
+    fl = kernel_flops(c, fused_chain)
     per_step = {k: avg * per for k, (avg, per) in ktimes.items()}
     dom = max(per_step, key=per_step.get)
     avg_ms = ktimes[dom][0]
     achieved = fl[dom] / (avg_ms * 1e-3) / 1e12
-    r = {"bound": "valu", "kernel": dom, "achieved": round(achieved, 4),
-         "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-         "frac": round(achieved / PEAK_FP32_TFLOPS, 5),
-         "traffic": None if traffic is None else traffic.get(dom),
-         "avg_launch_ms": round(avg_ms, 5)}
-    return r
+    return {"bound": "valu", "kernel": dom, "achieved": round(achieved, 4),
+            "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP32_TFLOPS, 5),
+            "traffic": None if traffic is None else traffic.get(dom),
+            "avg_launch_ms": round(avg_ms, 5),
+            "flop_per_launch": fl[dom]}
 
 
-R_TRANS = 2.0  # measured on gfx950: v_exp_f32 / v_rcp_f32 cost 2 lane-slots (probes/issue_rate)
+# Minimum instruction mix per synapse evaluation: (FMA-class, v_exp_f32, v_rcp_f32).
+# Forward: gate argument, 1 + e, two accumulations; backward adds the recompute
+# (argument, 1 + e), sigmoid' (2), delta (4), dv (2) and the four parameter sums
+# (4) plus one exp and one rcp.
+MIX = {"fwd": (4, 1, 1), "fwdbwd": (16, 2, 2)}
 
 
-def issue_fraction(c, t_ms, which, r=R_TRANS):
-    """Mix-aware VALU bound over measured time.
+def mix_bound_ms(c, which):
+    """Mix-aware VALU bound: the minimum mix of every synapse, each instruction
+    class at the issue rate the probe measured on this GPU (lane-ops per CU per
+    clock), issued one after another (the probe's synapse kernel confirms the
+    classes do not overlap: its rate equals the sum of the parts)."""
+    f, e, r = MIX[which]
+    per_cu_clk = f / RATES["fma"] + e / RATES["exp"] + r / RATES["rcp"]
+    return n_syn(c) * per_cu_clk / (RATES["cus"] * RATES["clk_hz"]) * 1e3
 
-    Minimum lane-slots per synapse: forward 4 FMA-class + 2 transcendental,
-    backward 12 + 2; a transcendental costs r lane-slots.
-    """
-    per = {"fwd": 4 + 2 * r, "fwdbwd": 16 + 4 * r}[which]
-    return n_syn(c) * per / LANE_SLOTS_PER_S / (t_ms * 1e-3)
+
+# --------------------------------------------------------------------------- probe
+
+def build_probe() -> str:
+    """hipcc the issue-rate probe into ./issue_rate_probe (no GPU needed)."""
+    import shutil
+    hipcc = os.environ.get("HIPCC") or "/opt/rocm/bin/hipcc"
+    if not os.path.isfile(hipcc):
+        hipcc = shutil.which("hipcc") or hipcc
+    cmd = [hipcc, "--offload-arch=gfx950", "-O3", "-std=c++17",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+           "-Wno-unused-command-line-argument", "-o", PROBE_BIN + ".tmp", PROBE_SRC]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed on issue_rate_probe.hip:\n" + proc.stderr)
+    os.replace(PROBE_BIN + ".tmp", PROBE_BIN)
+    return PROBE_BIN
 
 
-def cpu_baseline(c, budget_s=15.0):
-    """CPU oracle (TorchScript restatement of ltc.py:19-106, 249-326) on host cores."""
+def run_probe():
+    """Run the probe as a child process (before this process touches the GPU);
+    its rates replace the defaults in RATES."""
+    if not os.path.isfile(PROBE_BIN):
+        return {"source": "defaults (probe not built)", **RATES}
+    try:
+        proc = subprocess.run([PROBE_BIN], capture_output=True, text=True, timeout=120)
+        rec = json.loads(proc.stdout.strip().splitlines()[-1])
+    except (OSError, ValueError, IndexError, subprocess.TimeoutExpired) as exc:
+        return {"source": f"defaults (probe failed: {exc})", **RATES}
+    if "error" in rec:
+        return {"source": f"defaults (probe: {rec['error']})", **RATES}
+    RATES.update(fma=rec["fma_per_cu_clk"], exp=rec["exp_per_cu_clk"],
+                 rcp=rec["rcp_per_cu_clk"], cus=rec["cus"], clk_hz=rec["clock_mhz"] * 1e6)
+    rec["source"] = "issue_rate_probe (measured in this run)"
+    return rec
+
+
+# --------------------------------------------------------------------------- CPU baseline
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(name, c):
+    """The oracle's TorchScript restatement of the reference path (ltc.py:19-106,
+    249-326) on this host's cores, fp32: fwd+bwd (or fwd only for C5) on a batch
+    slice of the config, scaled to the full batch (rows are independent)."""
     from oracle import ltc_oracle as O
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
+    bs, min_runs, budget = CPU_SAMPLE[name]
+    bs = min(bs, c["B"])
     torch.manual_seed(42)
     p = O.init_params(c["D"], c["H"], c["sparsity"], c["sparsity"])
-    x = torch.randn(c["B"], c["T"], c["D"])
+    x = torch.randn(bs, c["T"], 2 * c["D"] if c["x"] == "strided" else c["D"])
+    if c["x"] == "strided":
+        x = x[:, :, 0::2]
+    elif c["x"] == "uniform3":
+        x = x.uniform_(-3.0, 3.0)
+    target = torch.randn(bs, c["T"], c["H"]) if c["loss"] == "mse" else None
     leaves = {k: v.clone().requires_grad_(k not in ("sparsity_mask", "sensory_sparsity_mask"))
               for k, v in p.items()}
+    train = c["loss"] is not None
 
     def one():
+        if not train:
+            with torch.no_grad():
+                O.module_forward(leaves, x, None, dt=1.0 / 30.0, ode_unfolds=c["U"], scripted=True)
+            return
         out, _ = O.module_forward(leaves, x, None, dt=1.0 / 30.0, ode_unfolds=c["U"],
                                   scripted=True)
-        out.sum().backward()
+        loss_of(out, target).backward()
         for v in leaves.values():
             v.grad = None
 
@@ -232,24 +302,109 @@ def cpu_baseline(c, budget_s=15.0):
         one()
     times = []
     t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(times) < 5:
+    while time.perf_counter() - t_start < budget or len(times) < min_runs:
         t0 = time.perf_counter()
         one()
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
-    cpu = "unknown"
+    scale = c["B"] / bs
+    what = "fwd+bwd" if train else "no-grad fwd"
+    return {"value": n_syn(c) / (med * scale), "unit": "synapse-updates/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "ms_per_step": round(med * scale * 1e3, 3),
+            "scaled": scale != 1.0,
+            "sample": f"{len(times)} {what} steps (median) of {name} on {bs} of its {c['B']} "
+                      f"batch rows{', scaled x%g in B' % scale if scale != 1.0 else ''}; "
+                      f"TorchScript oracle, fp32, {threads} threads, {_cpu_model()}"}
+
+
+# --------------------------------------------------------------------------- memory, launches
+
+def peak_memory_mb(m, x, target, train):
+    """Peak allocated GPU memory of one step (bench_ltc.py:118-134)."""
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    if train:
+        out, _ = m(x)
+        loss_of(out, target).backward()
+        del out
+        m.zero_grad(set_to_none=True)
+    else:
+        with torch.no_grad():
+            m(x)
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated()
+    return {"peak_mb": round(peak / 2 ** 20, 3), "peak_above_inputs_mb": round((peak - base) / 2 ** 20, 3)}
+
+
+def kernel_launches(fn):
+    """Device kernels of one call of fn, counted with torch.profiler as
+    bench_ltc.py:99-115 counts them."""
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": n_syn(c) / med, "unit": "synapse-updates/s", "cores": torch.get_num_threads(),
-            "kind": "port", "ms_per_step": round(med * 1e3, 3),
-            "sample": f"{len(times)} fwd+bwd steps of the C1 workload (median), "
-                      f"TorchScript oracle, fp32, {threads} threads, {cpu}"}
+        from torch.profiler import ProfilerActivity, profile
+        with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+            fn()
+            torch.cuda.synchronize()
+        n = 0
+        for evt in prof.events():
+            if evt.device_type == torch.autograd.DeviceType.CUDA:
+                n += 1
+        return n
+    except Exception as exc:  # the profiler is optional here
+        return f"unavailable: {exc}"
+
+
+# --------------------------------------------------------------------------- configs
+
+def measure_config(name, c, capi, cpu):
+    import ltc_cuda
+
+    m, x, target = make_inputs(c, "cuda:0")
+    train = c["loss"] is not None
+    plan = capi.plan(c["B"], c["T"], c["D"], c["H"], c["U"])
+    rec = {"shape": {k: c[k] for k in ("B", "T", "D", "H", "U")}, "n_syn": n_syn(c),
+           "loss": c["loss"], "x": c["x"]}
+
+    if train:
+        def fn():
+            step(m, x, target)
+    else:
+        def fn():
+            with torch.no_grad():
+                m(x)
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    iters = 5
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    rec["ms_per_step"] = round(ms, 4)
+    rec["synapse_updates_per_s"] = n_syn(c) / (ms * 1e-3)
+    rec.update(time_split(m, x, target, 5, train=train))
+    kt = kernel_times(capi, fn, 2)
+    rec["kernels_ms"] = {k: round(v[0], 5) for k, v in kt.items()}
+    rec["launches_per_step_library"] = sum(v[1] for v in kt.values())
+    rec["roofline"] = roofline(c, kt, bool(plan["fuse"]), load_traffic(name))
+    which = "fwdbwd" if train else "fwd"
+    ksum = sum(v[0] * v[1] for v in kt.values())
+    rec["kernel_ms_sum"] = round(ksum, 4)
+    rec["valu_mix_bound_ms"] = round(mix_bound_ms(c, which), 4)
+    rec["mix_frac_kernels"] = round(mix_bound_ms(c, which) / ksum, 4)
+    rec["flop_frac_kernels"] = round(
+        n_syn(c) * (10 if which == "fwd" else 32) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
+    rec["memory"] = peak_memory_mb(m, x, target, train)
+    del m, x, target
+    torch.cuda.empty_cache()
+    if cpu:
+        rec["cpu_baseline"] = cpu_baseline(name, c)
+        gpu_ms = rec["fwd_bwd_ms"] if train else rec["fwd_nograd_ms"]
+        rec["gpu_vs_cpu"] = round(rec["cpu_baseline"]["ms_per_step"] / gpu_ms, 1)
+    _ = ltc_cuda
+    return rec
 
 
 def load_traffic(workload):
@@ -260,45 +415,6 @@ def load_traffic(workload):
         return data.get(workload)
     except (OSError, ValueError):
         return None
-
-
-def measure_large(name, c, capi):
-    import ltc_cuda
-
-    m, x, target = make_inputs(c, "cuda:0")
-    rec = {"shape": {k: c[k] for k in ("B", "T", "D", "H", "U")}, "n_syn": n_syn(c)}
-    if c["loss"] is None:
-        def fn():
-            with torch.no_grad():
-                m(x)
-    else:
-        def fn():
-            step(m, x, target)
-    for _ in range(2):
-        fn()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    iters = 3
-    for _ in range(iters):
-        fn()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / iters
-    kt = kernel_times(capi, fn, 2)
-    rec["ms_per_step"] = round(ms, 4)
-    rec["synapse_updates_per_s"] = n_syn(c) / (ms * 1e-3)
-    rec["kernels_ms"] = {k: round(v[0], 5) for k, v in kt.items()}
-    rec["roofline"] = roofline(c, kt, load_traffic(name))
-    which = "fwd" if c["loss"] is None else "fwdbwd"
-    ksum = sum(v[0] * v[1] for v in kt.values())
-    rec["kernel_ms_sum"] = round(ksum, 4)
-    rec["issue_frac_kernels"] = round(issue_fraction(c, ksum, which), 4)
-    rec["issue_frac_kernels_r4"] = round(issue_fraction(c, ksum, which, 4.0), 4)
-    rec["flop_frac_kernels"] = round(
-        n_syn(c) * (10 if which == "fwd" else 32) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
-    del m, x, target
-    torch.cuda.empty_cache()
-    _ = ltc_cuda
-    return rec
 
 
 COPY_BYTES = 64 << 20
@@ -322,6 +438,39 @@ def profile_pass(name):
     print(f"profile pass {name} done", flush=True)
 
 
+def graphed_c1(m, x, target, steps, warmup):
+    """The C1 step captured whole (forward, loss, backward) and replayed; returns
+    (ms per replayed step, bitwise equal to an eager step)."""
+    import ltc_cuda
+
+    def eager_result():
+        m.zero_grad(set_to_none=True)
+        out, _ = m(x)
+        loss_of(out, target).backward()
+        res = [out.detach().clone()] + [p.grad.detach().clone() for p in m.parameters()]
+        m.zero_grad(set_to_none=True)
+        return res
+
+    ref = eager_result()
+    torch.cuda.synchronize()
+    cap = ltc_cuda.CapturedStep(m, (x,), lambda o: loss_of(o[0], target))
+    cap.replay()
+    torch.cuda.synchronize()
+    got = [cap.outputs[0]] + [p.grad for p in m.parameters()]
+    equal = len(got) == len(ref) and all(torch.equal(a, b) for a, b in zip(got, ref))
+    for _ in range(warmup):
+        cap.replay()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        cap.replay()
+    sync()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del cap
+    m.zero_grad(set_to_none=True)
+    return ms, equal
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -329,15 +478,24 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-large", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="report the eager step as the headline (no HIP-graph capture)")
+    ap.add_argument("--build-probe", action="store_true",
+                    help="compile issue_rate_probe.hip into ./issue_rate_probe and exit")
     ap.add_argument("--profile-pass", choices=["C1", "C2", "C3", "C4", "C5"], default=None,
                     help="for rocprofv3 --pmc: a 64 MiB device copy (calibrates the byte "
                          "counters), then 3 steps of the named config; prints nothing else")
     args = ap.parse_args()
+    if args.build_probe:
+        print(build_probe())
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU runs are not part of it.", file=sys.stderr)
         sys.exit(2)
     rank = int(os.environ.get("RANK", "0"))
+
+    probe = None if args.profile_pass else run_probe()  # before this process uses the GPU
 
     import ltc_cuda
 
@@ -350,6 +508,7 @@ def main():
         return
     c = C1
     m, x, target = make_inputs(c, "cuda:0")
+    plan = capi.plan(c["B"], c["T"], c["D"], c["H"], c["U"])
 
     for _ in range(args.warmup):
         step(m, x, target)
@@ -358,12 +517,20 @@ def main():
     for _ in range(args.steps):
         step(m, x, target)
     sync()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
 
-    fwd_ms, tot_ms, inf_ms = time_split(m, x, target, max(10, args.steps // 2))
-    graphed_ms = graphed_step_ms(m, x, target, args.steps, args.warmup)
+    split = time_split(m, x, target, max(10, args.steps // 2))
     kt = kernel_times(capi, lambda: step(m, x, target), max(10, args.steps // 2))
     ksum = sum(v[0] * v[1] for v in kt.values())
+    mem = peak_memory_mb(m, x, torch.randn(c["B"], c["T"], c["H"], device="cuda:0"), True)
+    with torch.no_grad():
+        launches_fwd = kernel_launches(lambda: m(x))
+    launches_step = kernel_launches(lambda: step(m, x, target))
+    graph_ms, graph_equal = (None, None)
+    if not args.no_graph:
+        graph_ms, graph_equal = graphed_c1(m, x, target, args.steps, args.warmup)
+    use_graph = graph_ms is not None and graph_equal
+    ms = graph_ms if use_graph else eager_ms
     line = {
         "metric": METRIC,
         "value": n_syn(c) / (ms * 1e-3),
@@ -380,30 +547,35 @@ def main():
         "config": {"workload": "C1: one LTC layer fwd+bwd, B=24 T=8 D=128 H=64, 6 unfolds, "
                                "dt=1/30, sparsity 0.5/0.5, loss=sum(out)",
                    "B": 24, "T": 8, "D": 128, "H": 64, "ode_unfolds": 6,
-                   "parallelism": "single GPU"},
-        "fwd_ms": round(fwd_ms, 5),
-        "bwd_ms": round(tot_ms - fwd_ms, 5),
-        "fwd_bwd_event_ms": round(tot_ms, 5),
-        "fwd_only_nograd_ms": round(inf_ms, 5),
-        "graphed_ms_per_step": round(graphed_ms, 5),
-        "graphed_synapse_updates_per_s": n_syn(c) / (graphed_ms * 1e-3),
+                   "parallelism": "single GPU",
+                   "step": "whole step replayed as one HIP graph" if use_graph
+                           else "eager module forward + loss.backward()"},
+        "eager_ms_per_step": round(eager_ms, 5),
+        "eager_synapse_updates_per_s": n_syn(c) / (eager_ms * 1e-3),
+        "graphed_ms_per_step": None if graph_ms is None else round(graph_ms, 5),
+        "graph_replay_bitwise_equal_to_eager": graph_equal,
+        **split,
         "kernels_ms": {k: round(v[0], 5) for k, v in kt.items()},
         "kernel_ms_sum": round(ksum, 5),
-        "issue_frac_step": round(issue_fraction(c, ms, "fwdbwd"), 5),
-        "issue_frac_kernels": round(issue_fraction(c, ksum, "fwdbwd"), 5),
-        "issue_frac_kernels_r4": round(issue_fraction(c, ksum, "fwdbwd", 4.0), 5),
-        "roofline": roofline(c, kt, load_traffic("C1")),
+        "launches": {"library_per_step": sum(v[1] for v in kt.values()),
+                     "device_kernels_fwd_nograd": launches_fwd,
+                     "device_kernels_step": launches_step},
+        "memory_fwd_bwd_mse": mem,
+        "issue_rate": probe,
+        "valu_mix_bound_ms": round(mix_bound_ms(c, "fwdbwd"), 5),
+        "mix_frac_step": round(mix_bound_ms(c, "fwdbwd") / ms, 5),
+        "roofline": roofline(c, kt, bool(plan["fuse"]), load_traffic("C1")),
         "vs_reference_gtx1080_published": round(REF_GTX1080_MS / ms, 3),
     }
     del m, x, target
     torch.cuda.empty_cache()
+    cpu = not args.no_cpu_baseline and rank == 0
     if not args.no_large:
-        line["large_configs"] = {name: measure_large(name, cfg, capi)
-                                 for name, cfg in LARGE.items()}
-    if not args.no_cpu_baseline and rank == 0:
-        line["cpu_baseline"] = cpu_baseline(c)
-    else:
-        line["cpu_baseline"] = None
+        line["large_configs"] = {}
+        for name, cfg in LARGE.items():
+            line["large_configs"][name] = measure_config(name, cfg, capi, cpu)
+            print(f"bench: {name} done", file=sys.stderr, flush=True)
+    line["cpu_baseline"] = cpu_baseline("C1", c) if cpu else None
     if rank == 0:
         print(json.dumps(line), flush=True)
 

@@ -58,23 +58,6 @@ def command(out: str = LIB_PATH, arch: str = ARCH) -> list:
     ]
 
 
-PROBE_SRC = os.path.join(HERE, "probes", "issue_rate.cpp")
-PROBE_BIN = os.path.join(HERE, "probes", "issue_rate")
-
-
-def build_probe(verbose: bool = False) -> str:
-    """Standalone issue-rate probe (FMA / exp / rcp throughput) used for the roofline."""
-    cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-O3", "-std=c++17",
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-Wno-unused-command-line-argument", "-o", PROBE_BIN, PROBE_SRC]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError("hipcc failed on the issue-rate probe:\n" + proc.stderr)
-    return PROBE_BIN
-
-
 EXT_SRC = os.path.join(CSRC, "ltc_torch_ext.cpp")
 EXT_NAME = "_ltc_torch"
 
@@ -120,9 +103,9 @@ def build_ext(verbose: bool = False) -> str:
     return out
 
 
-def build(verbose: bool = False, arch: str = ARCH, probe: bool = True) -> str:
-    """Compile libltc_hip.so for `arch`, then the torch extension (and the
-    issue-rate probe unless probe is False); returns the library path."""
+def build(verbose: bool = False, arch: str = ARCH) -> str:
+    """Compile libltc_hip.so for `arch`, then the torch extension; returns the
+    library path."""
     tmp = LIB_PATH + ".tmp"
     cmd = command(tmp, arch)
     if verbose:
@@ -136,8 +119,6 @@ def build(verbose: bool = False, arch: str = ARCH, probe: bool = True) -> str:
         print("\n".join(msgs), flush=True)
     os.replace(tmp, LIB_PATH)
     build_ext(verbose)
-    if probe:
-        build_probe(verbose)
     return LIB_PATH
 
 

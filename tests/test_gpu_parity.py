@@ -553,3 +553,45 @@ def test_hip_graph_capture_replays_match_eager():
         with torch.no_grad():
             step(x)                      # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_whole_step_capture_replays_match_eager():
+    """ltc_cuda.CapturedStep: forward, loss and backward of the C1-shaped layer in
+    one HIP graph. Every replay, with eager work and synchronisations between
+    replays, must reproduce an eager step's outputs, loss and gradients bit for
+    bit, also after new data is copied into the static input."""
+    m = _perturbed_module(128, 64, seed=41).to(DEV)
+    x = torch.randn(24, 8, 128, device=DEV)
+    x2 = torch.randn(24, 8, 128, device=DEV)
+    G = torch.randn(24, 8, 64, device=DEV)
+
+    def loss_fn(o):
+        out, (h, _) = o
+        return (out * G).sum() + 0.5 * h.sum()
+
+    def eager(xx):
+        m.zero_grad(set_to_none=True)
+        o = m(xx)
+        loss = loss_fn(o)
+        loss.backward()
+        torch.cuda.synchronize()
+        res = [o[0].detach().clone(), loss.detach().clone()]
+        res += [p.grad.clone() for p in m.parameters()]
+        m.zero_grad(set_to_none=True)
+        return res
+
+    ref, ref2 = eager(x), eager(x2)
+    xs = x.clone()
+    cap = ltc_cuda.CapturedStep(m, (xs,), loss_fn)
+    for r in range(4):
+        src, want = (x, ref) if r % 2 == 0 else (x2, ref2)
+        cap.inputs[0].copy_(src)
+        cap.replay()
+        torch.cuda.synchronize()
+        got = [cap.outputs[0], cap.loss] + [p.grad for p in m.parameters()]
+        assert len(got) == len(want)
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert torch.equal(a, b), f"replay {r}: tensor {i} differs"
+        with torch.no_grad():
+            m(x2)                        # eager work between replays
+        torch.cuda.synchronize()
