@@ -798,23 +798,24 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 // Single-row kernels at Hp = 64 (NB = 1: one wave spans all columns).
 // Every wave keeps the row's per-column state in lane o and updates it from
 // the same KS partials in the same fixed order, so the copies agree bitwise;
-// a wave reads the values of its own synapse rows with v_readlane instead of
-// through LDS. That leaves one barrier per unfold: the partials alternate
+// a wave reads the values of its own synapse rows back from its private LDS
+// copy, with no barrier. That leaves one barrier per unfold: the partials alternate
 // between two LDS buffers by unfold parity, and a buffer is rewritten two
 // unfolds later, after every wave has passed the barrier that follows its
 // reads. The forward's results are bitwise those of ode_fwd_kernel; the
 // chain's match ode_bwd_kernel's to the rounding of the multiply-adds the
 // compiler contracts differently in the two bodies.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
 template <int RCP>
 __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
   constexpr int HP = 64, KS = HP / RCP;
   extern __shared__ float4 lds4[];
   float2* red = reinterpret_cast<float2*>(lds4);  // [2][KS][64]
+  // Each wave's own copy of the row state, [KS][64]: a wave writes it and
+  // reads its synapse rows back as broadcasts (all lanes one address), so the
+  // values reach the VALU without a v_readlane per synapse; the LDS orders one
+  // wave's accesses, so no barrier is needed.
+  float* vw = reinterpret_cast<float*>(red + 2 * KS * HP);
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int tid = threadIdx.x;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
@@ -841,9 +842,20 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
       // The gates of all RCP synapses in phases (arguments, exponentials,
       // reciprocals), so that each transcendental's result is consumed
       // several instructions later; the sums keep their order.
+      float* vme = vw + ks * HP;
+      vme[o] = v;
+      float vi[RCP];
+#pragma unroll
+      for (int q = 0; q < RCP; q += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(vme + r0 + q);
+        vi[q] = w4.x;
+        vi[q + 1] = w4.y;
+        vi[q + 2] = w4.z;
+        vi[q + 3] = w4.w;
+      }
       float z[RCP];
 #pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) z[rr] = fmaf(preg[rr].x, lane_value(v, r0 + rr), preg[rr].y);
+      for (int rr = 0; rr < RCP; ++rr) z[rr] = fmaf(preg[rr].x, vi[rr], preg[rr].y);
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
 #pragma unroll
@@ -890,6 +902,9 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
   constexpr int HP = 64, KS = HP / RCP;
   extern __shared__ float4 lds4[];
   float* red = reinterpret_cast<float*>(lds4);  // [2][KS][64]
+  // Each wave's own copy of alpha/beta, [KS][64] float2, read back as
+  // broadcasts (see ode_fwd_row_kernel).
+  float2* abw = reinterpret_cast<float2*>(red + 2 * KS * HP);
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int tid = threadIdx.x;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
@@ -950,11 +965,20 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
       for (int rr = 0; rr < RCP; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
+      float2* abme = abw + ks * HP;
+      abme[o] = make_float2(al, be);
+      float2 abj[RCP];
+#pragma unroll
+      for (int q = 0; q < RCP; q += 2) {
+        const float4 w4 = *reinterpret_cast<const float4*>(abme + r0 + q);
+        abj[q] = make_float2(w4.x, w4.y);
+        abj[q + 1] = make_float2(w4.z, w4.w);
+      }
       float acc = 0.f;
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) {
         const float4 p = preg[rr];
-        const float cx = lane_value(al, r0 + rr), cy = lane_value(be, r0 + rr);
+        const float cx = abj[rr].x, cy = abj[rr].y;
         const float a = ga[rr];
         const float a2 = fmaf(-a, a, a);
         const float dl = fmaf(cx, p.z, cy * p.w) * a2;
@@ -1758,6 +1782,25 @@ __device__ __forceinline__ bool xch_gather(unsigned long long* slot, int p, int 
   return true;
 }
 
+// Cluster and member of workgroup g. Workgroup g runs on XCD g % 8. By
+// default member p = g % CP, so the members of a cluster spread over the XCDs
+// and each XCD's L2 holds only the operand-image columns of the members it
+// runs (what the streamed forms read every unfold). With `xcd_local` (used
+// when operands are register-resident and NCL is a multiple of 8) all members
+// of a cluster run on one XCD instead: cluster cl lives on XCD cl % 8, so the
+// saved rows all its members read come through one L2.
+__device__ __forceinline__ void cluster_coords(int g, int CP, bool xcd_local, int& p, int& cl) {
+  if (xcd_local) {
+    const int xcd = g & 7, slot = g >> 3;
+    const int q = slot / CP;
+    p = slot - q * CP;
+    cl = xcd + 8 * q;
+  } else {
+    cl = g / CP;
+    p = g - cl * CP;
+  }
+}
+
 struct FwdCK {
   const float4* recF;  // [Hp + 8][Hp]: 8 zero rows of slack for the streamed prefetch
   const float* neuron;
@@ -1772,6 +1815,7 @@ struct FwdCK {
   int* status;
   long long spin;  // wait budget of each exchange, wall-clock ticks
   int B, T, H, Hp, U, KS, RC, CP;
+  int xcd_local;   // cluster_coords: all members of a cluster on one XCD
   float eps;
 };
 
@@ -1786,7 +1830,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][64]
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
-  const int p = blockIdx.x % CP, cl = blockIdx.x / CP;
+  int p, cl;
+  cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
   const int c = p * kClW + o;  // output column of this thread
   const int b0 = cl * NB;
   const int r0 = ks * RC;
@@ -1979,6 +2024,7 @@ struct BwdCK {
   int* status;
   long long spin;  // wait budget of each exchange, wall-clock ticks
   int B, T, H, Hp, U, KS, RC, CP;
+  int xcd_local;   // cluster_coords: all members of a cluster on one XCD
 };
 
 // Cluster chain: member p forms dL/dv_i for its JW columns i (reduction over
@@ -2016,7 +2062,8 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   // With JW = 64 ks is uniform across each wave; with JW = 32 a wave holds two.
   const int ks = JW == 64 ? __builtin_amdgcn_readfirstlane(tid / JW) : tid / JW;
   const int o = tid % JW;
-  const int p = blockIdx.x % CP, cl = blockIdx.x / CP;
+  int p, cl;
+  cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
   const int c = p * JW + o;
   const int b0 = cl * NB;
   const int r0 = ks * RC;
@@ -2512,8 +2559,10 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
   if (p.CP > 0) {
     hipError_t e = clear_cluster(p, cb, false, s);
     if (e != hipSuccess) return e;
+    // Register-resident operands (RC = 16) read no image from L2 in the loop.
+    const int xl = (p.RC == 16 && p.NCL % 8 == 0) ? 1 : 0;
     FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
-            cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, eps};
+            cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, xl, eps};
     switch (p.NB) {
       case 8: return fwd_cl_by_rcp<8>(p, a, s);
       case 4: return fwd_cl_by_rcp<4>(p, a, s);
@@ -2540,9 +2589,12 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
   if (p.CP > 0) {
     hipError_t e = clear_cluster(p, cb, true, s);
     if (e != hipSuccess) return e;
+    // The register-resident fused chain (Hp = 256) prefetches saved rows that
+    // every member of a cluster reads: keep a cluster on one XCD.
+    const int xl = (chain_prefetches(p) && p.NCLB % 8 == 0) ? 1 : 0;
     BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
             gstate, rpart, cb.xch, cb.status, cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB,
-            p.CPB};
+            p.CPB, xl};
     switch (p.NBB) {
       case 8: return bwd_cl_by_rcp<8>(p, a, s);
       case 4: return bwd_cl_by_rcp<4>(p, a, s);

@@ -217,7 +217,8 @@ inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp =
 // partials, or the single-row kernel's two partial buffers.
 inline long long fwd_lds(const Plan& p) {
   const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8;
-  const long long row = row_kernels(p) ? 2LL * p.KS * p.Hp * 8 : 0;
+  // single-row kernel: two partial buffers and each wave's copy of the state
+  const long long row = row_kernels(p) ? 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4 : 0;
   return base > row ? base : row;
 }
 
@@ -228,7 +229,9 @@ inline long long fwd_lds(const Plan& p) {
 // stores.
 inline long long chain_lds(const Plan& p) {
   long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
-  if (row_kernels(p) && 2LL * p.KSB * p.Hp * 4 > base) base = 2LL * p.KSB * p.Hp * 4;
+  // single-row chain: two partial buffers and each wave's copy of alpha/beta
+  const long long rowb = 2LL * p.KSB * p.Hp * 4 + (long long)p.KSB * p.Hp * 8;
+  if (row_kernels(p) && rowb > base) base = rowb;
   const long long plane =
       p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;
   return base > plane ? base : plane;

@@ -78,6 +78,7 @@ CLUSTER_SHAPES = [  # (B, T, D, H, expected CP, expected NB)
     (45, 1, 8, 512, 8, 2),
     (100, 1, 4, 512, 8, 4),
     (20, 1, 4, 1000, 16, 2),   # Hp 1024
+    (64, 2, 8, 256, 4, 1),     # 64 and 32 clusters: each cluster on one XCD (register-resident forms)
 ]
 
 
@@ -98,7 +99,8 @@ def test_cluster_path_forward_matches_oracle(shape):
 
 
 @pytest.mark.parametrize("shape", [CLUSTER_SHAPES[0], CLUSTER_SHAPES[3], CLUSTER_SHAPES[4],
-                                   CLUSTER_SHAPES[5], CLUSTER_SHAPES[6], (9, 2, 8, 256, 4, 1),
+                                   CLUSTER_SHAPES[5], CLUSTER_SHAPES[6], CLUSTER_SHAPES[7],
+                                   (9, 2, 8, 256, 4, 1),
                                    (250, 1, 4, 256, 4, 4), (9, 2, 8, 500, 8, 1)],
                          ids=lambda s: "B%dT%dD%dH%d" % s[:4])
 def test_cluster_path_backward_matches_oracle(shape):
