@@ -896,8 +896,10 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
 
 // Fused chain (FUSE) of one row at Hp = 64: thread (ks, o) holds the RCP
 // synapses (i = o, j = ks*RCP + rr) with their four gradient sums. Launched
-// with RCP = 8 (8 waves): measured 44 us against 45.5 us at RCP = 4 (C1).
-template <int RCP>
+// with RCP = 8 (8 waves): 33.9 us at C1 against 36.5 us at RCP = 4 (rocprofv3
+// kernel trace, 200 launches).
+// FULL: H == 64, so every column is live and no lane needs masking.
+template <int RCP, bool FULL>
 __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
   constexpr int HP = 64, KS = HP / RCP;
   extern __shared__ float4 lds4[];
@@ -910,7 +912,7 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
   const int b0 = blockIdx.x;
   const int r0 = ks * RCP;
-  const bool col = o < H;
+  const bool col = FULL || o < H;
   const float C = k.neuron[o];
   float4 preg[RCP], gacc[RCP];
 #pragma unroll
@@ -950,11 +952,15 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
         al = g * crd;  // saved 1/den
         be = -g * cvk1 * crd;
       }
-      accA += al;
-      accB += be;
-      pC += al * (cvk - cvk1);
-      pGv += al * cvk1;
-      pA += al;
+      // Every wave forms alpha/beta of the whole row (it needs them all), but
+      // only wave 0 keeps the per-step and per-row sums it alone writes out.
+      if (ks == 0) {
+        accA += al;
+        accB += be;
+        pC += al * (cvk - cvk1);
+        pGv += al * cvk1;
+        pA += al;
+      }
       const float gdir = al * C;
       // The RCP gates depend on v^k only: evaluated in phases (arguments,
       // exponentials, reciprocals) ahead of the alpha/beta products.
@@ -2396,7 +2402,10 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
 #define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
   if constexpr (NB == 1) {
     if (row_kernels(p) && p.FUSE && rcp == 8) {
-      hipLaunchKernelGGL((ode_bwd_row_kernel<8>), grid, block, lds, s, a);
+      if (p.H == 64)
+        hipLaunchKernelGGL((ode_bwd_row_kernel<8, true>), grid, block, lds, s, a);
+      else
+        hipLaunchKernelGGL((ode_bwd_row_kernel<8, false>), grid, block, lds, s, a);
       return hipGetLastError();
     }
   }

@@ -199,9 +199,12 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         Hp, NB, KSB = p["Hp"], p["NB"], p["KSB"]
         base = NB * Hp * 8 + KSB * NB * Hp * 4
         assert base <= 65536
-        if NB == 1 and Hp == 64:  # single-row kernels: two partial buffers
-            base = max(base, 2 * KSB * Hp * 4)
-            assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8, 2 * p["KS"] * Hp * 8)
+        if NB == 1 and Hp == 64:
+            # single-row kernels: two partial buffers and every wave's own copy
+            # of the row state (forward) or of alpha/beta (chain)
+            base = max(base, 2 * KSB * Hp * 4 + KSB * Hp * 8)
+            assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8,
+                                       2 * p["KS"] * Hp * 8 + p["KS"] * Hp * 4)
         planes = 4 if (NB == 1 and Hp == 64) else 1
         plane = planes * Hp * (Hp + 1) * 4 if p["fuse"] else 0
         assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
