@@ -835,6 +835,11 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
     d = k.sd[e];
   };
   if (T > 0) load_sens(0, snr, sdr);
+  // Wait for the operands and the first step's sums here, once: otherwise the
+  // unfold loop's first use of sdr carries a vmcnt(0) wait every unfold, and
+  // on gfx9 that also waits for the previous unfold's vsave/densave stores
+  // (C1 forward 27.1 -> 26.8 us).
+  __builtin_amdgcn_s_waitcnt(0);
   int par = 0;
   for (int t = 0; t < T; ++t) {
     if (t + 1 < T) load_sens(t + 1, snn, sdn);
