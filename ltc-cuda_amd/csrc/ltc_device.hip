@@ -899,6 +899,115 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
   }
 }
 
+// Sum of x over the four 16-lane groups of a wave, in every lane. gfx950's
+// v_permlane32_swap / v_permlane16_swap exchange halves and rows of a wave
+// in the VALU: after the two steps every lane holds (x0 + x2) + (x1 + x3)
+// with the same bits.
+__device__ __forceinline__ float group_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Single-row forward at Hp = 64 with wave-owned columns: 4 waves, wave w owns
+// the 16 output columns j = 16w + (lane & 15), and the lane's row group
+// g = lane >> 4 covers presynaptic rows [16g, 16g + 16) of column j, with
+// their operands in registers. A column's sums over its four row groups
+// finish inside the wave (group_sum4), so an unfold has one LDS round trip:
+// the new state goes to a double-buffered LDS row and, after the unfold's one
+// barrier, every lane reads its 16 rows' values back as broadcasts.
+// A buffer is rewritten one unfold after it was read, across that barrier.
+__global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
+  constexpr int HP = 64, RC = 16;
+  extern __shared__ float4 lds4[];
+  float* vsh = reinterpret_cast<float*>(lds4);  // [2][64], the state by unfold parity
+  const int H = k.H, B = k.B, T = k.T, U = k.U;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int g = lane >> 4;
+  const int j = w * 16 + (lane & 15);  // output column of this lane
+  const int r0 = g * RC;               // its first presynaptic row
+  const bool lead = g == 0;            // one lane per column stores
+  const int b0 = blockIdx.x;
+  const bool col = j < H;
+  const float C = k.neuron[j], G = k.neuron[HP + j], L = k.neuron[2 * HP + j];
+  const float GL = G * L, CG = C + G;
+  float4 preg[RC];
+#pragma unroll
+  for (int rr = 0; rr < RC; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * HP + j];
+  float v = (k.state0 != nullptr && col) ? k.state0[(long long)b0 * H + j] : 0.f;
+  if (lead) vsh[j] = v;
+  float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
+  auto load_sens = [&](int t, float& a, float& d) {
+    const long long e = ((long long)b0 * T + t) * HP + j;
+    a = k.sn[e];
+    d = k.sd[e];
+  };
+  if (T > 0) load_sens(0, snr, sdr);
+  // One wait for the operands and the first step's sums, before the loop
+  // (see ode_fwd_row_kernel).
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  int par = 0;
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 < T) load_sens(t + 1, snn, sdn);
+    for (int u = 0; u < U; ++u) {
+      const float* vr = vsh + par * HP + r0;
+      float vi[RC];
+#pragma unroll
+      for (int q = 0; q < RC; q += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(vr + q);
+        vi[q] = w4.x;
+        vi[q + 1] = w4.y;
+        vi[q + 2] = w4.z;
+        vi[q + 3] = w4.w;
+      }
+      // Gates in phases (arguments, exponentials, reciprocals); the sums keep
+      // their order.
+      float z[RC];
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) z[rr] = fmaf(preg[rr].x, vi[rr], preg[rr].y);
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
+      float na = 0.f, qa = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) {
+        na = fmaf(z[rr], preg[rr].z, na);
+        qa = fmaf(z[rr], preg[rr].w, qa);
+      }
+      na = group_sum4(na);
+      qa = group_sum4(qa);
+      const float den = CG + (qa + sdr) + k.eps;
+      const float num = C * v + GL + (na + snr);
+      const float rden = __builtin_amdgcn_rcpf(den);
+      const float vnew = col ? num * rden : 0.f;
+      if (lead) {
+        vsh[(par ^ 1) * HP + j] = vnew;
+        if (k.vsave != nullptr) {
+          const long long e = ((long long)(t * U + u) * B + b0) * HP + j;
+          k.vsave[e] = v;
+          k.densave[e] = rden;
+        }
+        if (u == U - 1 && col) k.out[((long long)b0 * T + t) * H + j] = vnew;
+      }
+      lds_barrier();
+      v = vnew;
+      par ^= 1;
+    }
+    snr = snn;
+    sdr = sdn;
+  }
+  if (lead) {
+    if (col) k.hfin[(long long)b0 * H + j] = v;
+    if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0) * HP + j] = v;
+  }
+}
+
 // Fused chain (FUSE) of one row at Hp = 64: thread (ks, o) holds the RCP
 // synapses (i = o, j = ks*RCP + rr) with their four gradient sums. Launched
 // with RCP = 8 (8 waves): 33.9 us at C1 against 36.5 us at RCP = 4 (rocprofv3
@@ -1049,6 +1158,167 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
     const int e = tid + q * NT;
     const int pl = e >> 12, i = (e >> 6) & 63, j = e & 63;
     vals[q] = tile[pl * PL + i * TLD + j];
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
+}
+
+// Sum of x over the eight 8-lane groups of a wave, in every lane: the two
+// swaps of group_sum4, then DPP row_ror:8, which hands each lane the value
+// of the lane 8 away within its 16-lane row.
+__device__ __forceinline__ float group_sum8(float x) {
+  x = group_sum4(x);
+  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf,
+                                                             0xf, false));
+  return x + y;
+}
+
+// Fused single-row chain at Hp = 64 with wave-owned presynaptic neurons: 8
+// waves, wave w owns i = 8w + (lane & 7), and the lane's group jg = lane >> 3
+// covers postsynaptic j in [8jg, 8jg + 8), with those 8 synapses' operands and
+// four gradient sums in registers. dL/dv_i finishes inside the wave
+// (group_sum8), so an unfold has one LDS round trip: alpha/beta of every
+// column go to a double-buffered LDS row and, after the unfold's one barrier,
+// every lane reads its 8 columns' pairs back as broadcasts.
+template <bool FULL>
+__global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
+  constexpr int HP = 64, RC = 8;
+  extern __shared__ float4 lds4[];
+  float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][64] alpha/beta by unfold parity
+  const int H = k.H, B = k.B, T = k.T, U = k.U;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int jg = lane >> 3;
+  const int i = w * 8 + (lane & 7);  // presynaptic neuron (and the column of its own alpha/beta)
+  const int r0 = jg * RC;            // first postsynaptic column of this lane's synapses
+  const bool lead = jg == 0;         // one lane per neuron keeps the sums and stores
+  const int b0 = blockIdx.x;
+  const bool col = FULL || i < H;
+  const float C = k.neuron[i];
+  float4 preg[RC], gacc[RC];
+#pragma unroll
+  for (int rr = 0; rr < RC; ++rr) {
+    preg[rr] = k.recB[(long long)(r0 + rr) * HP + i];
+    gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + i] : 0.f;
+  float pC = 0.f, pGv = 0.f, pA = 0.f;
+  if (T == 0) return;
+  const long long BHp = (long long)B * HP;
+  // Saved pre-state v^k (also v_i of the synapses), 1/den and v^{k+1} of
+  // column i for unfold n, software-pipelined one unfold ahead.
+  auto load = [&](long long n, float& vk, float& rd, float& vk1) {
+    const long long e = (n * B + b0) * HP + i;
+    vk = k.vsave[e];
+    rd = col ? k.densave[e] : 1.f;
+    vk1 = k.vsave[e + BHp];
+  };
+  auto gout = [&](int t) {
+    return col ? k.gout[(long long)b0 * k.gs.b + (long long)t * k.gs.t + (long long)i * k.gs.c]
+               : 0.f;
+  };
+  float cvk, crd, cvk1, nvk = 0.f, nrd = 1.f, nvk1 = 0.f;
+  load((long long)T * U - 1, cvk, crd, cvk1);
+  float gcur = gout(T - 1), gnext = 0.f;
+  int par = 0;
+  for (int t = T - 1; t >= 0; --t) {
+    if (t > 0) gnext = gout(t - 1);
+    float accA = 0.f, accB = 0.f;
+    g += gcur;
+    for (int u = U - 1; u >= 0; --u) {
+      const long long n = (long long)t * U + u;
+      if (n > 0) load(n - 1, nvk, nrd, nvk1);
+      float al = 0.f, be = 0.f;
+      if (col) {
+        al = g * crd;  // saved 1/den
+        be = -g * cvk1 * crd;
+      }
+      if (lead) {
+        abs_[par * HP + i] = make_float2(al, be);
+        accA += al;
+        accB += be;
+        pC += al * (cvk - cvk1);
+        pGv += al * cvk1;
+        pA += al;
+      }
+      const float gdir = al * C;
+      // The gates depend on v^k only: evaluated in phases ahead of the barrier.
+      float ga[RC];
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
+      lds_barrier();
+      float2 abj[RC];
+      const float2* ar = abs_ + par * HP + r0;
+#pragma unroll
+      for (int q = 0; q < RC; q += 2) {
+        const float4 w4 = *reinterpret_cast<const float4*>(ar + q);
+        abj[q] = make_float2(w4.x, w4.y);
+        abj[q + 1] = make_float2(w4.z, w4.w);
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < RC; ++rr) {
+        const float4 p = preg[rr];
+        const float cx = abj[rr].x, cy = abj[rr].y;
+        const float a = ga[rr];
+        const float a2 = fmaf(-a, a, a);
+        const float dl = fmaf(cx, p.z, cy * p.w) * a2;
+        acc = fmaf(dl, p.x, acc);
+        gacc[rr].x = fmaf(cx, a, gacc[rr].x);
+        gacc[rr].y = fmaf(cy, a, gacc[rr].y);
+        gacc[rr].z += dl;
+        gacc[rr].w = fmaf(dl, cvk, gacc[rr].w);
+      }
+      const float sum = group_sum8(acc);
+      g = col ? fmaf(kNegLn2, sum, gdir) : 0.f;
+      par ^= 1;
+      if (n > 0) {
+        cvk = nvk;
+        crd = nrd;
+        cvk1 = nvk1;
+      }
+    }
+    if (lead) {
+      const long long e = ((long long)b0 * T + t) * HP + i;
+      k.dsn[e] = accA;
+      k.dsd[e] = accB;
+    }
+    gcur = gnext;
+  }
+  if (lead) {
+    if (k.gstate != nullptr && col) k.gstate[(long long)b0 * H + i] = g;
+    float* np = k.npart + (long long)b0 * 3 * HP + i;
+    np[0] = pC;
+    np[HP] = pGv;
+    np[2 * HP] = pA;
+  }
+  // Recurrent-gradient partials through four padded [64][65] LDS planes at
+  // once, whole rows out (layout [workgroup][4][i][j]).
+  constexpr int TLD = HP + 1, PL = HP * TLD;
+  constexpr int NT = 512, PER = 4 * HP * HP / NT;
+  float* tile = reinterpret_cast<float*>(lds4);
+  float* out = k.rpart + (long long)blockIdx.x * 4 * HP * HP;
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < RC; ++rr) {
+    const float4 v4 = gacc[rr];
+    const int e = i * TLD + r0 + rr;
+    tile[e] = v4.x;
+    tile[PL + e] = v4.y;
+    tile[2 * PL + e] = v4.z;
+    tile[3 * PL + e] = v4.w;
+  }
+  __syncthreads();
+  float vals[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = tid + q * NT;
+    const int pl = e >> 12, ii = (e >> 6) & 63, jj = e & 63;
+    vals[q] = tile[pl * PL + ii * TLD + jj];
   }
 #pragma unroll
   for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
@@ -2384,9 +2654,9 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
   if constexpr (NB == 1) {
     if (row_kernels(p) && rcp > 0) {
-      if (rcp == 4) hipLaunchKernelGGL((ode_fwd_row_kernel<4>), grid, block, lds, s, a);
-      else if (rcp == 8) hipLaunchKernelGGL((ode_fwd_row_kernel<8>), grid, block, lds, s, a);
-      else hipLaunchKernelGGL((ode_fwd_row_kernel<16>), grid, block, lds, s, a);
+      if (rcp == 16) hipLaunchKernelGGL(ode_fwd_row_wave_kernel, grid, dim3(256), lds, s, a);
+      else if (rcp == 4) hipLaunchKernelGGL((ode_fwd_row_kernel<4>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((ode_fwd_row_kernel<8>), grid, block, lds, s, a);
       return hipGetLastError();
     }
   }
@@ -2408,9 +2678,9 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   if constexpr (NB == 1) {
     if (row_kernels(p) && p.FUSE && rcp == 8) {
       if (p.H == 64)
-        hipLaunchKernelGGL((ode_bwd_row_kernel<8, true>), grid, block, lds, s, a);
+        hipLaunchKernelGGL((ode_bwd_row_wave_kernel<true>), grid, block, lds, s, a);
       else
-        hipLaunchKernelGGL((ode_bwd_row_kernel<8, false>), grid, block, lds, s, a);
+        hipLaunchKernelGGL((ode_bwd_row_wave_kernel<false>), grid, block, lds, s, a);
       return hipGetLastError();
     }
   }
