@@ -78,20 +78,22 @@ def n_syn(c, B=None):
     return B * c["T"] * (c["D"] * c["H"] + c["U"] * c["H"] ** 2)
 
 
-def kernel_flops(c, fused_chain):
+def kernel_flops(c, fused_chain, counts=None):
     """Algorithmic FLOP per launch of each kernel: per sensory synapse, the
     forward counts 10 (z 2, sigmoid 4, two products 2, two sums 2) and the
     backward 22; per recurrent synapse-unfold, the forward 10 and the chain 14
     (sigmoid recompute 6, sigmoid' 2, delta 4, dv 2), plus the 8 of the four
     parameter-gradient sums, which the fused chain does itself (22) and
-    rec_grad does otherwise. Per-neuron, LayerNorm and finalize work is not
-    counted."""
+    rec_grad does otherwise. Recurrent synapses count as the kernels evaluate
+    them (counts: syn_counts; the compacted kernels skip masked ones).
+    Per-neuron, LayerNorm and finalize work is not counted."""
+    counts = counts or syn_counts(c)
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
-    sens = c["B"] * c["T"] * c["D"] * c["H"]
+    sens = counts["sens"]
     return {
         "ltc_sens_fwd": 10 * sens,
-        "ltc_ode_fwd": 10 * rec,
-        "ltc_ode_bwd": (22 if fused_chain else 14) * rec,
+        "ltc_ode_fwd": 10 * counts["rec_fwd"],
+        "ltc_ode_bwd": (22 if fused_chain else 14) * counts["rec_bwd"],
         "ltc_rec_grad": 8 * rec,
         "ltc_sens_bwd": 22 * sens,
         "ltc_prep": 0,
@@ -185,8 +187,8 @@ def kernel_times(capi, fn, iters):
     return {k: (ms / n, n // iters) for k, (ms, n) in t.items() if n > 0}
 
 
-def roofline(c, ktimes, fused_chain, traffic=None):
-    fl = kernel_flops(c, fused_chain)
+def roofline(c, ktimes, fused_chain, traffic=None, counts=None):
+    fl = kernel_flops(c, fused_chain, counts)
     per_step = {k: avg * per for k, (avg, per) in ktimes.items()}
     dom = max(per_step, key=per_step.get)
     avg_ms = ktimes[dom][0]
@@ -206,14 +208,55 @@ def roofline(c, ktimes, fused_chain, traffic=None):
 MIX = {"fwd": (4, 1, 1), "fwdbwd": (16, 2, 2)}
 
 
-def mix_bound_ms(c, which):
-    """Mix-aware VALU bound: the minimum mix of every synapse, each instruction
-    class at the issue rate the probe measured on this GPU (lane-ops per CU per
-    clock), issued one after another (the probe's synapse kernel confirms the
-    classes do not overlap: its rate equals the sum of the parts)."""
-    f, e, r = MIX[which]
-    per_cu_clk = f / RATES["fma"] + e / RATES["exp"] + r / RATES["rcp"]
-    return n_syn(c) * per_cu_clk / (RATES["cus"] * RATES["clk_hz"]) * 1e3
+def mask_density(m):
+    """Fractions of nonzero entries in the recurrent and sensory masks."""
+    return (float((m.sparsity_mask != 0).float().mean()),
+            float((m.sensory_sparsity_mask != 0).float().mean()))
+
+
+def syn_counts(c, plan=None, density=(1.0, 1.0)):
+    """Synapse evaluations per step: sensory, recurrent forward and recurrent
+    chain as the kernels run them (the compacted Hp = 256 kernels skip the
+    recurrent synapses with a zero mask entry: plan fields cmp_fwd / cmp_bwd),
+    and the layer's active-only count (both masks' densities)."""
+    rho_r, rho_s = density
+    sens = c["B"] * c["T"] * c["D"] * c["H"]
+    rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
+    plan = plan or {}
+    return {"sens": sens,
+            "rec_fwd": rec * (rho_r if plan.get("cmp_fwd") else 1.0),
+            "rec_bwd": rec * (rho_r if plan.get("cmp_bwd") else 1.0),
+            "active": sens * rho_s + rec * rho_r}
+
+
+def mix_bound_ms(c, which, counts=None):
+    """Mix-aware VALU bound: the minimum mix of every synapse evaluation, each
+    instruction class at the issue rate the probe measured on this GPU
+    (lane-ops per CU per clock), issued one after another (the probe's synapse
+    kernel confirms the classes do not overlap). With `counts` (syn_counts) the
+    recurrent synapses are priced as the kernels evaluate them: forward part
+    (4, 1, 1) for each forward evaluation, the backward's (12, 1, 1) for each
+    chain evaluation."""
+    def clk(mix):
+        f, e, r = mix
+        return f / RATES["fma"] + e / RATES["exp"] + r / RATES["rcp"]
+    if counts is None:
+        work = n_syn(c) * clk(MIX[which])
+    elif which == "fwd":
+        work = (counts["sens"] + counts["rec_fwd"]) * clk(MIX["fwd"])
+    else:
+        bwd_part = tuple(a - b for a, b in zip(MIX["fwdbwd"], MIX["fwd"]))
+        work = (counts["sens"] * clk(MIX["fwdbwd"]) + counts["rec_fwd"] * clk(MIX["fwd"]) +
+                counts["rec_bwd"] * clk(bwd_part))
+    return work / (RATES["cus"] * RATES["clk_hz"]) * 1e3
+
+
+def flop_count(c, which, counts):
+    """Algorithmic FLOP per step over the evaluated synapses (10 per forward
+    evaluation; sensory backward 22, chain 22 with its parameter sums)."""
+    if which == "fwd":
+        return 10 * (counts["sens"] + counts["rec_fwd"])
+    return 32 * counts["sens"] + 10 * counts["rec_fwd"] + 22 * counts["rec_bwd"]
 
 
 # --------------------------------------------------------------------------- probe
@@ -363,8 +406,11 @@ def measure_config(name, c, capi, cpu):
     m, x, target = make_inputs(c, "cuda:0")
     train = c["loss"] is not None
     plan = capi.plan(c["B"], c["T"], c["D"], c["H"], c["U"])
+    dens = mask_density(m)
+    counts = syn_counts(c, plan, dens)
     rec = {"shape": {k: c[k] for k in ("B", "T", "D", "H", "U")}, "n_syn": n_syn(c),
            "loss": c["loss"], "x": c["x"]}
+    rec.update(sparsity_record(plan, dens, counts))
 
     if train:
         def fn():
@@ -376,7 +422,13 @@ def measure_config(name, c, capi, cpu):
     for _ in range(2):
         fn()
     torch.cuda.synchronize()
-    iters = 5
+    # about 50 ms of timed steps (5 to 200), so that a short step is not one
+    # host hiccup away from twice its time
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    one_ms = (time.perf_counter() - t0) * 1e3
+    iters = max(5, min(200, int(50.0 / max(one_ms, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(iters):
         fn()
@@ -384,18 +436,19 @@ def measure_config(name, c, capi, cpu):
     ms = (time.perf_counter() - t0) * 1e3 / iters
     rec["ms_per_step"] = round(ms, 4)
     rec["synapse_updates_per_s"] = n_syn(c) / (ms * 1e-3)
+    rec["active_synapse_updates_per_s"] = counts["active"] / (ms * 1e-3)
     rec.update(time_split(m, x, target, 5, train=train))
     kt = kernel_times(capi, fn, 2)
     rec["kernels_ms"] = {k: round(v[0], 5) for k, v in kt.items()}
     rec["launches_per_step_library"] = sum(v[1] for v in kt.values())
-    rec["roofline"] = roofline(c, kt, bool(plan["fuse"]), load_traffic(name))
+    rec["roofline"] = roofline(c, kt, bool(plan["fuse"]), load_traffic(name), counts)
     which = "fwdbwd" if train else "fwd"
     ksum = sum(v[0] * v[1] for v in kt.values())
     rec["kernel_ms_sum"] = round(ksum, 4)
-    rec["valu_mix_bound_ms"] = round(mix_bound_ms(c, which), 4)
-    rec["mix_frac_kernels"] = round(mix_bound_ms(c, which) / ksum, 4)
+    rec["valu_mix_bound_ms"] = round(mix_bound_ms(c, which, counts), 4)
+    rec["mix_frac_kernels"] = round(mix_bound_ms(c, which, counts) / ksum, 4)
     rec["flop_frac_kernels"] = round(
-        n_syn(c) * (10 if which == "fwd" else 32) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
+        flop_count(c, which, counts) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
     rec["memory"] = peak_memory_mb(m, x, target, train)
     del m, x, target
     torch.cuda.empty_cache()
@@ -405,6 +458,15 @@ def measure_config(name, c, capi, cpu):
         rec["gpu_vs_cpu"] = round(rec["cpu_baseline"]["ms_per_step"] / gpu_ms, 1)
     _ = ltc_cuda
     return rec
+
+
+def sparsity_record(plan, dens, counts):
+    """What the kernels skip, and the active-only count beside the dense one."""
+    return {"mask_density": {"recurrent": round(dens[0], 5), "sensory": round(dens[1], 5)},
+            "skips_masked_recurrent": {"forward": bool(plan.get("cmp_fwd")),
+                                       "chain": bool(plan.get("cmp_bwd"))},
+            "n_syn_active": int(round(counts["active"])),
+            "n_syn_evaluated": int(round(counts["sens"] + counts["rec_fwd"]))}
 
 
 def load_traffic(workload):
@@ -509,6 +571,8 @@ def main():
     c = C1
     m, x, target = make_inputs(c, "cuda:0")
     plan = capi.plan(c["B"], c["T"], c["D"], c["H"], c["U"])
+    dens = mask_density(m)
+    counts = syn_counts(c, plan, dens)
 
     for _ in range(args.warmup):
         step(m, x, target)
@@ -550,6 +614,8 @@ def main():
                    "parallelism": "single GPU",
                    "step": "whole step replayed as one HIP graph" if use_graph
                            else "eager module forward + loss.backward()"},
+        "active_synapse_updates_per_s": counts["active"] / (ms * 1e-3),
+        **sparsity_record(plan, dens, counts),
         "eager_ms_per_step": round(eager_ms, 5),
         "eager_synapse_updates_per_s": n_syn(c) / (eager_ms * 1e-3),
         "graphed_ms_per_step": None if graph_ms is None else round(graph_ms, 5),
@@ -562,9 +628,9 @@ def main():
                      "device_kernels_step": launches_step},
         "memory_fwd_bwd_mse": mem,
         "issue_rate": probe,
-        "valu_mix_bound_ms": round(mix_bound_ms(c, "fwdbwd"), 5),
-        "mix_frac_step": round(mix_bound_ms(c, "fwdbwd") / ms, 5),
-        "roofline": roofline(c, kt, bool(plan["fuse"]), load_traffic("C1")),
+        "valu_mix_bound_ms": round(mix_bound_ms(c, "fwdbwd", counts), 5),
+        "mix_frac_step": round(mix_bound_ms(c, "fwdbwd", counts) / ms, 5),
+        "roofline": roofline(c, kt, bool(plan["fuse"]), load_traffic("C1"), counts),
         "vs_reference_gtx1080_published": round(REF_GTX1080_MS / ms, 3),
     }
     del m, x, target

@@ -296,10 +296,13 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * that each own 64 columns of NB rows (threads and LDS fields then describe
  * one cluster member), then the chain kernel's cluster size, rows per
  * cluster and workgroups (its clusters may differ from the forward's when
- * its parameter gradients are fused). Returns the number of values written,
- * or -1 for invalid sizes. The plan depends on the current device's CU count.
+ * its parameter gradients are fused), then 1 when the forward and 1 when the
+ * chain kernel read compacted images (they then skip the recurrent synapses
+ * that cannot contribute: zero weights in the forward, zero mask entries in
+ * the module path's chain). Returns the number of values written, or -1 for
+ * invalid sizes. The plan depends on the current device's CU count.
  */
-#define LTC_PLAN_FIELDS 20
+#define LTC_PLAN_FIELDS 22
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

@@ -92,7 +92,11 @@ void plan_fused_chain(ltc::Plan& p, int ncu) {
   for (int nb : {1, 2, 4, 8}) {
     const int ncl = (p.B + nb - 1) / nb;
     if (ncl > slots) continue;
-    if (ltc::cluster_chain_lds(nb, p.Hp, 16, 32, p.Hp == 256) > chain_lds_limit()) continue;
+    // at Hp = 256 the compacted chain adds its slot table
+    if (ltc::cluster_chain_lds(nb, p.Hp, 16, 32, p.Hp == 256) +
+            (p.Hp == 256 ? ltc::cmp_index_lds(512) : 0) >
+        chain_lds_limit())
+      continue;
     p.CPB = cp;
     p.JWB = 32;
     p.NBB = nb;
@@ -116,6 +120,8 @@ bool plan_cluster(ltc::Plan& p, int ncu) {
       const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
       if (lf > kClusterLds || ltc::cluster_chain_lds(nb, p.Hp, ks, 64, false) > chain_lds_limit())
         continue;
+      // the compacted forward (Hp = 256, 16 rows per thread) adds its slot table
+      if (p.Hp == 256 && ks == 16 && lf + ltc::cmp_index_lds(64 * ks) > chain_lds_limit()) continue;
       p.CP = cp;
       p.NCL = ncl;
       p.NB = nb;
@@ -271,6 +277,21 @@ long long image_rows(const ltc::Plan& p) { return p.Hp + (p.CP > 0 ? ltc::kImage
 // Wait budget of the cluster exchanges (ltc_set_cluster_spin_ticks).
 std::atomic<long long> g_spin{ltc::kDefaultSpinTicks};
 
+// Compacted images of the register-resident cluster kernels (forward / chain).
+void carve_cmp(const ltc::Plan& p, Carver& c, ltc::Prepped& pp, bool fwd, bool bwd) {
+  const long long n = (long long)p.Hp * p.Hp;
+  if (fwd && ltc::cmp_fwd(p)) {
+    pp.cF = c.take<float4>(n);
+    pp.cFi = c.take<int>(n);
+    pp.cFn = c.take<int>(p.Hp);
+  }
+  if (bwd && ltc::cmp_bwd(p)) {
+    pp.cB = c.take<float4>(n);
+    pp.cBi = c.take<int>(n);
+    pp.cBn = c.take<int>(p.Hp);
+  }
+}
+
 ltc::ClusterBuf carve_cluster(const ltc::Plan& p, Carver& c, bool bwd) {
   ltc::ClusterBuf cb{nullptr, nullptr, g_spin.load(std::memory_order_relaxed)};
   if (p.CP > 0) {
@@ -292,6 +313,7 @@ FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
   w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
   w.pp.neuron = c.take<float>(3LL * p.Hp);
+  carve_cmp(p, c, w.pp, true, false);
   w.sn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.sd = c.take<float>((long long)p.B * p.T * p.Hp);
   w.cb = carve_cluster(p, c, false);
@@ -320,6 +342,8 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
     w.pp.recB = c.take<float4>(image_rows(p) * p.Hp);
     w.pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
     w.pp.neuron = c.take<float>(3LL * p.Hp);
+    // the forward's as well: the per-step backward recomputes a forward unfold
+    carve_cmp(p, c, w.pp, true, true);
   }
   w.absave = p.FUSE ? nullptr : c.take<float2>(p.N * p.Hp);
   w.dsn = c.take<float>((long long)p.B * p.T * p.Hp);
@@ -363,6 +387,7 @@ ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
   pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
   pp.sensB = c.take<float4>((long long)p.Dp * p.Hp);
   pp.neuron = c.take<float>(3LL * p.Hp);
+  carve_cmp(p, c, pp, true, true);
   return pp;
 }
 
@@ -1316,12 +1341,12 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const long long nbb = p.CP > 0 ? p.NBB : p.NB;
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
-      p.CP > 0 ? (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * cols * 8 : ltc::fwd_lds(p),
-      p.CP > 0 ? ltc::cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, ltc::chain_prefetches(p))
-               : ltc::chain_lds(p),
+      p.CP > 0 ? ltc::cluster_fwd_lds(p) : ltc::fwd_lds(p),
+      p.CP > 0 ? ltc::cluster_bwd_lds(p) : ltc::chain_lds(p),
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
-      p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB};
+      p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,
+      ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -162,10 +162,88 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_
 }
 
 // ---------------------------------------------------------------------------
+// Compacted image columns (one wave per column). op(r, v, act) gives row r's
+// operand and whether it can contribute; a ballot over each 64 rows gives the
+// active rows their entry numbers in ascending row order. Entry e goes to
+// chunk e % 16, slot e / 16, so a dense column gives every chunk the rows
+// ks, ks + 16, ... and all lanes of a wave the same row per slot. Slots past
+// the column's count get zero operands and row 0.
+// ---------------------------------------------------------------------------
+template <class Op>
+__device__ __forceinline__ void compact_column(int col, int Hp, int lane, float4* cimg, int* cidx,
+                                               int* ccnt, Op op) {
+  const int sc = Hp / kCmpChunks;
+  auto at = [&](int e) {
+    return (long long)((e % kCmpChunks) * sc + e / kCmpChunks) * Hp + col;
+  };
+  int n = 0;
+  for (int r0 = 0; r0 < Hp; r0 += 64) {
+    const int r = r0 + lane;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    bool act = false;
+    op(r, v, act);
+    const unsigned long long m = __ballot(act);
+    if (act) {
+      const long long a = at(n + __popcll(m & ((1ULL << lane) - 1ULL)));
+      cimg[a] = v;
+      cidx[a] = r;
+    }
+    n += __popcll(m);
+  }
+  for (int e = n + lane; e < Hp; e += 64) {
+    const long long a = at(e);
+    cimg[a] = make_float4(0.f, 0.f, 0.f, 0.f);
+    cidx[a] = 0;
+  }
+  if (lane == 0) ccnt[col] = n;
+}
+
+// Compacted columns a prep launch builds: Hp forward columns when cF is set,
+// then Hp chain columns when the chain image is built and cB is set.
+__host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, bool fwd, bool bwd) {
+  return ((fwd && pp.cF != nullptr) ? Hp : 0) + ((bwd && pp.cB != nullptr) ? Hp : 0);
+}
+
+// ---------------------------------------------------------------------------
 // Parameter images (one launch, flat index space over three segments).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int H, int D,
-                                                   int Hp, int Dp, int bwd, int segs) {
+                                                   int Hp, int Dp, int bwd, int segs,
+                                                   int nflat_blocks) {
+  if ((int)blockIdx.x >= nflat_blocks) {
+    // Compacted columns, one per wave (forward, then chain).
+    const int lane = threadIdx.x & 63;
+    int col = ((int)blockIdx.x - nflat_blocks) * 4 + (int)(threadIdx.x >> 6);
+    const bool fwd_c = (segs & kPrepRec) && pp.cF != nullptr;
+    auto operand = [&](int i, int j, float4& v) {
+      const long long e = (long long)i * H + j;
+      const float S = rp.sigma[e], M = rp.mu[e];
+      v = make_float4(-S * kLog2e, S * M * kLog2e, rp.w_erev[e], rp.w_pos[e]);
+    };
+    if (fwd_c) {
+      if (col < Hp) {
+        const int j = col;
+        compact_column(j, Hp, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+          if (i < H && j < H) {
+            operand(i, j, v);
+            act = v.z != 0.f || v.w != 0.f;
+          }
+        });
+        return;
+      }
+      col -= Hp;
+    }
+    if (bwd && (segs & kPrepRec) && pp.cB != nullptr && col < Hp) {
+      const int i = col;
+      compact_column(i, Hp, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+        if (i < H && j < H) {
+          operand(i, j, v);
+          act = true;
+        }
+      });
+    }
+    return;
+  }
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   const long long nrec = (segs & kPrepRec) ? (long long)Hp * Hp : 0;
   const long long nsens = (segs & kPrepSens) ? (long long)Dp * Hp : 0;
@@ -912,6 +990,16 @@ __device__ __forceinline__ float group_sum4(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Sum of x over the eight 8-lane groups of a wave, in every lane: the two
+// swaps of group_sum4, then DPP row_ror:8, which hands each lane the value
+// of the lane 8 away within its 16-lane row.
+__device__ __forceinline__ float group_sum8(float x) {
+  x = group_sum4(x);
+  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf,
+                                                             0xf, false));
+  return x + y;
+}
+
 // Single-row forward at Hp = 64 with wave-owned columns: 4 waves, wave w owns
 // the 16 output columns j = 16w + (lane & 15), and the lane's row group
 // g = lane >> 4 covers presynaptic rows [16g, 16g + 16) of column j, with
@@ -920,6 +1008,8 @@ __device__ __forceinline__ float group_sum4(float x) {
 // the new state goes to a double-buffered LDS row and, after the unfold's one
 // barrier, every lane reads its 16 rows' values back as broadcasts.
 // A buffer is rewritten one unfold after it was read, across that barrier.
+// (8 waves of 8 columns, summed with group_sum8, measured slower at C1:
+// 27.1 against 25.9 us.)
 __global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
   constexpr int HP = 64, RC = 16;
   extern __shared__ float4 lds4[];
@@ -1161,16 +1251,6 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
   }
 #pragma unroll
   for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
-}
-
-// Sum of x over the eight 8-lane groups of a wave, in every lane: the two
-// swaps of group_sum4, then DPP row_ror:8, which hands each lane the value
-// of the lane 8 away within its 16-lane row.
-__device__ __forceinline__ float group_sum8(float x) {
-  x = group_sum4(x);
-  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf,
-                                                             0xf, false));
-  return x + y;
 }
 
 // Fused single-row chain at Hp = 64 with wave-owned presynaptic neurons: 8
@@ -1714,11 +1794,46 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int CPL>
 __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
                                                         int Hp, int Dp, int recb, int sensf,
-                                                        int sensb, int nprep_blocks, LnBuf ln,
-                                                        int T, int BT) {
+                                                        int sensb, int nprep_blocks, int ncmp_blocks,
+                                                        LnBuf ln, int T, int BT) {
+  if ((int)blockIdx.x >= nprep_blocks && (int)blockIdx.x < nprep_blocks + ncmp_blocks) {
+    // Compacted columns, one per wave: forward (synapses whose w_pos or w_erev
+    // is nonzero), then chain (synapses whose mask entry is nonzero).
+    const int lane = threadIdx.x & 63;
+    int col = ((int)blockIdx.x - nprep_blocks) * 4 + (int)(threadIdx.x >> 6);
+    auto operand = [&](int i, int j, float4& v) {
+      const long long e = (long long)i * H + j;
+      const float S = lp.sigma[e], M = lp.mu[e];
+      const float wp = softplus_t(lp.w[e]) * lp.mask[e];
+      v = make_float4(-S * kLog2e, S * M * kLog2e, wp * lp.erev[e], wp);
+    };
+    if (pp.cF != nullptr) {
+      if (col < Hp) {
+        const int j = col;
+        compact_column(j, Hp, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+          if (i < H && j < H) {
+            operand(i, j, v);
+            act = v.z != 0.f || v.w != 0.f;
+          }
+        });
+        return;
+      }
+      col -= Hp;
+    }
+    if (recb && pp.cB != nullptr && col < Hp) {
+      const int i = col;
+      compact_column(i, Hp, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+        if (i < H && j < H && lp.mask[(long long)i * H + j] != 0.f) {
+          operand(i, j, v);
+          act = true;
+        }
+      });
+    }
+    return;
+  }
   if ((int)blockIdx.x >= nprep_blocks) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row = ((int)blockIdx.x - nprep_blocks) * 4 + w;
+    const int row = ((int)blockIdx.x - nprep_blocks - ncmp_blocks) * 4 + w;
     if (row >= BT) return;
     const int b = row / T, t = row - b * T;
     const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
@@ -1923,11 +2038,18 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
   if (tid < nrec) {
     const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
     const long long HH = (long long)Hp * Hp;
+    const float mk = k.lp.mask[tid];
+    if (mk == 0.f) {
+      // A masked synapse's four gradients are zero; the compacted chain
+      // leaves its partials unwritten.
+      k.g.w[tid] = k.g.erev[tid] = k.g.mu[tid] = k.g.sigma[tid] = 0.f;
+      return;
+    }
     const float* src = k.rpart + (long long)i * Hp + j;
     float sp[4];
     sum_partials_planes<4>(src, HH, 4 * HH, k.NCH, sp);
     const float dwe = sp[0], dwp = sp[1], sd = sp[2], sdv = sp[3];
-    const float wv = k.lp.w[tid], mk = k.lp.mask[tid], ev = k.lp.erev[tid];
+    const float wv = k.lp.w[tid], ev = k.lp.erev[tid];
     const float wpos = softplus_t(wv) * mk;
     // w_pos feeds the synapse directly and through w_erev = w_pos * erev.
     k.g.w[tid] = (dwp + dwe * ev) * mk * softplus_grad(wv);
@@ -2098,17 +2220,86 @@ struct FwdCK {
   int B, T, H, Hp, U, KS, RC, CP;
   int xcd_local;   // cluster_coords: all members of a cluster on one XCD
   float eps;
+  // Compacted forward image (RC = 16): operands, row indices, column counts.
+  const float4* cimg;
+  const int* cidx;
+  const int* ccnt;
 };
 
+// The NB state values of LDS row r in the compacted kernels' [Hp][NB] layout.
+template <int NB>
+__device__ __forceinline__ void lds_rows(const float* base, int byte_off, float (&v)[NB]) {
+  const char* at = reinterpret_cast<const char*>(base) + byte_off;
+  if constexpr (NB % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < NB; q += 4) {
+      const float4 w = *reinterpret_cast<const float4*>(at + q * 4);
+      v[q] = w.x;
+      v[q + 1] = w.y;
+      v[q + 2] = w.z;
+      v[q + 3] = w.w;
+    }
+  } else if constexpr (NB == 2) {
+    const float2 w = *reinterpret_cast<const float2*>(at);
+    v[0] = w.x;
+    v[1] = w.y;
+  } else {
+    v[0] = *reinterpret_cast<const float*>(at);
+  }
+}
+
+// Two compacted forward synapses (slots with LDS row offsets o0, o1) for every
+// row of the tile, gates in phases as in fwd_synapses.
+template <int NB>
+__device__ __forceinline__ void fwd_synapses_cmp(const float4* p, const float* vs, int o0, int o1,
+                                                 float* na, float* qa) {
+  float z[2][NB];
+  lds_rows<NB>(vs, o0, z[0]);
+  lds_rows<NB>(vs, o1, z[1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = fmaf(p[i].x, z[i][b], p[i].y);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = 1.0f + __builtin_amdgcn_exp2f(z[i][b]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = __builtin_amdgcn_rcpf(z[i][b]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      na[b] = fmaf(z[i][b], p[i].z, na[b]);
+      qa[b] = fmaf(z[i][b], p[i].w, qa[b]);
+    }
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// RCP = 16 (Hp = 256): the compacted image (CMP). Thread (o, ks) holds the
+// entries ks, ks + 16, ... of column c's active rows, and the wave runs as
+// many slots as its fullest lane; the state sits in LDS as [Hp][NB] so that a
+// slot's NB values are one read at a per-lane row. Slot row offsets live in
+// an LDS table [4][threads] of int4.
 template <int NB, int RCP>
 __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   constexpr int PER = NB * kClW;
+  constexpr bool CMP = RCP == 16;
   extern __shared__ float4 lds4[];
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
   const int RC = RCP > 0 ? RCP : k.RC;
-  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp]
+  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp] ([Hp][NB] with CMP)
   float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][64]
+  int4* slot_tab = reinterpret_cast<int4*>(red + KS * NB * kClW);  // CMP: [4][threads]
+  auto vat = [&](int b, int j) { return CMP ? j * NB + b : b * Hp + j; };
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
   int p, cl;
@@ -2127,15 +2318,30 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   const float GL = G * L, CG = C + G;
 
   float4 preg[RCP > 0 ? RCP : 1];
-  if constexpr (RCP > 0) {
+  int nslot = 0;  // CMP: slots the wave runs
+  if constexpr (CMP) {
+    const int cnt = k.ccnt[c];
+    nslot = wave_max(cnt > ks ? (cnt - 1 - ks) / kCmpChunks + 1 : 0);
+    int ix[RCP];
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(ks * RCP + rr) * Hp + c;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * NB * 4;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
+  } else if constexpr (RCP > 0) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * Hp + c];
   }
   if (tid == 0) gave_up = 0;
   for (int e = tid; e < NB * Hp; e += nthr) {
     const int b = e / Hp, j = e - b * Hp;
-    vs[e] = (k.state0 != nullptr && b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j]
-                                                          : 0.f;
+    vs[vat(b, j)] = (k.state0 != nullptr && b0 + b < B && j < H)
+                        ? k.state0[(long long)(b0 + b) * H + j]
+                        : 0.f;
   }
   lds_barrier();
 
@@ -2155,7 +2361,17 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
       float na[NB], qa[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) na[b] = qa[b] = 0.f;
-      if constexpr (RCP > 0) {
+      if constexpr (CMP) {
+        // Wave-uniform slot count: the skipped pairs branch around.
+#pragma unroll
+        for (int q = 0; q < RCP / 4; ++q) {
+          if (4 * q < nslot) {
+            const int4 of = slot_tab[q * nthr + tid];
+            fwd_synapses_cmp<NB>(preg + 4 * q, vs, of.x, of.y, na, qa);
+            if (4 * q + 2 < nslot) fwd_synapses_cmp<NB>(preg + 4 * q + 2, vs, of.z, of.w, na, qa);
+          }
+        }
+      } else if constexpr (RCP > 0) {
 #pragma unroll
         for (int rr = 0; rr < RCP; rr += kFwdGroup<NB>)
           fwd_synapses<NB, kFwdGroup<NB>>(preg + rr, vs, Hp, r0 + rr, na, qa);
@@ -2176,7 +2392,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
       unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;
       if (owner) {
         const float2 nq = ks_sum_wide(red + bo * kClW + o, NB * kClW, KS);
-        const float vold = vs[bo * Hp + c];
+        const float vold = vs[vat(bo, c)];
         const float den = CG + (nq.y + sdr) + k.eps;
         const float num = C * vold + GL + (nq.x + snr);
         const float rden = __builtin_amdgcn_rcpf(den);
@@ -2188,14 +2404,14 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
           k.vsave[e] = vold;
           k.densave[e] = rden;
         }
-        vs[bo * Hp + c] = vnew;
+        vs[vat(bo, c)] = vnew;
         if (u == U - 1 && live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
       }
       const bool ok = xch_gather<PER>(
           slot, p, nwords, tid, nthr, tag, k.spin, [](int, int) {},
           [&](int, int a, float v) {
             const int q = a / PER, r = a - q * PER;
-            vs[(r >> 6) * Hp + q * kClW + (r & 63)] = v;
+            vs[vat(r >> 6, q * kClW + (r & 63))] = v;
           });
       if (!ok) gave_up = 1;
       lds_barrier();
@@ -2209,7 +2425,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
     sdr = sdn;
   }
   if (live) {
-    const float v = vs[bo * Hp + c];
+    const float v = vs[vat(bo, c)];
     if (c < H) k.hfin[(long long)(b0 + bo) * H + c] = v;
     if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0 + bo) * Hp + c] = v;
   }
@@ -2306,7 +2522,42 @@ struct BwdCK {
   long long spin;  // wait budget of each exchange, wall-clock ticks
   int B, T, H, Hp, U, KS, RC, CP;
   int xcd_local;   // cluster_coords: all members of a cluster on one XCD
+  // Compacted chain image (fused, RC = 16): operands, row indices, column counts.
+  const float4* cimg;
+  const int* cidx;
+  const int* ccnt;
 };
+
+// One compacted chain synapse for every row of the tile: alpha/beta of its
+// row come from the [Hp][NB] float2 layout at byte offset `off` (one 8*NB
+// byte read per lane), the rest as bwd_synapse<NB, true>.
+template <int NB>
+__device__ __forceinline__ void bwd_synapse_cmp(const float4 p, const float2* ab, int off,
+                                                const float* vi, float* acc, float4& gacc) {
+  float2 c[NB];
+  const char* at = reinterpret_cast<const char*>(ab) + off;
+  if constexpr (NB % 2 == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; b += 2) {
+      const float4 w = *reinterpret_cast<const float4*>(at + b * 8);
+      c[b] = make_float2(w.x, w.y);
+      c[b + 1] = make_float2(w.z, w.w);
+    }
+  } else {
+    c[0] = *reinterpret_cast<const float2*>(at);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float a = gate(fmaf(p.x, vi[b], p.y));
+    const float a2 = fmaf(-a, a, a);
+    const float dl = fmaf(c[b].x, p.z, c[b].y * p.w) * a2;
+    acc[b] = fmaf(dl, p.x, acc[b]);
+    gacc.x = fmaf(c[b].x, a, gacc.x);
+    gacc.y = fmaf(c[b].y, a, gacc.y);
+    gacc.z += dl;
+    gacc.w = fmaf(dl, vi[b], gacc.w);
+  }
+}
 
 // Cluster chain: member p forms dL/dv_i for its JW columns i (reduction over
 // every postsynaptic j) and publishes them; alpha_j/beta_j of the other
@@ -2318,6 +2569,13 @@ struct BwdCK {
 // unfolds, and writes one partial per cluster, so the separate
 // parameter-gradient pass and its gate evaluation go away. Its operands are
 // register-resident (RCP rows) or streamed (RCS rows, chain_fused_stream).
+// FUSE with RCP = 16 (Hp = 256) reads the compacted image (CMP): thread
+// (o, ks) holds the entries ks, ks + 16, ... of column c's synapses, the wave
+// runs as many slots as its fullest lane, alpha/beta sit in LDS as [Hp][NB]
+// float2 (a slot's NB pairs at one per-lane row), and the slot row offsets
+// come from an LDS table [4][threads] of int4. Each slot's gradient sums go
+// to its synapse's place in the partial; synapses without an entry are
+// never written.
 template <int NB, int JW, int RCP, bool FUSE, int RCS = 0>
 __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) {
   static_assert(!FUSE || RCP > 0 || RCS > 0, "the fused chain needs a compile-time row count");
@@ -2328,17 +2586,20 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   // issues no loads of its own (register-resident operands), since the load
   // counter is in order and the prefetch would delay the operands' waits.
   constexpr bool PF = FUSE && RCP > 0;
+  constexpr bool CMP = FUSE && RCP == 16;
   constexpr int HPC = 16 * NACC;  // Hp of the fused forms (512 threads, 16 chunks)
   extern __shared__ float4 lds4[];
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
   const int RC = RCP > 0 ? RCP : (RCS > 0 ? RCS : k.RC);
-  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
+  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp] ([Hp][NB] with CMP)
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
   // PF: saved forward values of the cluster's rows, fetched one synapse
   // phase ahead of use: 1/den of unfold n-1, and v of slots n and n-1.
   float* pden = red + KS * NB * JW;                     // [NB][Hp]
   float* pv = pden + NB * Hp;                           // [2][NB][Hp]
+  int4* slot_tab = reinterpret_cast<int4*>(pv + 2 * NB * Hp);  // CMP: [4][threads]
+  auto abat = [&](int b, int col) { return CMP ? col * NB + b : b * Hp + col; };
   const int tid = threadIdx.x, nthr = blockDim.x;
   // With JW = 64 ks is uniform across each wave; with JW = 32 a wave holds two.
   const int ks = JW == 64 ? __builtin_amdgcn_readfirstlane(tid / JW) : tid / JW;
@@ -2358,7 +2619,22 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   if (T == 0) return;
 
   float4 preg[RCP > 0 ? RCP : 1];
-  if constexpr (RCP > 0) {
+  int nmine = 0, nslot = 0;  // CMP: this lane's entries, slots the wave runs
+  if constexpr (CMP) {
+    const int cnt = k.ccnt[c];
+    nmine = cnt > ks ? (cnt - 1 - ks) / kCmpChunks + 1 : 0;
+    nslot = wave_max(nmine);
+    int ix[RCP];
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(ks * RCP + rr) * Hp + c;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * NB * 8;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
+  } else if constexpr (RCP > 0) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + c];
   }
@@ -2387,7 +2663,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       pA += al;
       gdir = al * C;
     }
-    ab[bo * Hp + c] = make_float2(al, be);
+    ab[abat(bo, c)] = make_float2(al, be);
     if (!FUSE && live) k.absave[(n * B + b0 + bo) * Hp + c] = make_float2(al, be);
   };
   auto gout_at = [&](int b, int t, int col) {
@@ -2429,7 +2705,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       al = gg * rden;
       be = -gg * k.vsave[ee + BHp] * rden;
     }
-    ab[b * Hp + col] = make_float2(al, be);
+    ab[abat(b, col)] = make_float2(al, be);
   }
   // v of slot n_last, the post-unfold state of unfold n_last - 1.
   if constexpr (PF)
@@ -2465,6 +2741,27 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       const int lane_bytes = c * 16 + ((tid >> 5) & 1) * RCS * Hp * 16;
       const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
       chain_fused_stream<NB, RCS>(rsB, lane_bytes, srow0, r0, Hp, ab, cvi, acc, gacc);
+    } else if constexpr (CMP) {
+      // Wave-uniform slot count: the skipped pairs branch around.
+#pragma unroll
+      for (int q = 0; q < RCP / 4; ++q) {
+        if (4 * q < nslot) {
+          const int4 of = slot_tab[q * nthr + tid];
+          const int off[4] = {of.x, of.y, of.z, of.w};
+#pragma unroll
+          for (int h = 0; h < 4; h += 2) {
+            if (4 * q + h < nslot) {
+#pragma unroll
+              for (int i = 0; i < 2; ++i) {
+                const int rr = 4 * q + h + i;
+                bwd_synapse_cmp<NB>(preg[rr], ab, off[h + i], cvi, acc, gacc[rr]);
+                asm volatile("" : "+v"(gacc[rr].x), "+v"(gacc[rr].y), "+v"(gacc[rr].z),
+                             "+v"(gacc[rr].w));
+              }
+            }
+          }
+        }
+      }
     } else if constexpr (FUSE) {
 #pragma unroll
       for (int rr = 0; rr < RCP; ++rr) {
@@ -2536,7 +2833,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
               al = gg * rden;
               be = -gg * vn[b * Hp + col] * rden;
             }
-            ab[b * Hp + col] = make_float2(al, be);
+            ab[abat(b, col)] = make_float2(al, be);
           });
       if (!ok) gave_up = 1;
       if (owner) own_ab(n - 1, pden[bo * Hp + c], vm[bo * Hp + c], vn[bo * Hp + c]);
@@ -2569,7 +2866,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
               al = gg * rden;
               be = -gg * pvk1[x] * rden;
             }
-            ab[b * Hp + col] = make_float2(al, be);
+            ab[abat(b, col)] = make_float2(al, be);
           });
       if (!ok) gave_up = 1;
       if (owner) own_ab(n - 1, nden, nvk, nvk1);
@@ -2595,13 +2892,27 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     // This cluster's share of the recurrent parameter gradients for synapses
     // (i = c, j = r0 + rr), layout [cluster][4][i][j] as rec_grad_kernel's.
     const long long HH = (long long)Hp * Hp;
-    float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp + r0;
+    if constexpr (CMP) {
+      float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp;
 #pragma unroll
-    for (int rr = 0; rr < NACC; ++rr) {
-      out[rr] = gacc[rr].x;
-      out[HH + rr] = gacc[rr].y;
-      out[2 * HH + rr] = gacc[rr].z;
-      out[3 * HH + rr] = gacc[rr].w;
+      for (int rr = 0; rr < NACC; ++rr) {
+        if (rr < nmine) {
+          const int j = k.cidx[(long long)(ks * RCP + rr) * Hp + c];
+          out[j] = gacc[rr].x;
+          out[HH + j] = gacc[rr].y;
+          out[2 * HH + j] = gacc[rr].z;
+          out[3 * HH + j] = gacc[rr].w;
+        }
+      }
+    } else {
+      float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp + r0;
+#pragma unroll
+      for (int rr = 0; rr < NACC; ++rr) {
+        out[rr] = gacc[rr].x;
+        out[HH + rr] = gacc[rr].y;
+        out[2 * HH + rr] = gacc[rr].z;
+        out[3 * HH + rr] = gacc[rr].w;
+      }
     }
   }
 }
@@ -2706,12 +3017,8 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
 
 // Cluster path: grid NCL * CP, 64 * KS threads. The forward keeps its operands
 // in registers when RC = 16, otherwise they stream (RC is a multiple of 8).
-size_t fwd_cl_lds_bytes(const Plan& p) {
-  return (size_t)p.NB * p.Hp * 4 + (size_t)p.KS * p.NB * 64 * 8;
-}
-size_t bwd_cl_lds_bytes(const Plan& p) {
-  return (size_t)cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, chain_prefetches(p));
-}
+size_t fwd_cl_lds_bytes(const Plan& p) { return (size_t)cluster_fwd_lds(p); }
+size_t bwd_cl_lds_bytes(const Plan& p) { return (size_t)cluster_bwd_lds(p); }
 
 hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s) {
   const long long n = bwd ? cluster_words_bwd(p) : cluster_words(p);
@@ -2761,9 +3068,11 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
                           ((segs & kPrepSens) ? (long long)p.Dp * p.Hp : 0) +
                           ((segs & kPrepNeuron) ? 3LL * p.Hp : 0);
   if (total == 0) return hipSuccess;
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  hipLaunchKernelGGL(prep_kernel, dim3(blocks), dim3(256), 0, s, rp, pp, p.H, p.D, p.Hp, p.Dp,
-                     bwd ? (p.FUSE ? 1 : 2) : 0, segs);
+  const int nflat = (int)((total + 255) / 256);
+  const bool rec = (segs & kPrepRec) != 0;
+  const int ncmp = (cmp_columns(pp, p.Hp, rec, rec && bwd) + 3) / 4;
+  hipLaunchKernelGGL(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
+                     p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat);
   return hipGetLastError();
 }
 
@@ -2846,7 +3155,10 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
     // Register-resident operands (RC = 16) read no image from L2 in the loop.
     const int xl = (p.RC == 16 && p.NCL % 8 == 0) ? 1 : 0;
     FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
-            cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, xl, eps};
+            cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, xl, eps,
+            pp.cF, pp.cFi, pp.cFn};
+    if (cmp_fwd(p) && (pp.cF == nullptr || pp.cFi == nullptr || pp.cFn == nullptr))
+      return hipErrorInvalidValue;
     switch (p.NB) {
       case 8: return fwd_cl_by_rcp<8>(p, a, s);
       case 4: return fwd_cl_by_rcp<4>(p, a, s);
@@ -2878,7 +3190,9 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
     const int xl = (chain_prefetches(p) && p.NCLB % 8 == 0) ? 1 : 0;
     BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
             gstate, rpart, cb.xch, cb.status, cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB,
-            p.CPB, xl};
+            p.CPB, xl, pp.cB, pp.cBi, pp.cBn};
+    if (cmp_bwd(p) && (pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr))
+      return hipErrorInvalidValue;
     switch (p.NBB) {
       case 8: return bwd_cl_by_rcp<8>(p, a, s);
       case 4: return bwd_cl_by_rcp<4>(p, a, s);
@@ -2974,10 +3288,11 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   const int nln = ln ? (BT + 3) / 4 : 0;
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   const bool bwd = (images & kLeafBwdImages) != 0;
-#define LTC_PREPL(C)                                                                      \
-  hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + nln), dim3(256), 0, s, lp, pp, p.H, \
-                     p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                           \
-                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, lb, p.T, BT)
+  const int ncmp = (cmp_columns(pp, p.Hp, true, bwd) + 3) / 4;
+#define LTC_PREPL(C)                                                                           \
+  hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + ncmp + nln), dim3(256), 0, s, lp, pp, \
+                     p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                          \
+                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, ncmp, lb, p.T, BT)
   if (nln == 0 || p.D <= 64) LTC_PREPL(1);
   else if (p.D <= 128) LTC_PREPL(2);
   else if (p.D <= 256) LTC_PREPL(4);

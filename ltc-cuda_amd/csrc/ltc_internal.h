@@ -68,13 +68,37 @@ struct Plan {
 //   sensF[d][h] = {-Ss*log2e, Ss*Ms*log2e, Ws*Es, Ws}, [Dp][Hp]
 //   sensB[h][d] = {-Ss*log2e, Ss*Ms*log2e, Es, Ws*Ss}, [Hp][Dp]
 //   neuron = C[Hp], G[Hp], L[Hp]
+//
+// Compacted recurrent images (the register-resident cluster kernels, Hp = 256):
+// per column, the synapses that can contribute, in ascending row order; entry
+// e of column c sits in chunk e % 16, slot e / 16:
+//   cF[(ks*16 + s)*Hp + j]  forward operand of column j (postsynaptic), rows i
+//                           with WE or WP nonzero (a synapse with both zero adds
+//                           exact zeros to the forward sums);
+//   cB[(ks*16 + s)*Hp + i]  chain operand of column i (presynaptic), rows j: every
+//                           real synapse, or on the module path only those whose
+//                           mask entry is nonzero (the others have zero gradients);
+//   cFi / cBi               the row index of each slot (0 in padding slots);
+//   cFn / cBn               the entry count of each column.
+// Padding slots hold zero operands, which add exact zeros. Null when the plan
+// does not use the compacted kernels.
 struct Prepped {
   float4* recF;
   float4* recB;
   float4* sensF;
   float4* sensB;
   float* neuron;
+  float4* cF;
+  int* cFi;
+  int* cFn;
+  float4* cB;
+  int* cBi;
+  int* cBn;
 };
+// Chunks (and slots per chunk) of a compacted image column.
+constexpr int kCmpChunks = 16;
+// LDS of the compacted kernels' slot table: one int per slot per thread.
+inline long long cmp_index_lds(int threads) { return (long long)threads * kCmpChunks * 4; }
 
 struct RawParams {
   const float* w_pos;
@@ -209,6 +233,25 @@ inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.
 inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
+// The cluster forward with register-resident operands (16 rows per thread,
+// Hp = 256) and the fused cluster chain with register-resident operands read
+// compacted images.
+inline bool cmp_fwd(const Plan& p) { return p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16; }
+inline bool cmp_bwd(const Plan& p) {
+  return p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16;
+}
+// Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
+// compacted image, its slot table.
+inline long long cluster_bwd_lds(const Plan& p) {
+  return cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, chain_prefetches(p)) +
+         (cmp_bwd(p) ? cmp_index_lds(p.JWB * p.KSB) : 0);
+}
+// Dynamic LDS of a cluster forward member: state rows [NB][Hp], the KS
+// partials [KS][NB][64] float2, and with the compacted image the slot table.
+inline long long cluster_fwd_lds(const Plan& p) {
+  return (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * 64 * 8 +
+         (cmp_fwd(p) ? cmp_index_lds(64 * p.KS) : 0);
+}
 // One row per workgroup at Hp = 64: the single-row kernels (every wave keeps
 // the row's state, one barrier per unfold, partials double-buffered).
 inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp == 64; }
