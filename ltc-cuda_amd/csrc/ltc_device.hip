@@ -26,6 +26,8 @@
 //    (t,k,b) by separate kernels into partial buffers that a finalize kernel
 //    sums in a fixed order. No atomics anywhere, so every result is bitwise
 //    reproducible run to run.
+#include <type_traits>
+
 #include "ltc_internal.h"
 
 namespace ltc {
@@ -48,6 +50,13 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Largest value of v over the wave, as a wave-uniform value.
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+  return __builtin_amdgcn_readfirstlane(v);
 }
 
 // Sum of the K partials base[0], base[stride], ..., base[(K-1)*stride]: all K
@@ -164,18 +173,16 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_
 // ---------------------------------------------------------------------------
 // Compacted image columns (one wave per column). op(r, v, act) gives row r's
 // operand and whether it can contribute; a ballot over each 64 rows gives the
-// active rows their entry numbers in ascending row order. Entry e goes to
-// chunk e % 16, slot e / 16, so a dense column gives every chunk the rows
-// ks, ks + 16, ... and all lanes of a wave the same row per slot. Slots past
-// the column's count get zero operands and row 0.
+// active rows their entry numbers in ascending row order. With nch chunks,
+// entry e goes to chunk e % nch, slot e / nch, so a dense column gives every
+// chunk the rows ks, ks + nch, ... and all lanes of a chunk the same row per
+// slot. Slots past the column's count get zero operands and row 0.
 // ---------------------------------------------------------------------------
 template <class Op>
-__device__ __forceinline__ void compact_column(int col, int Hp, int lane, float4* cimg, int* cidx,
-                                               int* ccnt, Op op) {
-  const int sc = Hp / kCmpChunks;
-  auto at = [&](int e) {
-    return (long long)((e % kCmpChunks) * sc + e / kCmpChunks) * Hp + col;
-  };
+__device__ __forceinline__ void compact_column(int col, int Hp, int nch, int lane, float4* cimg,
+                                               int* cidx, int* ccnt, Op op) {
+  const int sc = Hp / nch;
+  auto at = [&](int e) { return (long long)((e % nch) * sc + e / nch) * Hp + col; };
   int n = 0;
   for (int r0 = 0; r0 < Hp; r0 += 64) {
     const int r = r0 + lane;
@@ -209,7 +216,7 @@ __host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, bool fwd, 
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int H, int D,
                                                    int Hp, int Dp, int bwd, int segs,
-                                                   int nflat_blocks) {
+                                                   int nflat_blocks, int nchf, int nchb) {
   if ((int)blockIdx.x >= nflat_blocks) {
     // Compacted columns, one per wave (forward, then chain).
     const int lane = threadIdx.x & 63;
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
     if (fwd_c) {
       if (col < Hp) {
         const int j = col;
-        compact_column(j, Hp, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+        compact_column(j, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
           if (i < H && j < H) {
             operand(i, j, v);
             act = v.z != 0.f || v.w != 0.f;
@@ -235,7 +242,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
     }
     if (bwd && (segs & kPrepRec) && pp.cB != nullptr && col < Hp) {
       const int i = col;
-      compact_column(i, Hp, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+      compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
         if (i < H && j < H) {
           operand(i, j, v);
           act = true;
@@ -443,6 +450,11 @@ struct FwdK {
   float* densave;
   int B, T, H, Hp, U, KS, RC;
   float eps;
+  // Compacted forward image (the single-row forward): operands, row indices,
+  // column counts.
+  const float4* cimg;
+  const int* cidx;
+  const int* ccnt;
 };
 
 template <int NB>
@@ -628,6 +640,11 @@ struct BwdK {
   float* gstate;
   float* rpart;     // per-workgroup recurrent partials [grid][4][Hp][Hp] (fused only)
   int B, T, H, Hp, U, KS, RC;
+  // Compacted chain image (the single-row fused chain): operands, row
+  // indices, column counts.
+  const float4* cimg;
+  const int* cidx;
+  const int* ccnt;
 };
 
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
@@ -1002,34 +1019,25 @@ __device__ __forceinline__ float group_sum8(float x) {
 
 // Single-row forward at Hp = 64 with wave-owned columns: 4 waves, wave w owns
 // the 16 output columns j = 16w + (lane & 15), and the lane's row group
-// g = lane >> 4 covers presynaptic rows [16g, 16g + 16) of column j, with
-// their operands in registers. A column's sums over its four row groups
-// finish inside the wave (group_sum4), so an unfold has one LDS round trip:
-// the new state goes to a double-buffered LDS row and, after the unfold's one
-// barrier, every lane reads its 16 rows' values back as broadcasts.
-// A buffer is rewritten one unfold after it was read, across that barrier.
-// (8 waves of 8 columns, summed with group_sum8, measured slower at C1:
-// 27.1 against 25.9 us.)
-__global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
-  constexpr int HP = 64, RC = 16;
-  extern __shared__ float4 lds4[];
-  float* vsh = reinterpret_cast<float*>(lds4);  // [2][64], the state by unfold parity
+// g = lane >> 4 holds the compacted entries g, g + 4, ... of column j (the
+// rows i whose synapse (i -> j) has a nonzero weight, ascending), with their
+// operands and LDS row offsets in registers. The wave runs NS slots, its
+// fullest lane's count rounded up to even, in a loop unrolled for that NS.
+// A column's sums over its four row groups finish inside the wave
+// (group_sum4), so an unfold has one LDS round trip: the new state goes to a
+// double-buffered LDS row and, after the unfold's one barrier, every lane
+// reads its slots' rows back. A buffer is rewritten one unfold after it was
+// read, across that barrier. (8 waves of 8 columns, summed with group_sum8,
+// measured slower at C1: 27.1 against 25.9 us.)
+template <int NS>
+__device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&preg)[16],
+                                                  const int (&ix)[16], float* vsh, int j, bool lead,
+                                                  bool col, float v) {
+  constexpr int HP = 64;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int g = lane >> 4;
-  const int j = w * 16 + (lane & 15);  // output column of this lane
-  const int r0 = g * RC;               // its first presynaptic row
-  const bool lead = g == 0;            // one lane per column stores
   const int b0 = blockIdx.x;
-  const bool col = j < H;
   const float C = k.neuron[j], G = k.neuron[HP + j], L = k.neuron[2 * HP + j];
   const float GL = G * L, CG = C + G;
-  float4 preg[RC];
-#pragma unroll
-  for (int rr = 0; rr < RC; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * HP + j];
-  float v = (k.state0 != nullptr && col) ? k.state0[(long long)b0 * H + j] : 0.f;
-  if (lead) vsh[j] = v;
   float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
   auto load_sens = [&](int t, float& a, float& d) {
     const long long e = ((long long)b0 * T + t) * HP + j;
@@ -1041,60 +1049,100 @@ __global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
   // (see ode_fwd_row_kernel).
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();
-  int par = 0;
-  for (int t = 0; t < T; ++t) {
-    if (t + 1 < T) load_sens(t + 1, snn, sdn);
-    for (int u = 0; u < U; ++u) {
-      const float* vr = vsh + par * HP + r0;
-      float vi[RC];
+  int t = 0, u = 0;
+  // One unfold reading state buffer P (compile-time, so the per-lane row
+  // offsets are the whole LDS address) and writing buffer P ^ 1.
+  auto unfold = [&](auto pc) {
+    constexpr int P = decltype(pc)::value;
+    if (u == 0 && t + 1 < T) load_sens(t + 1, snn, sdn);
+    const char* vr = reinterpret_cast<const char*>(vsh + P * HP);
+    // Gates in phases (states, arguments, exponentials, reciprocals); the
+    // sums keep their order.
+    float z[NS];
 #pragma unroll
-      for (int q = 0; q < RC; q += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(vr + q);
-        vi[q] = w4.x;
-        vi[q + 1] = w4.y;
-        vi[q + 2] = w4.z;
-        vi[q + 3] = w4.w;
-      }
-      // Gates in phases (arguments, exponentials, reciprocals); the sums keep
-      // their order.
-      float z[RC];
+    for (int rr = 0; rr < NS; ++rr) z[rr] = *reinterpret_cast<const float*>(vr + ix[rr]);
 #pragma unroll
-      for (int rr = 0; rr < RC; ++rr) z[rr] = fmaf(preg[rr].x, vi[rr], preg[rr].y);
+    for (int rr = 0; rr < NS; ++rr) z[rr] = fmaf(preg[rr].x, z[rr], preg[rr].y);
 #pragma unroll
-      for (int rr = 0; rr < RC; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
+    for (int rr = 0; rr < NS; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
 #pragma unroll
-      for (int rr = 0; rr < RC; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
-      float na = 0.f, qa = 0.f;
+    for (int rr = 0; rr < NS; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
+    float na = 0.f, qa = 0.f;
 #pragma unroll
-      for (int rr = 0; rr < RC; ++rr) {
-        na = fmaf(z[rr], preg[rr].z, na);
-        qa = fmaf(z[rr], preg[rr].w, qa);
-      }
-      na = group_sum4(na);
-      qa = group_sum4(qa);
-      const float den = CG + (qa + sdr) + k.eps;
-      const float num = C * v + GL + (na + snr);
-      const float rden = __builtin_amdgcn_rcpf(den);
-      const float vnew = col ? num * rden : 0.f;
-      if (lead) {
-        vsh[(par ^ 1) * HP + j] = vnew;
-        if (k.vsave != nullptr) {
-          const long long e = ((long long)(t * U + u) * B + b0) * HP + j;
-          k.vsave[e] = v;
-          k.densave[e] = rden;
-        }
-        if (u == U - 1 && col) k.out[((long long)b0 * T + t) * H + j] = vnew;
-      }
-      lds_barrier();
-      v = vnew;
-      par ^= 1;
+    for (int rr = 0; rr < NS; ++rr) {
+      na = fmaf(z[rr], preg[rr].z, na);
+      qa = fmaf(z[rr], preg[rr].w, qa);
     }
-    snr = snn;
-    sdr = sdn;
+    na = group_sum4(na);
+    qa = group_sum4(qa);
+    const float den = CG + (qa + sdr) + k.eps;
+    const float num = C * v + GL + (na + snr);
+    const float rden = __builtin_amdgcn_rcpf(den);
+    const float vnew = col ? num * rden : 0.f;
+    if (lead) {
+      vsh[(P ^ 1) * HP + j] = vnew;
+      if (k.vsave != nullptr) {
+        const long long e = ((long long)(t * U + u) * B + b0) * HP + j;
+        k.vsave[e] = v;
+        k.densave[e] = rden;
+      }
+      if (u == U - 1 && col) k.out[((long long)b0 * T + t) * H + j] = vnew;
+    }
+    lds_barrier();
+    v = vnew;
+    if (++u == U) {
+      u = 0;
+      ++t;
+      snr = snn;
+      sdr = sdn;
+    }
+  };
+  const long long N = (long long)T * U;
+  long long n = 0;
+  for (; n + 1 < N; n += 2) {
+    unfold(std::integral_constant<int, 0>{});
+    unfold(std::integral_constant<int, 1>{});
   }
+  if (n < N) unfold(std::integral_constant<int, 0>{});
   if (lead) {
     if (col) k.hfin[(long long)b0 * H + j] = v;
     if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0) * HP + j] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
+  constexpr int HP = 64, RC = 16;
+  extern __shared__ float4 lds4[];
+  float* vsh = reinterpret_cast<float*>(lds4);  // [2][64], the state by unfold parity
+  const int H = k.H;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int g = lane >> 4;
+  const int j = (tid >> 6) * 16 + (lane & 15);  // output column of this lane
+  const bool lead = g == 0;                     // one lane per column stores
+  const bool col = j < H;
+  const int cnt = k.ccnt[j];
+  const int nslot = wave_max(cnt > g ? (cnt - 1 - g) / 4 + 1 : 0);
+  float4 preg[RC];
+  int ix[RC];
+#pragma unroll
+  for (int rr = 0; rr < RC; ++rr) {
+    const long long a = (long long)(g * RC + rr) * HP + j;
+    preg[rr] = k.cimg[a];
+    ix[rr] = k.cidx[a] * 4;
+  }
+  const float v = (k.state0 != nullptr && col) ? k.state0[(long long)blockIdx.x * H + j] : 0.f;
+  if (lead) vsh[j] = v;
+  switch ((nslot + 1) >> 1) {
+    case 0:
+    case 1: fwd_row_wave_loop<2>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 2: fwd_row_wave_loop<4>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 3: fwd_row_wave_loop<6>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 4: fwd_row_wave_loop<8>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 5: fwd_row_wave_loop<10>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 6: fwd_row_wave_loop<12>(k, preg, ix, vsh, j, lead, col, v); break;
+    case 7: fwd_row_wave_loop<14>(k, preg, ix, vsh, j, lead, col, v); break;
+    default: fwd_row_wave_loop<16>(k, preg, ix, vsh, j, lead, col, v); break;
   }
 }
 
@@ -1255,35 +1303,26 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
 
 // Fused single-row chain at Hp = 64 with wave-owned presynaptic neurons: 8
 // waves, wave w owns i = 8w + (lane & 7), and the lane's group jg = lane >> 3
-// covers postsynaptic j in [8jg, 8jg + 8), with those 8 synapses' operands and
-// four gradient sums in registers. dL/dv_i finishes inside the wave
+// holds the compacted entries jg, jg + 8, ... of column i (its postsynaptic
+// j: every real synapse on the boundary, those with a nonzero mask entry on
+// the module path), with their operands, four gradient sums and LDS offsets
+// in registers. The wave runs NS slots, its fullest lane's count rounded up
+// to even, in a loop unrolled for that NS. dL/dv_i finishes inside the wave
 // (group_sum8), so an unfold has one LDS round trip: alpha/beta of every
 // column go to a double-buffered LDS row and, after the unfold's one barrier,
-// every lane reads its 8 columns' pairs back as broadcasts.
-template <bool FULL>
-__global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
-  constexpr int HP = 64, RC = 8;
-  extern __shared__ float4 lds4[];
-  float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][64] alpha/beta by unfold parity
+// every lane reads its slots' pairs back. The unfold loop runs in pairs so
+// that the buffer of each unfold is known at compile time.
+template <int NS, bool FULL>
+__device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&preg)[8],
+                                                  const int (&jx)[8], float4 (&gacc)[8],
+                                                  float2* abs_, int i, bool lead) {
+  constexpr int HP = 64;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int jg = lane >> 3;
-  const int i = w * 8 + (lane & 7);  // presynaptic neuron (and the column of its own alpha/beta)
-  const int r0 = jg * RC;            // first postsynaptic column of this lane's synapses
-  const bool lead = jg == 0;         // one lane per neuron keeps the sums and stores
   const int b0 = blockIdx.x;
   const bool col = FULL || i < H;
   const float C = k.neuron[i];
-  float4 preg[RC], gacc[RC];
-#pragma unroll
-  for (int rr = 0; rr < RC; ++rr) {
-    preg[rr] = k.recB[(long long)(r0 + rr) * HP + i];
-    gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
   float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + i] : 0.f;
   float pC = 0.f, pGv = 0.f, pA = 0.f;
-  if (T == 0) return;
   const long long BHp = (long long)B * HP;
   // Saved pre-state v^k (also v_i of the synapses), 1/den and v^{k+1} of
   // column i for unfold n, software-pipelined one unfold ahead.
@@ -1299,76 +1338,85 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
   };
   float cvk, crd, cvk1, nvk = 0.f, nrd = 1.f, nvk1 = 0.f;
   load((long long)T * U - 1, cvk, crd, cvk1);
-  float gcur = gout(T - 1), gnext = 0.f;
-  int par = 0;
-  for (int t = T - 1; t >= 0; --t) {
-    if (t > 0) gnext = gout(t - 1);
-    float accA = 0.f, accB = 0.f;
-    g += gcur;
-    for (int u = U - 1; u >= 0; --u) {
-      const long long n = (long long)t * U + u;
-      if (n > 0) load(n - 1, nvk, nrd, nvk1);
-      float al = 0.f, be = 0.f;
-      if (col) {
-        al = g * crd;  // saved 1/den
-        be = -g * cvk1 * crd;
-      }
-      if (lead) {
-        abs_[par * HP + i] = make_float2(al, be);
-        accA += al;
-        accB += be;
-        pC += al * (cvk - cvk1);
-        pGv += al * cvk1;
-        pA += al;
-      }
-      const float gdir = al * C;
-      // The gates depend on v^k only: evaluated in phases ahead of the barrier.
-      float ga[RC];
-#pragma unroll
-      for (int rr = 0; rr < RC; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
-#pragma unroll
-      for (int rr = 0; rr < RC; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
-#pragma unroll
-      for (int rr = 0; rr < RC; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
-      lds_barrier();
-      float2 abj[RC];
-      const float2* ar = abs_ + par * HP + r0;
-#pragma unroll
-      for (int q = 0; q < RC; q += 2) {
-        const float4 w4 = *reinterpret_cast<const float4*>(ar + q);
-        abj[q] = make_float2(w4.x, w4.y);
-        abj[q + 1] = make_float2(w4.z, w4.w);
-      }
-      float acc = 0.f;
-#pragma unroll
-      for (int rr = 0; rr < RC; ++rr) {
-        const float4 p = preg[rr];
-        const float cx = abj[rr].x, cy = abj[rr].y;
-        const float a = ga[rr];
-        const float a2 = fmaf(-a, a, a);
-        const float dl = fmaf(cx, p.z, cy * p.w) * a2;
-        acc = fmaf(dl, p.x, acc);
-        gacc[rr].x = fmaf(cx, a, gacc[rr].x);
-        gacc[rr].y = fmaf(cy, a, gacc[rr].y);
-        gacc[rr].z += dl;
-        gacc[rr].w = fmaf(dl, cvk, gacc[rr].w);
-      }
-      const float sum = group_sum8(acc);
-      g = col ? fmaf(kNegLn2, sum, gdir) : 0.f;
-      par ^= 1;
-      if (n > 0) {
-        cvk = nvk;
-        crd = nrd;
-        cvk1 = nvk1;
-      }
+  float gcur = gout(T - 1), gnext = 0.f, accA = 0.f, accB = 0.f;
+  int t = T - 1, u = U - 1;
+  auto unfold = [&](auto pc) {
+    constexpr int P = decltype(pc)::value;
+    const long long n = (long long)t * U + u;
+    if (u == U - 1) {
+      if (t > 0) gnext = gout(t - 1);
+      accA = accB = 0.f;
+      g += gcur;
+    }
+    if (n > 0) load(n - 1, nvk, nrd, nvk1);
+    float al = 0.f, be = 0.f;
+    if (col) {
+      al = g * crd;  // saved 1/den
+      be = -g * cvk1 * crd;
     }
     if (lead) {
-      const long long e = ((long long)b0 * T + t) * HP + i;
-      k.dsn[e] = accA;
-      k.dsd[e] = accB;
+      abs_[P * HP + i] = make_float2(al, be);
+      accA += al;
+      accB += be;
+      pC += al * (cvk - cvk1);
+      pGv += al * cvk1;
+      pA += al;
     }
-    gcur = gnext;
+    const float gdir = al * C;
+    // The gates depend on v^k only: evaluated in phases ahead of the barrier.
+    float ga[NS];
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
+    lds_barrier();
+    const char* ar = reinterpret_cast<const char*>(abs_ + P * HP);
+    float2 abj[NS];
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) abj[rr] = *reinterpret_cast<const float2*>(ar + jx[rr]);
+    float acc = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) {
+      const float4 p = preg[rr];
+      const float cx = abj[rr].x, cy = abj[rr].y;
+      const float a = ga[rr];
+      const float a2 = fmaf(-a, a, a);
+      const float dl = fmaf(cx, p.z, cy * p.w) * a2;
+      acc = fmaf(dl, p.x, acc);
+      gacc[rr].x = fmaf(cx, a, gacc[rr].x);
+      gacc[rr].y = fmaf(cy, a, gacc[rr].y);
+      gacc[rr].z += dl;
+      gacc[rr].w = fmaf(dl, cvk, gacc[rr].w);
+    }
+    const float sum = group_sum8(acc);
+    g = col ? fmaf(kNegLn2, sum, gdir) : 0.f;
+    if (n > 0) {
+      cvk = nvk;
+      crd = nrd;
+      cvk1 = nvk1;
+    }
+    if (u == 0) {
+      if (lead) {
+        const long long e = ((long long)b0 * T + t) * HP + i;
+        k.dsn[e] = accA;
+        k.dsd[e] = accB;
+      }
+      gcur = gnext;
+      --t;
+      u = U - 1;
+    } else {
+      --u;
+    }
+  };
+  const long long N = (long long)T * U;
+  long long m = 0;
+  for (; m + 1 < N; m += 2) {
+    unfold(std::integral_constant<int, 0>{});
+    unfold(std::integral_constant<int, 1>{});
   }
+  if (m < N) unfold(std::integral_constant<int, 0>{});
   if (lead) {
     if (k.gstate != nullptr && col) k.gstate[(long long)b0 * H + i] = g;
     float* np = k.npart + (long long)b0 * 3 * HP + i;
@@ -1376,8 +1424,43 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
     np[HP] = pGv;
     np[2 * HP] = pA;
   }
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
+  constexpr int HP = 64, RC = 8;
+  extern __shared__ float4 lds4[];
+  float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][64] alpha/beta by unfold parity
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int jg = lane >> 3;
+  const int i = (tid >> 6) * 8 + (lane & 7);  // presynaptic neuron (and its own alpha/beta column)
+  const bool lead = jg == 0;                  // one lane per neuron keeps the sums and stores
+  const int cnt = k.ccnt[i];
+  const int nmine = cnt > jg ? (cnt - 1 - jg) / 8 + 1 : 0;
+  const int nslot = wave_max(nmine);
+  float4 preg[RC], gacc[RC];
+  int jx[RC];
+#pragma unroll
+  for (int rr = 0; rr < RC; ++rr) {
+    const long long a = (long long)(jg * RC + rr) * HP + i;
+    preg[rr] = k.cimg[a];
+    jx[rr] = k.cidx[a] * 8;
+    gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (k.T == 0) return;
+  switch ((nslot + 1) >> 1) {
+    case 0:
+    case 1: bwd_row_wave_loop<2, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 2: bwd_row_wave_loop<4, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 3: bwd_row_wave_loop<6, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    default: bwd_row_wave_loop<8, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+  }
   // Recurrent-gradient partials through four padded [64][65] LDS planes at
-  // once, whole rows out (layout [workgroup][4][i][j]).
+  // once, whole rows out (layout [workgroup][4][i][j]); each lane places its
+  // entries' sums at their columns j. Places without an entry are left as
+  // they are (their synapses are masked or padding, and the finalize does not
+  // read them).
   constexpr int TLD = HP + 1, PL = HP * TLD;
   constexpr int NT = 512, PER = 4 * HP * HP / NT;
   float* tile = reinterpret_cast<float*>(lds4);
@@ -1385,12 +1468,14 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
   __syncthreads();
 #pragma unroll
   for (int rr = 0; rr < RC; ++rr) {
-    const float4 v4 = gacc[rr];
-    const int e = i * TLD + r0 + rr;
-    tile[e] = v4.x;
-    tile[PL + e] = v4.y;
-    tile[2 * PL + e] = v4.z;
-    tile[3 * PL + e] = v4.w;
+    if (rr < nmine) {
+      const float4 v4 = gacc[rr];
+      const int e = i * TLD + (jx[rr] >> 3);
+      tile[e] = v4.x;
+      tile[PL + e] = v4.y;
+      tile[2 * PL + e] = v4.z;
+      tile[3 * PL + e] = v4.w;
+    }
   }
   __syncthreads();
   float vals[PER];
@@ -1795,7 +1880,8 @@ template <int CPL>
 __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
                                                         int Hp, int Dp, int recb, int sensf,
                                                         int sensb, int nprep_blocks, int ncmp_blocks,
-                                                        LnBuf ln, int T, int BT) {
+                                                        int nchf, int nchb, LnBuf ln, int T,
+                                                        int BT) {
   if ((int)blockIdx.x >= nprep_blocks && (int)blockIdx.x < nprep_blocks + ncmp_blocks) {
     // Compacted columns, one per wave: forward (synapses whose w_pos or w_erev
     // is nonzero), then chain (synapses whose mask entry is nonzero).
@@ -1810,7 +1896,7 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
     if (pp.cF != nullptr) {
       if (col < Hp) {
         const int j = col;
-        compact_column(j, Hp, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+        compact_column(j, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
           if (i < H && j < H) {
             operand(i, j, v);
             act = v.z != 0.f || v.w != 0.f;
@@ -1822,7 +1908,7 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
     }
     if (recb && pp.cB != nullptr && col < Hp) {
       const int i = col;
-      compact_column(i, Hp, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+      compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
         if (i < H && j < H && lp.mask[(long long)i * H + j] != 0.f) {
           operand(i, j, v);
           act = true;
@@ -2277,11 +2363,6 @@ __device__ __forceinline__ void fwd_synapses_cmp(const float4* p, const float* v
     }
 }
 
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-  return __builtin_amdgcn_readfirstlane(v);
-}
 
 // RCP = 16 (Hp = 256): the compacted image (CMP). Thread (o, ks) holds the
 // entries ks, ks + 16, ... of column c's active rows, and the wave runs as
@@ -3072,7 +3153,8 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   const bool rec = (segs & kPrepRec) != 0;
   const int ncmp = (cmp_columns(pp, p.Hp, rec, rec && bwd) + 3) / 4;
   hipLaunchKernelGGL(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
-                     p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat);
+                     p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat, cmp_chunks_fwd(p),
+                     cmp_chunks_bwd(p));
   return hipGetLastError();
 }
 
@@ -3167,7 +3249,9 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
     }
   }
   FwdK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave,
-         p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, eps};
+         p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, eps, pp.cF, pp.cFi, pp.cFn};
+  if (cmp_fwd(p) && (pp.cF == nullptr || pp.cFi == nullptr || pp.cFn == nullptr))
+    return hipErrorInvalidValue;
   switch (p.NB) {
     case 16: return fwd_by_rcp<16>(p, a, s);
     case 8: return fwd_by_rcp<8>(p, a, s);
@@ -3201,7 +3285,9 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
     }
   }
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
-         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB};
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn};
+  if (cmp_bwd(p) && (pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr))
+    return hipErrorInvalidValue;
   switch (p.NB) {
     case 16: return bwd_by_rcp<16>(p, a, s);
     case 8: return bwd_by_rcp<8>(p, a, s);
@@ -3292,7 +3378,8 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
 #define LTC_PREPL(C)                                                                           \
   hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + ncmp + nln), dim3(256), 0, s, lp, pp, \
                      p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                          \
-                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, ncmp, lb, p.T, BT)
+                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, ncmp,          \
+                     cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT)
   if (nln == 0 || p.D <= 64) LTC_PREPL(1);
   else if (p.D <= 128) LTC_PREPL(2);
   else if (p.D <= 256) LTC_PREPL(4);

@@ -69,13 +69,13 @@ struct Plan {
 //   sensB[h][d] = {-Ss*log2e, Ss*Ms*log2e, Es, Ws*Ss}, [Hp][Dp]
 //   neuron = C[Hp], G[Hp], L[Hp]
 //
-// Compacted recurrent images (the register-resident cluster kernels, Hp = 256):
-// per column, the synapses that can contribute, in ascending row order; entry
-// e of column c sits in chunk e % 16, slot e / 16:
-//   cF[(ks*16 + s)*Hp + j]  forward operand of column j (postsynaptic), rows i
+// Compacted recurrent images (cmp_fwd / cmp_bwd): per column, the synapses
+// that can contribute, in ascending row order; with NC chunks (cmp_chunks_*)
+// of Hp/NC slots, entry e of column c sits in chunk e % NC, slot e / NC:
+//   cF[(ks*Hp/NC + s)*Hp + j]  forward operand of column j (postsynaptic), rows i
 //                           with WE or WP nonzero (a synapse with both zero adds
 //                           exact zeros to the forward sums);
-//   cB[(ks*16 + s)*Hp + i]  chain operand of column i (presynaptic), rows j: every
+//   cB[(ks*Hp/NC + s)*Hp + i]  chain operand of column i (presynaptic), rows j: every
 //                           real synapse, or on the module path only those whose
 //                           mask entry is nonzero (the others have zero gradients);
 //   cFi / cBi               the row index of each slot (0 in padding slots);
@@ -95,7 +95,7 @@ struct Prepped {
   int* cBi;
   int* cBn;
 };
-// Chunks (and slots per chunk) of a compacted image column.
+// Chunks (and slots per chunk) of a compacted image column at Hp = 256.
 constexpr int kCmpChunks = 16;
 // LDS of the compacted kernels' slot table: one int per slot per thread.
 inline long long cmp_index_lds(int threads) { return (long long)threads * kCmpChunks * 4; }
@@ -233,13 +233,23 @@ inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.
 inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
-// The cluster forward with register-resident operands (16 rows per thread,
-// Hp = 256) and the fused cluster chain with register-resident operands read
-// compacted images.
-inline bool cmp_fwd(const Plan& p) { return p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16; }
-inline bool cmp_bwd(const Plan& p) {
-  return p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16;
+// One row per workgroup at Hp = 64: the single-row kernels (every wave keeps
+// the row's state, one barrier per unfold, partials double-buffered).
+inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp == 64; }
+// Kernels that read compacted images: the cluster forward and the fused
+// cluster chain with register-resident operands (16 rows per thread,
+// Hp = 256), and the single-row forward (4 row groups of 16) and fused chain
+// (8 groups of 8) at Hp = 64. The chunk count is the number of row groups a
+// column's entries are dealt over.
+inline bool cmp_fwd(const Plan& p) {
+  return (p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16) || (row_kernels(p) && p.RC == 16);
 }
+inline bool cmp_bwd(const Plan& p) {
+  return (p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16) ||
+         (row_kernels(p) && p.FUSE && p.RCB == 8);
+}
+inline int cmp_chunks_fwd(const Plan& p) { return row_kernels(p) ? 4 : kCmpChunks; }
+inline int cmp_chunks_bwd(const Plan& p) { return row_kernels(p) ? 8 : kCmpChunks; }
 // Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
 // compacted image, its slot table.
 inline long long cluster_bwd_lds(const Plan& p) {
@@ -252,10 +262,6 @@ inline long long cluster_fwd_lds(const Plan& p) {
   return (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * 64 * 8 +
          (cmp_fwd(p) ? cmp_index_lds(64 * p.KS) : 0);
 }
-// One row per workgroup at Hp = 64: the single-row kernels (every wave keeps
-// the row's state, one barrier per unfold, partials double-buffered).
-inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp == 64; }
-
 // Dynamic LDS of the single-workgroup forward: state rows and the KS
 // partials, or the single-row kernel's two partial buffers.
 inline long long fwd_lds(const Plan& p) {
