@@ -313,6 +313,10 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
  * needed), the whole cluster leaves early, and the call then overwrites
  * every output it writes (out, h_final and saved for a forward; every
  * gradient for a backward) with NaN and raises a sticky per-device fault flag.
+ * The module-path backward at H <= 64 (one batch row per workgroup, D <= 128,
+ * B <= 64) runs its sensory and LayerNorm backward in companion workgroups
+ * that wait for the chain workgroups the same bounded way, with the same
+ * outcome (every gradient NaN, the flag raised) when one runs out.
  * The call itself has already returned LTC_OK by then (it only queues work);
  * ltc_device_status() waits for the current device, returns LTC_EHIP with a
  * message when the flag is raised, and clears it when `clear` is nonzero.
@@ -321,7 +325,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
  */
 int ltc_device_status(int clear);
 
-/* Wait budget of every cluster exchange, in ticks of the GPU's 100 MHz wall
+/* Wait budget of every cluster exchange (and companion wait), in ticks of the GPU's 100 MHz wall
  * clock (default 20000000 = 0.2 s), for calls made after it returns; returns
  * the previous budget, or -1 for a negative argument. A budget of 0 makes
  * every member give up at its first wait: a host-forced failure for tests of

@@ -350,13 +350,22 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
   w.dsd = c.take<float>((long long)p.B * p.T * p.Hp);
   w.npart = c.take<float>((long long)p.B * 3 * p.Hp);
   w.rpart = c.take<float>((long long)p.NCH * 4 * p.Hp * p.Hp);
-  w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
+  // sensory partials: NRC row chunks, or one per batch row (fused row backward)
+  const long long nrc = ltc::row_bwd_fused(p) && p.B > p.NRC ? p.B : p.NRC;
+  w.spart = c.take<float>(nrc * 4 * p.Dp * p.Hp);
   w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
   w.cb = carve_cluster(p, c, true);
   w.ps.rec = c.take<float>((long long)ltc::presum_parts(p.NCH) * 4 * p.Hp * p.Hp);
   w.ps.neuron = c.take<float>((long long)ltc::presum_parts(p.B) * 3 * p.Hp);
   w.ps.ln = c.take<float>((long long)ltc::presum_parts(ltc::ln_bwd_blocks(p)) * 4 * p.Dp);
   return w;
+}
+
+// LayerNorm column partials of the module backward: one per ln_bwd block, or
+// one per batch row when the fused row backward forms them.
+long long module_ln_parts(const ltc::Plan& p) {
+  const long long n = ltc::ln_bwd_blocks(p);
+  return ltc::row_bwd_fused(p) && p.B > n ? p.B : n;
 }
 
 // Module-path extras: the normalised input and its row statistics live in the
@@ -391,6 +400,12 @@ ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
   return pp;
 }
 
+// The fused row backward's exchange words and status word, after the images
+// in the module's saved buffer (cleared by the forward's prep launch).
+unsigned long long* carve_row_words(const ltc::Plan& p, Carver& c) {
+  return ltc::row_bwd_fused(p) ? c.take<unsigned long long>(ltc::row_bwd_words(p)) : nullptr;
+}
+
 long long module_saved_floats(const ltc::Plan& p) {
   // boundary saved buffer, then xa and stats, then the parameter images, each
   // at 64-float (256-byte) alignment
@@ -398,6 +413,7 @@ long long module_saved_floats(const ltc::Plan& p) {
   c.take<float>(saved_floats(p));
   carve_ln(p, c);
   carve_images(p, c);
+  carve_row_words(p, c);
   return (c.off + 3) / 4;
 }
 
@@ -776,7 +792,7 @@ long long ltc_module_bwd_workspace_bytes(int B, int T, int D, int H, int ode_unf
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
   Carver c{nullptr};
   carve_bwd(p, c, false);
-  c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  c.take<float>(module_ln_parts(p) * 4 * p.Dp);
   return round_up(c.off, 256);
 }
 
@@ -838,6 +854,7 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   int images = ltc::kLeafFwdImages;
   float* vsave = nullptr;
   float* densave = nullptr;
+  unsigned long long* row_words = nullptr;
   if (save_intermediates) {
     // Training: LayerNorm rows and every parameter image go to the saved
     // buffer, so the backward starts with the chain (no image launch).
@@ -847,12 +864,16 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
     sc.take<float>(saved_floats(p));
     lw = carve_ln(p, sc);
     pp = carve_images(p, sc);
+    row_words = carve_row_words(p, sc);
     images |= ltc::kLeafBwdImages;
   }
   const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
   const ltc::Strides3 xas{(long long)T * D, D, 1};
   hipError_t e;
-  e = timed(ltc::K_PREP, s, [&] { return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s); });
+  e = timed(ltc::K_PREP, s, [&] {
+    return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s, row_words,
+                                 row_words ? ltc::row_bwd_words(p) : 0);
+  });
   if (e != hipSuccess) return hip_fail("prep launch", e);
   e = timed(ltc::K_SENS_FWD, s,
             [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, pp, wfw.sn, wfw.sd, s); });
@@ -912,7 +933,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   const ltc::Plan p = make_plan(B, T, D, H, ode_unfolds);
   Carver need{nullptr};
   carve_bwd(p, need, false);
-  need.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  need.take<float>((long long)module_ln_parts(p) * 4 * p.Dp);
   if (workspace_bytes < need.off || (need.off > 0 && !workspace))
     return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
@@ -932,17 +953,35 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   }
   Carver c{static_cast<char*>(workspace)};
   BwdWs wb = carve_bwd(p, c, false);
-  float* lnpart = c.take<float>((long long)ltc::ln_bwd_blocks(p) * 4 * p.Dp);
+  float* lnpart = c.take<float>((long long)module_ln_parts(p) * 4 * p.Dp);
   Carver sc{const_cast<char*>(reinterpret_cast<const char*>(saved))};
   sc.take<float>(saved_floats(p));
   const LnWs lw = carve_ln(p, sc);
   wb.pp = carve_images(p, sc);  // built by the forward (ltc_module_forward)
+  unsigned long long* row_words = carve_row_words(p, sc);  // cleared by the forward
   const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
   const ltc::Strides3 xas{(long long)T * D, D, 1};
   const ltc::Strides3 gs{sgb, sgt, sgh};
   const float* vsave = saved;
   const float* densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
   hipError_t e;
+  if (row_words != nullptr) {
+    // The sensory and LayerNorm backward run inside the chain launch.
+    const ltc::RowCompanion rc{lw.xa, ln, input_w, ln_weight, ln_bias, wb.spart, lnpart,
+                               grad_x, row_words, g_spin.load(std::memory_order_relaxed)};
+    e = timed(ltc::K_ODE_BWD, s, [&] {
+      return ltc::launch_ode_bwd_row_fused(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final,
+                                           wb.npart, grad_state, wb.rpart, rc, s);
+    });
+    if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+    const int* status = reinterpret_cast<const int*>(row_words + ltc::row_bwd_words(p) - 1);
+    e = timed(ltc::K_FINALIZE, s, [&] {
+      return ltc::launch_finalize_leaf_fused(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps,
+                                             lg, status, grad_state, s);
+    });
+    if (e != hipSuccess) return hip_fail("finalize launch", e);
+    return LTC_OK;
+  }
   e = timed(ltc::K_ODE_BWD, s, [&] {
     return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.absave,
                                wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, wb.cb, s);
@@ -1005,7 +1044,9 @@ SensWs carve_sens(const ltc::Plan& p, Carver& c, bool bwd) {
   w.sn = c.take<float>((long long)p.B * p.Hp);
   w.sd = c.take<float>((long long)p.B * p.Hp);
   if (bwd) {
-    w.spart = c.take<float>((long long)p.NRC * 4 * p.Dp * p.Hp);
+    // sensory partials: NRC row chunks, or one per batch row (fused row backward)
+  const long long nrc = ltc::row_bwd_fused(p) && p.B > p.NRC ? p.B : p.NRC;
+  w.spart = c.take<float>(nrc * 4 * p.Dp * p.Hp);
     w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.Dp);
   }
   return w;
@@ -1359,8 +1400,9 @@ int ltc_device_status(int clear) {
   if (e != hipSuccess) return hip_fail("device status read", e);
   if (v != 0)
     return fail(LTC_EHIP,
-                "a cluster launch on this device gave up waiting for its partner workgroups "
-                "(the grid was not resident at once); every output of that call was set to NaN");
+                "a launch on this device gave up waiting for its partner workgroups (a "
+                "cluster, or a fused row backward's companions: the grid was not resident at "
+                "once); every output of that call was set to NaN");
   return LTC_OK;
 }
 

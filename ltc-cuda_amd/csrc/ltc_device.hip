@@ -36,6 +36,23 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegLn2 = -0.69314718055994531f;
 
+// The device's sticky fault flag: raised when a call's workgroups gave up
+// waiting for each other (a gated fill after a cluster launch, or the fused
+// row backward's finalize), read and cleared by the host (device_fault).
+__device__ int g_fault;
+
+// Exchange words between workgroups: {value bits, tag} written and read
+// whole as 64-bit agent-scope atomics, so no fence or counter is needed.
+__device__ __forceinline__ void xch_put(unsigned long long* w, float v, unsigned tag) {
+  const unsigned long long word =
+      (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
+  __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long xch_get(unsigned long long* w) {
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // sigmoid(z) for zp = -z*log2(e). v_exp_f32 saturates to +inf for large zp
 // and rcp(inf) = 0, while exp2 of a large negative zp is 0 and rcp(1) = 1, so
 // both saturated limits are exact and a*(1-a) is 0 there (never inf/inf).
@@ -50,6 +67,13 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum of v over the wave, in every lane (xor butterfly).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
 }
 
 // Largest value of v over the wave, as a wave-uniform value.
@@ -645,6 +669,9 @@ struct BwdK {
   const float4* cimg;
   const int* cidx;
   const int* ccnt;
+  // Fused row backward: dL/dsn, dL/dsd of each (row, step) go out as words
+  // [B*T][2][64] with tag 1 instead of into dsn / dsd.
+  unsigned long long* rbw;
 };
 
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
@@ -1400,8 +1427,13 @@ __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&
     if (u == 0) {
       if (lead) {
         const long long e = ((long long)b0 * T + t) * HP + i;
-        k.dsn[e] = accA;
-        k.dsd[e] = accB;
+        if (k.rbw != nullptr) {
+          xch_put(k.rbw + 2 * e - i, accA, 1u);
+          xch_put(k.rbw + 2 * e - i + HP, accB, 1u);
+        } else {
+          k.dsn[e] = accA;
+          k.dsd[e] = accB;
+        }
       }
       gcur = gnext;
       --t;
@@ -1427,7 +1459,7 @@ __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&
 }
 
 template <bool FULL>
-__global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
+__device__ __forceinline__ void bwd_row_wave_body(const BwdK& k) {
   constexpr int HP = 64, RC = 8;
   extern __shared__ float4 lds4[];
   float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][64] alpha/beta by unfold parity
@@ -1487,6 +1519,198 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
   }
 #pragma unroll
   for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
+  bwd_row_wave_body<FULL>(k);
+}
+
+// Companion of the fused row backward for batch row b (module path): the
+// sensory backward and the LayerNorm backward of the row's T steps, as the
+// chain workgroup of the row publishes each step's dL/dsn, dL/dsd (latest
+// step first). 8 waves; lane l and wave w hold the DC*8 sensory synapses
+// (d = l + 64*kk, h = 8w + m) with their operands and four gradient sums
+// {sum gm*a, sum dsn*a, sum gm*a', sum gm*a'*x} (gm = dsn*E + dsd,
+// a' = a(1 - a)) in registers, as sens_bwd_kernel forms them. Per step:
+// 128 threads wait for the step's words while the others stage its input row
+// in LDS; each thread then adds its synapses' terms and its partial of
+// dL/dxa[d] over its 8 neurons; wave 0 sums the 8 partials of every d in a
+// fixed order and finishes the row's LayerNorm backward as ln_bwd_kernel
+// does, accumulating the column sums. Every wait is bounded by c.spin ticks;
+// a companion that runs out sets the status word (after the words) and
+// leaves, and the finalize then writes NaN into every output of the call.
+template <int DC>
+__device__ __forceinline__ void row_companion(const BwdK& k, const RowCompanion& c,
+                                              const float4* sensB, int D, int Dp, int b) {
+  constexpr int HP = 64, NX = 64 * DC;
+  extern __shared__ float4 lds4[];
+  // The operands of the second 64 inputs (DC = 2) stay in LDS, [8][8][64]
+  // float4, the first 64's in registers.
+  float4* qsh = lds4;
+  float2* absh = reinterpret_cast<float2*>(lds4 + (DC - 1) * 8 * 8 * 64);  // [64] of the step
+  float* xsh = reinterpret_cast<float*>(absh + HP);  // [NX] the step's input row
+  float* dxr = xsh + NX;                             // [8][NX] per-wave dL/dxa partials
+  int* flag = reinterpret_cast<int*>(dxr + 8 * NX);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = k.T;
+  float4 q[8], sa[DC][8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    q[m] = sensB[(long long)(8 * w + m) * Dp + lane];
+    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = sensB[(long long)(8 * w + m) * Dp + lane + 64];
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk) sa[kk][m] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float iw[DC], lw[DC], lb[DC], cw[DC], cb[DC], cl[DC], cbl[DC];
+#pragma unroll
+  for (int kk = 0; kk < DC; ++kk) {
+    const int d = lane + 64 * kk;
+    iw[kk] = d < D ? c.input_w[d] : 0.f;
+    lw[kk] = d < D ? c.ln_w[d] : 0.f;
+    lb[kk] = d < D ? c.ln_b[d] : 0.f;
+    cw[kk] = cb[kk] = cl[kk] = cbl[kk] = 0.f;
+  }
+  if (tid == 0) *flag = 0;
+  __syncthreads();
+  for (int t = T - 1; t >= 0; --t) {
+    const long long row = (long long)b * T + t;
+    // wave 0's LayerNorm inputs of the row, requested before the wait
+    float mean = 0.f, rstd = 0.f, xr[DC];
+    if (w == 0) {
+      mean = c.ln.stats[2 * row];
+      rstd = c.ln.stats[2 * row + 1];
+      const float* xrow = c.ln.x + (long long)b * c.ln.xs.b + (long long)t * c.ln.xs.t;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        xr[kk] = d < D ? xrow[(long long)d * c.ln.xs.c] : 0.f;
+      }
+    }
+    if (tid < 2 * HP) {
+      unsigned long long* wd = c.words + (row * 2 + (tid >> 6)) * HP + (tid & 63);
+      bool ok = c.spin > 0;
+      if (ok) {
+        unsigned long long v = xch_get(wd);
+        const long long t0 = wall_clock64();
+        while ((unsigned)(v >> 32) != 1u) {
+          if (wall_clock64() - t0 > c.spin) {
+            ok = false;
+            break;
+          }
+          v = xch_get(wd);
+        }
+        reinterpret_cast<float*>(absh)[(tid & 63) * 2 + (tid >> 6)] = __uint_as_float((unsigned)v);
+      }
+      if (!ok) *flag = 1;
+    } else if (tid - 2 * HP < NX) {
+      const int d = tid - 2 * HP;
+      xsh[d] = d < D ? c.xa[row * D + d] : 0.f;
+    }
+    __syncthreads();
+    if (*flag) break;
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk) {
+      const float xv = xsh[lane + 64 * kk];
+      float dxp = 0.f;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const float2 cc = absh[8 * w + m];
+        const float4 p = kk == 0 ? q[m] : qsh[(w * 8 + m) * 64 + lane];
+        const float a = gate(fmaf(p.x, xv, p.y));
+        const float a2 = fmaf(-a, a, a);
+        const float gm = fmaf(cc.x, p.z, cc.y);
+        sa[kk][m].x = fmaf(gm, a, sa[kk][m].x);
+        sa[kk][m].y = fmaf(cc.x, a, sa[kk][m].y);
+        const float ga2 = gm * a2;
+        sa[kk][m].z += ga2;
+        sa[kk][m].w = fmaf(ga2, xv, sa[kk][m].w);
+        dxp = fmaf(ga2, p.w, dxp);
+      }
+      dxr[w * NX + lane + 64 * kk] = dxp;
+      // one block of 64 inputs at a time (keeps the live registers in bounds)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    if (w == 0) {
+      float xh[DC], gxh[DC];
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        xh[kk] = gxh[kk] = 0.f;
+        if (d < D) {
+          float gxa = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < 8; ++ww) gxa += dxr[ww * NX + d];
+          xh[kk] = (xr[kk] - mean) * rstd;
+          const float xn = xh[kk] * lw[kk] + lb[kk];
+          const float gxn = gxa * iw[kk];
+          gxh[kk] = gxn * lw[kk];
+          cw[kk] = fmaf(gxa, xn, cw[kk]);
+          cb[kk] += gxa;
+          cl[kk] = fmaf(gxn, xh[kk], cl[kk]);
+          cbl[kk] += gxn;
+          s1 += gxh[kk];
+          s2 = fmaf(gxh[kk], xh[kk], s2);
+        }
+      }
+      const float m1 = wave_sum(s1) / (float)D, m2 = wave_sum(s2) / (float)D;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        if (d < D) c.gx[row * D + d] = rstd * (gxh[kk] - m1 - xh[kk] * m2);
+      }
+    }
+  }
+  if (*flag) {
+    if (tid == 0)
+      __hip_atomic_store(reinterpret_cast<int*>(c.words + (long long)k.B * T * 128), 1,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  // One sensory partial per row, layout [4][Hp][Dp] as sens_bwd_kernel's.
+  const long long DH = (long long)Dp * HP;
+  float* out = c.spart + (long long)b * 4 * DH;
+#pragma unroll
+  for (int kk = 0; kk < DC; ++kk)
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const long long e = (long long)(8 * w + m) * Dp + lane + 64 * kk;
+      out[e] = sa[kk][m].x;
+      out[DH + e] = sa[kk][m].y;
+      out[2 * DH + e] = sa[kk][m].z;
+      out[3 * DH + e] = sa[kk][m].w;
+    }
+  if (w == 0) {
+    float* lo = c.lnpart + (long long)b * 4 * Dp;
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk) {
+      const int d = lane + 64 * kk;
+      lo[d] = cw[kk];
+      lo[Dp + d] = cb[kk];
+      lo[2 * Dp + d] = cl[kk];
+      lo[3 * Dp + d] = cbl[kk];
+    }
+  }
+}
+
+// Fused row backward: workgroups [0, B) run the chain of their batch row
+// (bwd_row_wave_body, publishing dL/dsn, dL/dsd as words), workgroups
+// [Bc, Bc + B) the companions (Bc = B rounded up to 8, so that the companion
+// of row b runs on the same XCD as its chain workgroup); the ones between
+// return at once. The chain workgroups come first in the grid, so they are
+// dispatched before the companions that wait on them.
+template <bool FULL, int DC>
+__global__ __launch_bounds__(512) void ode_bwd_row_fused_kernel(BwdK k, RowCompanion c,
+                                                                const float4* sensB, int D, int Dp,
+                                                                int Bc) {
+  const int g = blockIdx.x;
+  if (g < k.B) {
+    bwd_row_wave_body<FULL>(k);
+  } else if (g >= Bc && g - Bc < k.B) {
+    row_companion<DC>(k, c, sensB, D, Dp, g - Bc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1861,11 +2085,6 @@ __device__ __forceinline__ float softplus_grad(float x) {
   return z / (z + 1.f);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 
 // Parameter images from the leaves (same flat segments as prep_kernel), plus
@@ -1881,7 +2100,8 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
                                                         int Hp, int Dp, int recb, int sensf,
                                                         int sensb, int nprep_blocks, int ncmp_blocks,
                                                         int nchf, int nchb, LnBuf ln, int T,
-                                                        int BT) {
+                                                        int BT, unsigned long long* clr,
+                                                        long long nclr) {
   if ((int)blockIdx.x >= nprep_blocks && (int)blockIdx.x < nprep_blocks + ncmp_blocks) {
     // Compacted columns, one per wave: forward (synapses whose w_pos or w_erev
     // is nonzero), then chain (synapses whose mask entry is nonzero).
@@ -2006,7 +2226,11 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
       else v = lp.vleak[j];
     }
     pp.neuron[tid] = v;
+    return;
   }
+  tid -= 3LL * Hp;
+  // the fused row backward's exchange words and status word (tag 0)
+  if (tid < nclr) clr[tid] = 0ULL;
 }
 
 // LayerNorm + affine backward. Block 256 = 4 waves, `rpb` rows per block (4
@@ -2115,10 +2339,54 @@ struct FinLeafK {
   const float* lnpart;
   LeafGrads g;
   int B, D, H, Hp, Dp, NCH, NRC, NLN;  // B, NCH: counts of neuron / recurrent partials
+  // Fused row backward: its status word, and the two outputs written before
+  // the finalize (dL/dx over nx floats, dL/dh0 over ns floats), which also
+  // become NaN when the status is set.
+  const int* status;
+  float* gstate;
+  long long nx, ns;
 };
+
+// Every output this thread owns, NaN (a fused row backward gave up).
+__device__ __forceinline__ void finalize_leaf_poison(const FinLeafK& k, long long tid) {
+  const float nan = __builtin_nanf("");
+  const long long nrec = (long long)k.H * k.H, nsens = (long long)k.D * k.H;
+  if (tid == 0) __hip_atomic_store(&g_fault, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid < nrec) {
+    k.g.w[tid] = k.g.erev[tid] = k.g.mu[tid] = k.g.sigma[tid] = nan;
+    return;
+  }
+  tid -= nrec;
+  if (tid < nsens) {
+    k.g.s_w[tid] = k.g.s_erev[tid] = k.g.s_mu[tid] = k.g.s_sigma[tid] = nan;
+    return;
+  }
+  tid -= nsens;
+  if (tid < k.H) {
+    k.g.cm[tid] = k.g.gleak[tid] = k.g.vleak[tid] = nan;
+    return;
+  }
+  tid -= k.H;
+  if (tid < k.D) {
+    k.g.input_w[tid] = k.g.input_b[tid] = k.g.ln_w[tid] = k.g.ln_b[tid] = nan;
+    return;
+  }
+  tid -= k.D;
+  if (tid < k.nx) {
+    k.g.x[tid] = nan;
+    return;
+  }
+  tid -= k.nx;
+  if (tid < k.ns && k.gstate != nullptr) k.gstate[tid] = nan;
+}
 
 __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
   long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k.status != nullptr &&
+      __hip_atomic_load(k.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+    finalize_leaf_poison(k, tid);
+    return;
+  }
   const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
   const long long nrec = (long long)H * H, nsens = (long long)D * H;
   if (tid < nrec) {
@@ -2210,15 +2478,6 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
 // ---------------------------------------------------------------------------
 constexpr int kClW = 64;                    // columns per cluster member
 
-__device__ __forceinline__ void xch_put(unsigned long long* w, float v, unsigned tag) {
-  const unsigned long long word =
-      (unsigned long long)__float_as_uint(v) | ((unsigned long long)tag << 32);
-  __hip_atomic_store(w, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ unsigned long long xch_get(unsigned long long* w) {
-  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Reads the (CP-1)*PER words of the other members for unfold `tag`, XB per
 // thread at a time. For each word: pre(x, a) is called once before the first
@@ -3008,9 +3267,6 @@ __global__ __launch_bounds__(256) void clear_words_kernel(unsigned long long* w,
   if (i == 0 && status != nullptr) *status = 0;
 }
 
-// The device's sticky fault flag: raised by a gated fill after a cluster
-// member gave up, read and cleared by the host (device_fault).
-__device__ int g_fault;
 
 // Segment list fill/copy (see FillList). Grid-stride over the concatenated
 // segments; with a gate, every thread first reads it and leaves when it is 0.
@@ -3285,7 +3541,7 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
     }
   }
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
-         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn};
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, nullptr};
   if (cmp_bwd(p) && (pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr))
     return hipErrorInvalidValue;
   switch (p.NB) {
@@ -3295,6 +3551,32 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
     case 2: return bwd_by_rcp<2>(p, a, s);
     default: return bwd_by_rcp<1>(p, a, s);
   }
+}
+
+hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const float* vsave,
+                                    const float* densave, const float* gout, Strides3 gs,
+                                    const float* ghfin, float* npart, float* gstate, float* rpart,
+                                    const RowCompanion& rc, hipStream_t s) {
+  if (!row_bwd_fused(p) || pp.cB == nullptr || pp.sensB == nullptr || rc.words == nullptr)
+    return hipErrorInvalidValue;
+  BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, nullptr, nullptr, nullptr,
+         npart, gstate, rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn,
+         rc.words};
+  const int Bc = (p.B + 7) / 8 * 8;
+  const dim3 grid((unsigned)(Bc + p.B)), block(512);
+  const int DC = p.Dp / 64;
+  // the chain's LDS (its gradient tile), or the companion's when larger
+  const size_t comp = (size_t)((DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9 * 64 * DC * 4 + 16);
+  const size_t lds = bwd_lds_bytes(p) > comp ? bwd_lds_bytes(p) : comp;
+#define LTC_RBF(F, C) \
+  hipLaunchKernelGGL((ode_bwd_row_fused_kernel<F, C>), grid, block, lds, s, a, rc, pp.sensB, p.D, p.Dp, Bc)
+  if (p.H == 64) {
+    if (DC == 1) LTC_RBF(true, 1); else LTC_RBF(true, 2);
+  } else {
+    if (DC == 1) LTC_RBF(false, 1); else LTC_RBF(false, 2);
+  }
+#undef LTC_RBF
+  return hipGetLastError();
 }
 
 hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
@@ -3367,8 +3649,11 @@ hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpar
 }
 
 hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
-                            const LnBuf* ln, hipStream_t s) {
-  const long long total = (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp;
+                            const LnBuf* ln, hipStream_t s, unsigned long long* clear_words,
+                            long long nclear) {
+  if (clear_words == nullptr) nclear = 0;
+  const long long total =
+      (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp + nclear;
   const int nprep = (int)((total + 255) / 256);
   const int BT = p.B * p.T;
   const int nln = ln ? (BT + 3) / 4 : 0;
@@ -3379,7 +3664,7 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + ncmp + nln), dim3(256), 0, s, lp, pp, \
                      p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                          \
                      (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, ncmp,          \
-                     cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT)
+                     cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT, clear_words, nclear)
   if (nln == 0 || p.D <= 64) LTC_PREPL(1);
   else if (p.D <= 128) LTC_PREPL(2);
   else if (p.D <= 256) LTC_PREPL(4);
@@ -3430,8 +3715,27 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
     nln = parts;
   }
   FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
-             pt.nrec, p.NRC, nln};
+             pt.nrec, p.NRC, nln, nullptr, nullptr, 0, 0};
   const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_finalize_leaf_fused(const Plan& p, const LeafParams& lp, const float* rpart,
+                                      const float* spart, const float* npart,
+                                      const float* lnpart, const PresumBuf& ps,
+                                      const LeafGrads& g, const int* status, float* gstate,
+                                      hipStream_t s) {
+  if (!row_bwd_fused(p)) return hipErrorInvalidValue;
+  Partials pt;
+  hipError_t e = presum(p, rpart, npart, ps, s, pt);
+  if (e != hipSuccess) return e;
+  const long long nx = (long long)p.B * p.T * p.D, ns = (long long)p.B * p.H;
+  // one sensory and one LayerNorm partial per batch row (B <= 64)
+  FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
+             pt.nrec, p.B, p.B, status, gstate, nx, ns};
+  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D + nx + ns;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -173,7 +173,8 @@ hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long
 constexpr int kLeafFwdImages = 1;
 constexpr int kLeafBwdImages = 2;
 hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
-                            const LnBuf* ln, hipStream_t s);
+                            const LnBuf* ln, hipStream_t s, unsigned long long* clear_words = nullptr,
+                            long long nclear = 0);
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
 // Cluster path scratch: exchange words and a status word (nonzero after a
@@ -248,6 +249,15 @@ inline bool cmp_bwd(const Plan& p) {
   return (p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16) ||
          (row_kernels(p) && p.FUSE && p.RCB == 8);
 }
+// Module-path backward at Hp = 64 with one row per workgroup, Dp <= 128 and
+// B <= 64: the sensory and LayerNorm backward run inside the chain launch, in
+// one companion workgroup per batch row that takes each step's dL/dsn, dL/dsd
+// from its row's chain workgroup as {value, tag} words (row_bwd_words of
+// them: [B*T][2][64], then a status word).
+inline bool row_bwd_fused(const Plan& p) {
+  return row_kernels(p) && p.FUSE && p.RCB == 8 && p.Dp <= 128 && p.B >= 1 && p.B <= 64;
+}
+inline long long row_bwd_words(const Plan& p) { return (long long)p.B * p.T * 128 + 1; }
 inline int cmp_chunks_fwd(const Plan& p) { return row_kernels(p) ? 4 : kCmpChunks; }
 inline int cmp_chunks_bwd(const Plan& p) { return row_kernels(p) ? 8 : kCmpChunks; }
 // Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
@@ -364,5 +374,34 @@ hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
                                 const float* spart, const float* npart, const float* lnpart,
                                 const PresumBuf& ps, const LeafGrads& g, hipStream_t s);
+
+// Fused row backward (row_bwd_fused): the chain of every batch row plus one
+// companion workgroup per row for its sensory and LayerNorm backward. The
+// companions write the sensory partials (one per row, [B][4][Hp][Dp]), the
+// LayerNorm column partials ([B][4][Dp]) and dL/dx; a companion that runs out
+// of its wait budget sets *status instead.
+struct RowCompanion {
+  const float* xa;     // [B*T][D] LayerNorm + affine output (the sensory input)
+  LnBuf ln;            // raw input and row statistics
+  const float* input_w;
+  const float* ln_w;
+  const float* ln_b;
+  float* spart;
+  float* lnpart;
+  float* gx;
+  unsigned long long* words;  // row_bwd_words(p), cleared before the launch
+  long long spin;
+};
+hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const float* vsave,
+                                    const float* densave, const float* gout, Strides3 gs,
+                                    const float* ghfin, float* npart, float* gstate, float* rpart,
+                                    const RowCompanion& rc, hipStream_t s);
+// The module finalize after a fused row backward: B sensory and B LayerNorm
+// partials, and with *status set every output (also dL/dx and dL/dh0) NaN.
+hipError_t launch_finalize_leaf_fused(const Plan& p, const LeafParams& lp, const float* rpart,
+                                      const float* spart, const float* npart,
+                                      const float* lnpart, const PresumBuf& ps,
+                                      const LeafGrads& g, const int* status, float* gstate,
+                                      hipStream_t s);
 
 }  // namespace ltc

@@ -91,3 +91,33 @@ def test_module_path_give_up_is_reported_through_python(capi):
     with pytest.raises(RuntimeError, match="gave up"):
         ltc_cuda.device_status()
     ltc_cuda.device_status()  # cleared by the call that raised
+
+
+@pytest.mark.parametrize("D1", [128, 48])
+def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi, D1):
+    """At H = 64 the module backward's sensory and LayerNorm part runs in
+    companion workgroups that wait for the chain's words: with a budget of 0
+    they leave at once, and the finalize writes NaN into every gradient."""
+    B1, T1, H1 = 24, 8, 64
+    plan = capi.plan(B1, T1, D1, H1, 6)
+    assert plan["CP"] == 0 and plan["Hp"] == 64 and plan["NB"] == 1 and plan["fuse"] == 1, plan
+    m = _perturbed_module(D1, H1, seed=34).to(DEV)
+    x = torch.randn(B1, T1, D1, device=DEV, requires_grad=True)
+    h0 = (torch.randn(B1, H1, device=DEV) * 0.2).requires_grad_(True)
+    out, (h, _) = m(x, (h0, h0))
+    assert torch.isfinite(out).all()
+    with _NoWait(capi):
+        (out.sum() + h.sum()).backward()
+    assert torch.isnan(x.grad).all() and torch.isnan(h0.grad).all()
+    for n, p in m.named_parameters():
+        assert torch.isnan(p.grad).all(), n
+    _expect_fault(capi)
+    m.zero_grad(set_to_none=True)
+    x.grad = h0.grad = None
+    out, (h, _) = m(x, (h0, h0))
+    (out.sum() + h.sum()).backward()
+    assert torch.isfinite(x.grad).all() and torch.isfinite(h0.grad).all()
+    for n, p in m.named_parameters():
+        assert torch.isfinite(p.grad).all(), n
+    capi.device_status()
+
