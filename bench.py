@@ -189,6 +189,9 @@ def kernel_times(capi, fn, iters):
 
 def roofline(c, ktimes, fused_chain, traffic=None, counts=None):
     fl = kernel_flops(c, fused_chain, counts)
+    if "ltc_ode_bwd" in ktimes and "ltc_sens_bwd" not in ktimes and "ltc_sens_fwd" in ktimes:
+        # the fused row backward: the chain launch also runs the sensory backward
+        fl["ltc_ode_bwd"] += fl["ltc_sens_bwd"]
     per_step = {k: avg * per for k, (avg, per) in ktimes.items()}
     dom = max(per_step, key=per_step.get)
     avg_ms = ktimes[dom][0]

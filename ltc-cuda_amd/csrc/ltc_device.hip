@@ -2932,14 +2932,18 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   __shared__ int gave_up;
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
   const int RC = RCP > 0 ? RCP : (RCS > 0 ? RCS : k.RC);
-  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp] ([Hp][NB] with CMP)
-  float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][JW]
+  // alpha/beta: [NB][Hp], or with CMP [Hp][ABS] float2, rows padded to
+  // ABS = NB + 2 pairs so that the per-lane row reads of 16 lanes spread over
+  // 16 bank groups instead of 4
+  constexpr int ABS = CMP ? NB + 2 : NB;
+  float2* ab = reinterpret_cast<float2*>(lds4);
+  float* red = reinterpret_cast<float*>(ab + ABS * Hp);  // [KS][NB][JW]
   // PF: saved forward values of the cluster's rows, fetched one synapse
   // phase ahead of use: 1/den of unfold n-1, and v of slots n and n-1.
   float* pden = red + KS * NB * JW;                     // [NB][Hp]
   float* pv = pden + NB * Hp;                           // [2][NB][Hp]
   int4* slot_tab = reinterpret_cast<int4*>(pv + 2 * NB * Hp);  // CMP: [4][threads]
-  auto abat = [&](int b, int col) { return CMP ? col * NB + b : b * Hp + col; };
+  auto abat = [&](int b, int col) { return CMP ? col * ABS + b : b * Hp + col; };
   const int tid = threadIdx.x, nthr = blockDim.x;
   // With JW = 64 ks is uniform across each wave; with JW = 32 a wave holds two.
   const int ks = JW == 64 ? __builtin_amdgcn_readfirstlane(tid / JW) : tid / JW;
@@ -2969,7 +2973,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     for (int rr = 0; rr < RCP; ++rr) {
       const long long a = (long long)(ks * RCP + rr) * Hp + c;
       preg[rr] = k.cimg[a];
-      ix[rr] = k.cidx[a] * NB * 8;
+      ix[rr] = k.cidx[a] * ABS * 8;
     }
 #pragma unroll
     for (int q = 0; q < RCP / 4; ++q)

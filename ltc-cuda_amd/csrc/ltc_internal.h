@@ -99,6 +99,8 @@ struct Prepped {
 constexpr int kCmpChunks = 16;
 // LDS of the compacted kernels' slot table: one int per slot per thread.
 inline long long cmp_index_lds(int threads) { return (long long)threads * kCmpChunks * 4; }
+// The compacted cluster chain pads each alpha/beta row by two pairs.
+inline long long cmp_pad_lds(int hp) { return 16LL * hp; }
 
 struct RawParams {
   const float* w_pos;
@@ -264,7 +266,7 @@ inline int cmp_chunks_bwd(const Plan& p) { return row_kernels(p) ? 8 : kCmpChunk
 // compacted image, its slot table.
 inline long long cluster_bwd_lds(const Plan& p) {
   return cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, chain_prefetches(p)) +
-         (cmp_bwd(p) ? cmp_index_lds(p.JWB * p.KSB) : 0);
+         (cmp_bwd(p) ? cmp_index_lds(p.JWB * p.KSB) + cmp_pad_lds(p.Hp) : 0);
 }
 // Dynamic LDS of a cluster forward member: state rows [NB][Hp], the KS
 // partials [KS][NB][64] float2, and with the compacted image the slot table.
