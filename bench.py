@@ -452,6 +452,10 @@ def measure_config(name, c, capi, cpu):
     rec["mix_frac_kernels"] = round(mix_bound_ms(c, which, counts) / ksum, 4)
     rec["flop_frac_kernels"] = round(
         flop_count(c, which, counts) / (ksum * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)
+    # the same against the dense, mask-inclusive work of the unit (every
+    # synapse evaluated, as the reference does): what skipping buys
+    rec["valu_mix_bound_dense_ms"] = round(mix_bound_ms(c, which), 4)
+    rec["mix_frac_kernels_dense"] = round(mix_bound_ms(c, which) / ksum, 4)
     rec["memory"] = peak_memory_mb(m, x, target, train)
     del m, x, target
     torch.cuda.empty_cache()
