@@ -525,15 +525,75 @@ __device__ __forceinline__ void fwd_synapses(const float4* p, const float* vs, i
     }
 }
 
+// The NB state values of LDS row r in the compacted kernels' [Hp][NB] layout.
+template <int NB>
+__device__ __forceinline__ void lds_rows(const float* base, int byte_off, float (&v)[NB]) {
+  const char* at = reinterpret_cast<const char*>(base) + byte_off;
+  if constexpr (NB % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < NB; q += 4) {
+      const float4 w = *reinterpret_cast<const float4*>(at + q * 4);
+      v[q] = w.x;
+      v[q + 1] = w.y;
+      v[q + 2] = w.z;
+      v[q + 3] = w.w;
+    }
+  } else if constexpr (NB == 2) {
+    const float2 w = *reinterpret_cast<const float2*>(at);
+    v[0] = w.x;
+    v[1] = w.y;
+  } else {
+    v[0] = *reinterpret_cast<const float*>(at);
+  }
+}
+
+// Two compacted forward synapses (slots with LDS row offsets o0, o1) for every
+// row of the tile, gates in phases as in fwd_synapses.
+template <int NB>
+__device__ __forceinline__ void fwd_synapses_cmp(const float4* p, const float* vs, int o0, int o1,
+                                                 float* na, float* qa) {
+  float z[2][NB];
+  lds_rows<NB>(vs, o0, z[0]);
+  lds_rows<NB>(vs, o1, z[1]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = fmaf(p[i].x, z[i][b], p[i].y);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = 1.0f + __builtin_amdgcn_exp2f(z[i][b]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) z[i][b] = __builtin_amdgcn_rcpf(z[i][b]);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      na[b] = fmaf(z[i][b], p[i].z, na[b]);
+      qa[b] = fmaf(z[i][b], p[i].w, qa[b]);
+    }
+}
+
+// With register-resident operands (RCP > 0) the kernel reads the compacted
+// image (CMP): thread (o, ks) holds the entries ks, ks + KS, ... of column o,
+// the wave runs as many slots as its fullest lane (wave-uniform branches
+// around unused pairs), the state sits in LDS as [Hp][NB] so that a slot's NB
+// values are one read at a per-lane row, and the slot row offsets come from an
+// LDS table [RCP/4][threads] of int4.
 template <int NB, int RCP>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   constexpr int MO = ode_owned_rows(NB);
+  constexpr bool CMP = RCP > 0;
   extern __shared__ float4 lds4[];
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
   const int RC = RCP > 0 ? RCP : k.RC;
-  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp]
+  float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp] ([Hp][NB] with CMP)
   float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][Hp]
-  const int tid = threadIdx.x;
+  int4* slot_tab = reinterpret_cast<int4*>(red + KS * NB * Hp);  // CMP: [RCP/4][threads]
+  auto vat = [&](int b, int j) { return CMP ? j * NB + b : b * Hp + j; };
+  const int tid = threadIdx.x, nthr = blockDim.x;
   // Hp is a multiple of 64, so ks is uniform across each wave.
   const int ks = __builtin_amdgcn_readfirstlane(tid / Hp), o = tid - ks * Hp;
   const __amdgpu_buffer_rsrc_t rsF = image_rsrc(k.recF, (long long)Hp * Hp * 16);
@@ -544,15 +604,27 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   const float GL = G * L, CG = C + G;
 
   float4 preg[RCP > 0 ? RCP : 1];
-  if constexpr (RCP > 0) {
+  int nslot = 0;  // CMP: slots the wave runs
+  if constexpr (CMP) {
+    const int cnt = k.ccnt[o];
+    nslot = wave_max(cnt > ks ? (cnt - 1 - ks) / KS + 1 : 0);
+    int ix[RCP];
 #pragma unroll
-    for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * Hp + o];
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(ks * RCP + rr) * Hp + o;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * NB * 4;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
   }
 
   for (int e = tid; e < NB * Hp; e += blockDim.x) {
     const int b = e / Hp, j = e - b * Hp;
-    vs[e] = (k.state0 != nullptr && b0 + b < B && j < H) ? k.state0[(long long)(b0 + b) * H + j]
-                                                          : 0.f;
+    vs[vat(b, j)] = (k.state0 != nullptr && b0 + b < B && j < H)
+                        ? k.state0[(long long)(b0 + b) * H + j]
+                        : 0.f;
   }
   lds_barrier();
 
@@ -577,10 +649,16 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
       float na[NB], qa[NB];
 #pragma unroll
       for (int b = 0; b < NB; ++b) na[b] = qa[b] = 0.f;
-      if constexpr (RCP > 0) {
+      if constexpr (CMP) {
+        // Wave-uniform slot count: the skipped pairs branch around.
 #pragma unroll
-        for (int rr = 0; rr < RCP; rr += kFwdGroup<NB>)
-          fwd_synapses<NB, kFwdGroup<NB>>(preg + rr, vs, Hp, r0 + rr, na, qa);
+        for (int q = 0; q < RCP / 4; ++q) {
+          if (4 * q < nslot) {
+            const int4 of = slot_tab[q * nthr + tid];
+            fwd_synapses_cmp<NB>(preg + 4 * q, vs, of.x, of.y, na, qa);
+            if (4 * q + 2 < nslot) fwd_synapses_cmp<NB>(preg + 4 * q + 2, vs, of.z, of.w, na, qa);
+          }
+        }
       } else {
         // Operands stream from L2, the next four requested while the current
         // four are evaluated.
@@ -603,7 +681,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
           const float2 nq = NB <= 2 ? ks_sum_1r(red + b * Hp + o, NB * Hp, KS)
                                     : ks_sum(red + b * Hp + o, NB * Hp, KS);
           const float n = nq.x, q = nq.y;
-          const float vold = vs[b * Hp + o];
+          const float vold = vs[vat(b, o)];
           const float den = CG + (q + sdr[m]) + k.eps;
           const float num = C * vold + GL + (n + snr[m]);
           // 1/den from v_rcp_f32 (within 1 ulp): the new state is num/den to
@@ -617,7 +695,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
             k.vsave[e] = vold;
             k.densave[e] = rden;
           }
-          vs[b * Hp + o] = vnew;
+          vs[vat(b, o)] = vnew;
           if (u == U - 1 && live && o < H) k.out[((long long)(b0 + b) * T + t) * H + o] = vnew;
         }
       }
@@ -635,7 +713,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   for (int m = 0; m < MO; ++m) {
     const int b = ks + m * KS;
     if (b < NB && b0 + b < B) {
-      const float v = vs[b * Hp + o];
+      const float v = vs[vat(b, o)];
       if (o < H) k.hfin[(long long)(b0 + b) * H + o] = v;
       if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0 + b) * Hp + o] = v;
     }
@@ -2571,56 +2649,6 @@ struct FwdCK {
   const int* ccnt;
 };
 
-// The NB state values of LDS row r in the compacted kernels' [Hp][NB] layout.
-template <int NB>
-__device__ __forceinline__ void lds_rows(const float* base, int byte_off, float (&v)[NB]) {
-  const char* at = reinterpret_cast<const char*>(base) + byte_off;
-  if constexpr (NB % 4 == 0) {
-#pragma unroll
-    for (int q = 0; q < NB; q += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(at + q * 4);
-      v[q] = w.x;
-      v[q + 1] = w.y;
-      v[q + 2] = w.z;
-      v[q + 3] = w.w;
-    }
-  } else if constexpr (NB == 2) {
-    const float2 w = *reinterpret_cast<const float2*>(at);
-    v[0] = w.x;
-    v[1] = w.y;
-  } else {
-    v[0] = *reinterpret_cast<const float*>(at);
-  }
-}
-
-// Two compacted forward synapses (slots with LDS row offsets o0, o1) for every
-// row of the tile, gates in phases as in fwd_synapses.
-template <int NB>
-__device__ __forceinline__ void fwd_synapses_cmp(const float4* p, const float* vs, int o0, int o1,
-                                                 float* na, float* qa) {
-  float z[2][NB];
-  lds_rows<NB>(vs, o0, z[0]);
-  lds_rows<NB>(vs, o1, z[1]);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) z[i][b] = fmaf(p[i].x, z[i][b], p[i].y);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) z[i][b] = 1.0f + __builtin_amdgcn_exp2f(z[i][b]);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) z[i][b] = __builtin_amdgcn_rcpf(z[i][b]);
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      na[b] = fmaf(z[i][b], p[i].z, na[b]);
-      qa[b] = fmaf(z[i][b], p[i].w, qa[b]);
-    }
-}
 
 
 // RCP = 16 (Hp = 256): the compacted image (CMP). Thread (o, ks) holds the

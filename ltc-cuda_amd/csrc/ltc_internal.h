@@ -244,8 +244,14 @@ inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp =
 // Hp = 256), and the single-row forward (4 row groups of 16) and fused chain
 // (8 groups of 8) at Hp = 64. The chunk count is the number of row groups a
 // column's entries are dealt over.
+// The single-workgroup forward with register-resident operands (RC of 4, 8 or
+// 16) reads one too, its entries dealt over its KS row chunks.
+inline bool generic_fwd_cmp(const Plan& p) {
+  return p.CP == 0 && !row_kernels(p) && (p.RC == 4 || p.RC == 8 || p.RC == 16);
+}
 inline bool cmp_fwd(const Plan& p) {
-  return (p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16) || (row_kernels(p) && p.RC == 16);
+  return (p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16) || (row_kernels(p) && p.RC == 16) ||
+         generic_fwd_cmp(p);
 }
 inline bool cmp_bwd(const Plan& p) {
   return (p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16) ||
@@ -260,7 +266,9 @@ inline bool row_bwd_fused(const Plan& p) {
   return row_kernels(p) && p.FUSE && p.RCB == 8 && p.Dp <= 128 && p.B >= 1 && p.B <= 64;
 }
 inline long long row_bwd_words(const Plan& p) { return (long long)p.B * p.T * 128 + 1; }
-inline int cmp_chunks_fwd(const Plan& p) { return row_kernels(p) ? 4 : kCmpChunks; }
+inline int cmp_chunks_fwd(const Plan& p) {
+  return row_kernels(p) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
+}
 inline int cmp_chunks_bwd(const Plan& p) { return row_kernels(p) ? 8 : kCmpChunks; }
 // Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
 // compacted image, its slot table.
@@ -277,7 +285,9 @@ inline long long cluster_fwd_lds(const Plan& p) {
 // Dynamic LDS of the single-workgroup forward: state rows and the KS
 // partials, or the single-row kernel's two partial buffers.
 inline long long fwd_lds(const Plan& p) {
-  const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8;
+  // with the compacted image, the slot table: one int per slot per thread
+  const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8 +
+                         (generic_fwd_cmp(p) ? (long long)p.Hp * p.KS * p.RC * 4 : 0);
   // single-row kernel: two partial buffers and each wave's copy of the state
   const long long row = row_kernels(p) ? 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4 : 0;
   return base > row ? base : row;
