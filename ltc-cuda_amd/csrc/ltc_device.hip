@@ -265,11 +265,19 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
       col -= Hp;
     }
     if (bwd && (segs & kPrepRec) && pp.cB != nullptr && col < Hp) {
+      // The fused chain (bwd == 1) keeps every real synapse (it also forms the
+      // parameter gradients); the unfused one (bwd == 2, folded operands) only
+      // those that add to dL/dv.
       const int i = col;
       compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
         if (i < H && j < H) {
           operand(i, j, v);
-          act = true;
+          if (bwd == 2) {
+            v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
+            act = v.z != 0.f || v.w != 0.f;
+          } else {
+            act = true;
+          }
         }
       });
     }
@@ -788,6 +796,31 @@ __device__ __forceinline__ void bwd_synapse_folded(const float4 p, const float2*
   }
 }
 
+// bwd_synapse_folded for a compacted slot: the NB alpha/beta pairs of its row
+// from the [Hp][NB] float2 layout at byte offset `off`.
+template <int NB>
+__device__ __forceinline__ void bwd_synapse_folded_cmp(const float4 p, const float2* ab, int off,
+                                                       const float* vi, float* acc) {
+  float2 c[NB];
+  const char* at = reinterpret_cast<const char*>(ab) + off;
+  if constexpr (NB % 2 == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; b += 2) {
+      const float4 w = *reinterpret_cast<const float4*>(at + b * 8);
+      c[b] = make_float2(w.x, w.y);
+      c[b + 1] = make_float2(w.z, w.w);
+    }
+  } else {
+    c[0] = *reinterpret_cast<const float2*>(at);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float a = gate(fmaf(p.x, vi[b], p.y));
+    const float a2 = fmaf(-a, a, a);
+    acc[b] = fmaf(fmaf(c[b].x, p.z, c[b].y * p.w), a2, acc[b]);
+  }
+}
+
 // Operands of unfold n for the synapse phase (all rows, column o) and for the
 // rows this thread finishes (1/den, v^k, v^{k+1}).
 template <int NB, int MO>
@@ -825,16 +858,25 @@ __device__ __forceinline__ void bwd_load_gout(const BwdK& k, int t, int b0, int 
 // FUSE (register-resident operands only): each operand also carries its
 // gradient accumulators, which removes the separate parameter-gradient pass
 // and its second gate evaluation.
+// Unfused with register-resident operands (CMP: RCP > 0, !FUSE) the kernel
+// reads the compacted folded image: only synapses with a nonzero weight add
+// to dL/dv (the parameter gradients come from rec_grad_kernel over every
+// synapse). Thread (o, ks) holds the entries ks, ks + KS, ... of column o,
+// alpha/beta sit in LDS as [Hp][NB], and the slot row offsets come from an
+// LDS table [RCP/4][threads] of int4, as in the forward.
 template <int NB, int RCP, bool FUSE>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   static_assert(!FUSE || RCP > 0, "fused gradients need register-resident operands");
   constexpr int MO = ode_owned_rows(NB);
+  constexpr bool CMP = !FUSE && RCP > 0;
   extern __shared__ float4 lds4[];
   const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U;
   const int RC = RCP > 0 ? RCP : k.RC;
-  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp]
+  float2* ab = reinterpret_cast<float2*>(lds4);        // [NB][Hp] ([Hp][NB] with CMP)
   float* red = reinterpret_cast<float*>(ab + NB * Hp);  // [KS][NB][Hp]
-  const int tid = threadIdx.x;
+  int4* slot_tab = reinterpret_cast<int4*>(red + KS * NB * Hp);  // CMP: [RCP/4][threads]
+  auto abat = [&](int b, int col) { return CMP ? col * NB + b : b * Hp + col; };
+  const int tid = threadIdx.x, nthr = blockDim.x;
   const int ks = __builtin_amdgcn_readfirstlane(tid / Hp), o = tid - ks * Hp;
   const __amdgpu_buffer_rsrc_t rsB = image_rsrc(k.recB, (long long)Hp * Hp * 16);
   const int b0 = blockIdx.x * NB;
@@ -843,7 +885,21 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 
   float4 preg[RCP > 0 ? RCP : 1];
   float4 gacc[FUSE ? RCP : 1];
-  if constexpr (RCP > 0) {
+  int nslot = 0;  // CMP: slots the wave runs
+  if constexpr (CMP) {
+    const int cnt = k.ccnt[o];
+    nslot = wave_max(cnt > ks ? (cnt - 1 - ks) / KS + 1 : 0);
+    int ix[RCP];
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(ks * RCP + rr) * Hp + o;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * NB * 8;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
+  } else if constexpr (RCP > 0) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + o];
   }
@@ -901,7 +957,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
             pA[m] += al;
             gdir[m] = al * C;
           }
-          ab[b * Hp + o] = make_float2(al, be);
+          ab[abat(b, o)] = make_float2(al, be);
           if (!FUSE && live) k.absave[(n * B + b0 + b) * Hp + o] = make_float2(al, be);
         }
       }
@@ -913,9 +969,20 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 #pragma unroll
         for (int rr = 0; rr < RCP; ++rr)
           bwd_synapse<NB, true>(preg[rr], ab, Hp, r0 + rr, cvi, acc, gacc[rr]);
-      } else if constexpr (RCP > 0) {
+      } else if constexpr (CMP) {
+        // Wave-uniform slot count: the skipped pairs branch around.
 #pragma unroll
-        for (int rr = 0; rr < RCP; ++rr) bwd_synapse_folded<NB>(preg[rr], ab, Hp, r0 + rr, cvi, acc);
+        for (int q = 0; q < RCP / 4; ++q) {
+          if (4 * q < nslot) {
+            const int4 of = slot_tab[q * nthr + tid];
+            bwd_synapse_folded_cmp<NB>(preg[4 * q], ab, of.x, cvi, acc);
+            bwd_synapse_folded_cmp<NB>(preg[4 * q + 1], ab, of.y, cvi, acc);
+            if (4 * q + 2 < nslot) {
+              bwd_synapse_folded_cmp<NB>(preg[4 * q + 2], ab, of.z, cvi, acc);
+              bwd_synapse_folded_cmp<NB>(preg[4 * q + 3], ab, of.w, cvi, acc);
+            }
+          }
+        }
       } else {
         // Streamed (folded) operands, double-buffered four at a time.
         stream_rows(rsB, o * 16, r0, RC, Hp, [&](const float4 p, int r) {
@@ -2205,11 +2272,20 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
       col -= Hp;
     }
     if (recb && pp.cB != nullptr && col < Hp) {
+      // The fused chain (recb == 1) keeps the synapses whose mask entry is
+      // nonzero; the unfused one (recb == 2, folded operands) those that add
+      // to dL/dv.
       const int i = col;
       compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
-        if (i < H && j < H && lp.mask[(long long)i * H + j] != 0.f) {
-          operand(i, j, v);
-          act = true;
+        if (i < H && j < H) {
+          if (recb == 2) {
+            operand(i, j, v);
+            v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
+            act = v.z != 0.f || v.w != 0.f;
+          } else if (lp.mask[(long long)i * H + j] != 0.f) {
+            operand(i, j, v);
+            act = true;
+          }
         }
       });
     }

@@ -253,9 +253,14 @@ inline bool cmp_fwd(const Plan& p) {
   return (p.CP > 0 && p.Hp == 256 && p.KS == 16 && p.RC == 16) || (row_kernels(p) && p.RC == 16) ||
          generic_fwd_cmp(p);
 }
+// The unfused single-workgroup chain with register-resident operands reads a
+// compacted folded image (only synapses that add to dL/dv).
+inline bool generic_bwd_cmp(const Plan& p) {
+  return p.CP == 0 && !row_kernels(p) && !p.FUSE && (p.RCB == 4 || p.RCB == 8 || p.RCB == 16);
+}
 inline bool cmp_bwd(const Plan& p) {
   return (p.CP > 0 && p.FUSE && p.Hp == 256 && p.JWB == 32 && p.KSB == 16 && p.RCB == 16) ||
-         (row_kernels(p) && p.FUSE && p.RCB == 8);
+         (row_kernels(p) && p.FUSE && p.RCB == 8) || generic_bwd_cmp(p);
 }
 // Module-path backward at Hp = 64 with one row per workgroup, Dp <= 128 and
 // B <= 64: the sensory and LayerNorm backward run inside the chain launch, in
@@ -269,7 +274,9 @@ inline long long row_bwd_words(const Plan& p) { return (long long)p.B * p.T * 12
 inline int cmp_chunks_fwd(const Plan& p) {
   return row_kernels(p) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
 }
-inline int cmp_chunks_bwd(const Plan& p) { return row_kernels(p) ? 8 : kCmpChunks; }
+inline int cmp_chunks_bwd(const Plan& p) {
+  return row_kernels(p) ? 8 : (p.CP > 0 ? kCmpChunks : p.KSB);
+}
 // Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
 // compacted image, its slot table.
 inline long long cluster_bwd_lds(const Plan& p) {
@@ -299,7 +306,9 @@ inline long long fwd_lds(const Plan& p) {
 // through which the recurrent-gradient partials are transposed for coalesced
 // stores.
 inline long long chain_lds(const Plan& p) {
-  long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4;
+  // with the compacted image, the slot table: one int per slot per thread
+  long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4 +
+                   (generic_bwd_cmp(p) ? (long long)p.Hp * p.KSB * p.RCB * 4 : 0);
   // single-row chain: two partial buffers and each wave's copy of alpha/beta
   const long long rowb = 2LL * p.KSB * p.Hp * 4 + (long long)p.KSB * p.Hp * 8;
   if (row_kernels(p) && rowb > base) base = rowb;

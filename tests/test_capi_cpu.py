@@ -216,6 +216,9 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         Hp, NB, KSB = p["Hp"], p["NB"], p["KSB"]
         base = NB * Hp * 8 + KSB * NB * Hp * 4
         assert base <= 65536
+        if not p["fuse"] and p["RCB"] in (4, 8, 16) and not (NB == 1 and Hp == 64):
+            # the unfused chain's compacted image: its slot table
+            base += Hp * KSB * p["RCB"] * 4
         if NB == 1 and Hp == 64:
             # single-row kernels: two partial buffers and every wave's own copy
             # of the row state (forward) or of alpha/beta (chain)
