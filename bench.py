@@ -226,9 +226,12 @@ def syn_counts(c, plan=None, density=(1.0, 1.0)):
     sens = c["B"] * c["T"] * c["D"] * c["H"]
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
     plan = plan or {}
+    # an unfused chain skips synapses for dL/dv only; its rec_grad pass still
+    # evaluates every synapse's parameter sums
+    skip_bwd = plan.get("cmp_bwd") and plan.get("fuse")
     return {"sens": sens,
             "rec_fwd": rec * (rho_r if plan.get("cmp_fwd") else 1.0),
-            "rec_bwd": rec * (rho_r if plan.get("cmp_bwd") else 1.0),
+            "rec_bwd": rec * (rho_r if skip_bwd else 1.0),
             "active": sens * rho_s + rec * rho_r}
 
 
