@@ -93,7 +93,7 @@ def kernel_flops(c, fused_chain, counts=None):
     return {
         "ltc_sens_fwd": 10 * sens,
         "ltc_ode_fwd": 10 * counts["rec_fwd"],
-        "ltc_ode_bwd": (22 if fused_chain else 14) * counts["rec_bwd"],
+        "ltc_ode_bwd": 22 * counts["rec_bwd"] if fused_chain else 14 * counts.get("rec_dv", rec),
         "ltc_rec_grad": 8 * rec,
         "ltc_sens_bwd": 22 * sens,
         "ltc_prep": 0,
@@ -232,6 +232,7 @@ def syn_counts(c, plan=None, density=(1.0, 1.0)):
     return {"sens": sens,
             "rec_fwd": rec * (rho_r if plan.get("cmp_fwd") else 1.0),
             "rec_bwd": rec * (rho_r if skip_bwd else 1.0),
+            "rec_dv": rec * (rho_r if plan.get("cmp_bwd") else 1.0),
             "active": sens * rho_s + rec * rho_r}
 
 
