@@ -187,11 +187,14 @@ def kernel_times(capi, fn, iters):
     return {k: (ms / n, n // iters) for k, (ms, n) in t.items() if n > 0}
 
 
-def roofline(c, ktimes, fused_chain, traffic=None, counts=None):
-    fl = kernel_flops(c, fused_chain, counts)
-    if "ltc_ode_bwd" in ktimes and "ltc_sens_bwd" not in ktimes and "ltc_sens_fwd" in ktimes:
+def roofline(c, ktimes, plan, traffic=None, counts=None):
+    fl = kernel_flops(c, bool(plan["fuse"]), counts)
+    if plan.get("module_row_bwd_fused") and "ltc_sens_bwd" not in ktimes:
         # the fused row backward: the chain launch also runs the sensory backward
         fl["ltc_ode_bwd"] += fl["ltc_sens_bwd"]
+    if plan.get("module_sens_in_prep") and "ltc_sens_fwd" not in ktimes:
+        # the prep launch forms the sensory sums of the module forward
+        fl["ltc_prep"] += fl["ltc_sens_fwd"]
     per_step = {k: avg * per for k, (avg, per) in ktimes.items()}
     dom = max(per_step, key=per_step.get)
     avg_ms = ktimes[dom][0]
@@ -448,7 +451,7 @@ def measure_config(name, c, capi, cpu):
     kt = kernel_times(capi, fn, 2)
     rec["kernels_ms"] = {k: round(v[0], 5) for k, v in kt.items()}
     rec["launches_per_step_library"] = sum(v[1] for v in kt.values())
-    rec["roofline"] = roofline(c, kt, bool(plan["fuse"]), load_traffic(name), counts)
+    rec["roofline"] = roofline(c, kt, plan, load_traffic(name), counts)
     which = "fwdbwd" if train else "fwd"
     ksum = sum(v[0] * v[1] for v in kt.values())
     rec["kernel_ms_sum"] = round(ksum, 4)
@@ -641,7 +644,7 @@ def main():
         "issue_rate": probe,
         "valu_mix_bound_ms": round(mix_bound_ms(c, "fwdbwd", counts), 5),
         "mix_frac_step": round(mix_bound_ms(c, "fwdbwd", counts) / ms, 5),
-        "roofline": roofline(c, kt, bool(plan["fuse"]), load_traffic("C1"), counts),
+        "roofline": roofline(c, kt, plan, load_traffic("C1"), counts),
         "vs_reference_gtx1080_published": round(REF_GTX1080_MS / ms, 3),
     }
     del m, x, target

@@ -299,10 +299,15 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * its parameter gradients are fused), then 1 when the forward and 1 when the
  * chain kernel read compacted images (they then skip the recurrent synapses
  * that cannot contribute: zero weights in the forward, zero mask entries in
- * the module path's chain). Returns the number of values written, or -1 for
- * invalid sizes. The plan depends on the current device's CU count.
+ * the module path's chain), then two module-path fields: 1 when the
+ * forward's parameter-image launch also forms the sensory sums (few rows,
+ * D <= 128, H a multiple of 4, and 16-byte aligned sensory leaves at the
+ * call: no separate sensory launch), and 1 when the backward runs the
+ * sensory and LayerNorm backward inside the chain launch. Returns the number
+ * of values written, or -1 for invalid sizes. The plan depends on the
+ * current device's CU count.
  */
-#define LTC_PLAN_FIELDS 22
+#define LTC_PLAN_FIELDS 24
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

@@ -869,15 +869,22 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   }
   const ltc::LnBuf ln{x, {sxb, sxt, sxd}, lw.xa, lw.stats};
   const ltc::Strides3 xas{(long long)T * D, D, 1};
+  // Few rows: the prep launch forms the sensory sums too (one launch fewer).
+  auto al16 = [](const float* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  const bool sens_in_prep = ltc::prep_sens_fused(p) && al16(sensory_w) && al16(sensory_erev) &&
+                            al16(sensory_mask) && al16(sensory_mu) && al16(sensory_sigma);
   hipError_t e;
   e = timed(ltc::K_PREP, s, [&] {
     return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s, row_words,
-                                 row_words ? ltc::row_bwd_words(p) : 0);
+                                 row_words ? ltc::row_bwd_words(p) : 0,
+                                 sens_in_prep ? wfw.sn : nullptr, sens_in_prep ? wfw.sd : nullptr);
   });
   if (e != hipSuccess) return hip_fail("prep launch", e);
-  e = timed(ltc::K_SENS_FWD, s,
-            [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, pp, wfw.sn, wfw.sd, s); });
-  if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  if (!sens_in_prep) {
+    e = timed(ltc::K_SENS_FWD, s,
+              [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, pp, wfw.sn, wfw.sd, s); });
+    if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  }
   e = timed(ltc::K_ODE_FWD, s, [&] {
     return ltc::launch_ode_fwd(p, pp, wfw.sn, wfw.sd, state, epsilon, out, h_final, vsave,
                                densave, wfw.cb, s);
@@ -1387,7 +1394,8 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,
-      ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0};
+      ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0, ltc::prep_sens_fused(p) ? 1 : 0,
+      ltc::row_bwd_fused(p) ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -35,6 +35,7 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegLn2 = -0.69314718055994531f;
+constexpr float kLn2 = 0.69314718055994531f;
 
 // The device's sticky fault flag: raised when a call's workgroups gave up
 // waiting for each other (a gated fill after a cluster launch, or the fused
@@ -70,9 +71,40 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Sum of v over the wave, in every lane (xor butterfly).
+// Sum of x over the four 16-lane groups of a wave, in every lane. gfx950's
+// v_permlane32_swap / v_permlane16_swap exchange halves and rows of a wave
+// in the VALU: after the two steps every lane holds (x0 + x2) + (x1 + x3)
+// with the same bits.
+__device__ __forceinline__ float group_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Sum of x over the eight 8-lane groups of a wave, in every lane: the two
+// swaps of group_sum4, then DPP row_ror:8, which hands each lane the value
+// of the lane 8 away within its 16-lane row.
+__device__ __forceinline__ float group_sum8(float x) {
+  x = group_sum4(x);
+  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf,
+                                                             0xf, false));
+  return x + y;
+}
+
+// Sum of v over the wave, in every lane with the same bits, without LDS
+// traffic: group_sum4 across the four 16-lane rows, then DPP row_ror by 8,
+// 4, 2 and 1 within each row. Each step is a butterfly (the vector being
+// rotated has period twice the shift), so both lanes of a pair add the
+// same two values.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  v = group_sum4(v);
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x122, 0xf, 0xf, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x121, 0xf, 0xf, false));
   return v;
 }
 
@@ -1166,29 +1198,6 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
   }
 }
 
-// Sum of x over the four 16-lane groups of a wave, in every lane. gfx950's
-// v_permlane32_swap / v_permlane16_swap exchange halves and rows of a wave
-// in the VALU: after the two steps every lane holds (x0 + x2) + (x1 + x3)
-// with the same bits.
-__device__ __forceinline__ float group_sum4(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
-// Sum of x over the eight 8-lane groups of a wave, in every lane: the two
-// swaps of group_sum4, then DPP row_ror:8, which hands each lane the value
-// of the lane 8 away within its 16-lane row.
-__device__ __forceinline__ float group_sum8(float x) {
-  x = group_sum4(x);
-  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf,
-                                                             0xf, false));
-  return x + y;
-}
-
 // Single-row forward at Hp = 64 with wave-owned columns: 4 waves, wave w owns
 // the 16 output columns j = 16w + (lane & 15), and the lane's row group
 // g = lane >> 4 holds the compacted entries g, g + 4, ... of column j (the
@@ -2223,7 +2232,19 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 
 // torch's softplus (beta 1, threshold 20) and its derivative z/(z+1), z = e^x.
-__device__ __forceinline__ float softplus_t(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+// softplus(x) = max(x, 0) + log(1 + y), y = e^-|x| in (0, 1], with log(1 + y)
+// formed from the hardware exp2/log2 as log(u) * (y / (u - 1)), u = fl(1 + y),
+// which corrects for the rounding of 1 + y (Goldberg, "What every computer
+// scientist should know about floating-point arithmetic", 1991, Theorem 4):
+// a few ulp, branch-free, in about 13 instructions where log1pf(expf(x))
+// takes about 150. Above 20 the second term is below half an ulp of x, so
+// the result is x, as with torch's threshold; NaN stays NaN.
+__device__ __forceinline__ float softplus_t(float x) {
+  const float y = __builtin_amdgcn_exp2f(-fabsf(x) * kLog2e);
+  const float u = 1.0f + y;
+  const float l = (__builtin_amdgcn_logf(u) * kLn2) * (y * __builtin_amdgcn_rcpf(u - 1.0f));
+  return fmaxf(x, 0.f) + (u == 1.0f ? y : l);
+}
 __device__ __forceinline__ float softplus_grad(float x) {
   if (x > 20.f) return 1.f;
   const float z = expf(x);
@@ -2232,26 +2253,199 @@ __device__ __forceinline__ float softplus_grad(float x) {
 
 
 
+// One (b,t) row's LayerNorm + affine (the row blocks of prep_leaf_kernel):
+// the row in registers, CPL values per lane, two-pass mean/variance,
+// xa = ((x - mean)*rstd*ln_w + ln_b)*input_w + input_b. load() issues the
+// row's and the four per-column vectors' loads together (one memory round
+// trip precedes the two reductions); finish() leaves every lane of the wave
+// with the row statistics and its xa values (xo; 0 past D).
+template <int CPL>
+struct LnRow {
+  float xv[CPL], lw[CPL], lb[CPL], iw[CPL], ib[CPL];
+  __device__ __forceinline__ void load(const LeafParams& lp, const LnBuf& ln, int row, int D,
+                                       int T) {
+    const int lane = threadIdx.x & 63;
+    const int b = row / T, t = row - b * T;
+    const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int d = lane + 64 * c;
+      const bool in = d < D;
+      xv[c] = in ? xr[d * ln.xs.c] : 0.f;
+      lw[c] = in ? lp.ln_w[d] : 0.f;
+      lb[c] = in ? lp.ln_b[d] : 0.f;
+      iw[c] = in ? lp.input_w[d] : 0.f;
+      ib[c] = in ? lp.input_b[d] : 0.f;
+    }
+  }
+  __device__ __forceinline__ void finish(const LeafParams& lp, int D, float (&xo)[CPL],
+                                         float& mean, float& rstd) {
+    const int lane = threadIdx.x & 63;
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) sum += xv[c];
+    mean = wave_sum(sum) / (float)D;
+    float sq = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int d = lane + 64 * c;
+      const float dv = d < D ? xv[c] - mean : 0.f;
+      sq = fmaf(dv, dv, sq);
+    }
+    rstd = 1.0f / sqrtf(wave_sum(sq) / (float)D + lp.ln_eps);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const float xn = (xv[c] - mean) * rstd * lw[c] + lb[c];
+      xo[c] = lane + 64 * c < D ? xn * iw[c] + ib[c] : 0.f;
+    }
+  }
+};
+
+template <int CPL>
+__device__ __forceinline__ void ln_row(const LeafParams& lp, const LnBuf& ln, int row, int D,
+                                       int T, float (&xo)[CPL], float& mean, float& rstd) {
+  LnRow<CPL> r;
+  r.load(lp, ln, row, D, T);
+  r.finish(lp, D, xo, mean, rstd);
+}
+
+// Threads per block of the prep launch when it forms the sensory sums.
+constexpr int kPrepSensThreads = 512;
+
+// The sensory sums of one (b,t) row for neurons [64*hb, 64*hb + 64), inside
+// the prep launch (prep_sens_fused), one 512-thread block per (row, 64
+// neurons). Lane -> four neurons h..h+3, h = 64*hb + 4*(lane & 15); input
+// group g = 4*w + (lane >> 4) of wave w (32 groups) -> inputs d = g + 32*i.
+// The five sensory leaves are read as 16-byte rows of four neurons (H % 4 ==
+// 0 and 16-byte aligned leaves, checked by the caller): 10*CPL loads per
+// thread, all in flight at once, and each synapse's operands are formed
+// from them (zero past D or H). Each wave normalises the whole row itself
+// (LnRow) and reads its inputs' xa from its own copy in LDS. The 32
+// groups' sums meet in a fixed order: the four lane groups (group_sum4),
+// then the waves in LDS. The blocks with hb == 0 save
+// xa and the row statistics for the backward, after the sums (stores count
+// against the load counter, so storing earlier would delay the barrier).
+template <int CPL>
+__device__ __forceinline__ void ln_sens_row(const LeafParams& lp, const LnBuf& ln, int row,
+                                            int hb, int H, int D, int Hp, int T, float* sn,
+                                            float* sd) {
+  constexpr int NW = kPrepSensThreads / 64;
+  __shared__ float4 part[NW - 1][2][16];
+  __shared__ __align__(16) float xs[NW][64 * CPL];
+  constexpr int NI = 2 * CPL;  // inputs per thread
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int h = hb * 64 + 4 * (lane & 15);
+  const int g = 4 * w + (lane >> 4);
+  const bool hok = h < H;  // H % 4 == 0: all four neurons or none
+  // The row's loads first, then the operands' (clamped to element 0,
+  // selected afterwards) in the order of use: the load counter is in order,
+  // so the LayerNorm waits only for the row, and each input's synapses only
+  // for their own operands, while the rest stream in.
+  // (Scheduling barriers keep the compiler from moving the row's loads
+  // behind the operands', the LayerNorm ahead of the operand loads, or
+  // operand arithmetic into the LayerNorm, where it would wait for them.)
+  LnRow<CPL> lr;
+  lr.load(lp, ln, row, D, T);
+  __builtin_amdgcn_sched_barrier(0);
+  float4 lsw[NI], lsm[NI], lse[NI], lsu[NI], lss[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int d = g + 4 * NW * i;
+    const long long e = (d < D && hok) ? (long long)d * H + h : 0;
+    lsw[i] = *reinterpret_cast<const float4*>(lp.s_w + e);
+    lsm[i] = *reinterpret_cast<const float4*>(lp.s_mask + e);
+    lse[i] = *reinterpret_cast<const float4*>(lp.s_erev + e);
+    lsu[i] = *reinterpret_cast<const float4*>(lp.s_mu + e);
+    lss[i] = *reinterpret_cast<const float4*>(lp.s_sigma + e);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float xo[CPL], mean, rstd;
+  lr.finish(lp, D, xo, mean, rstd);
+  __builtin_amdgcn_sched_barrier(0);
+  // Each wave reads only its own copy of the row: an in-wave LDS round trip,
+  // ordered by fences at wave scope, with no workgroup barrier.
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) xs[w][64 * c + lane] = xo[c];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float an[4] = {0.f, 0.f, 0.f, 0.f}, ad[4] = {0.f, 0.f, 0.f, 0.f};
+  // One synapse: w_pos = softplus(w) * mask (the mask zeroed past D or H,
+  // where the clamped loads hold element 0's finite values, so the synapse
+  // adds exact zeros), gate argument sigma*log2(e)*(mu - xa), and the sums
+  // n += (a*w_pos)*erev, d += a*w_pos.
+  auto syn = [&](int j, float sw, float sm, float se, float su, float ss, float xa) {
+    const float t = gate((su - xa) * (ss * kLog2e)) * (softplus_t(sw) * sm);
+    an[j] = fmaf(t, se, an[j]);
+    ad[j] += t;
+  };
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int d = g + 4 * NW * i;  // < 64 * CPL
+    const bool ok = d < D && hok;
+    const float xa = xs[w][d];
+    const float4 m = lsm[i];
+    syn(0, lsw[i].x, ok ? m.x : 0.f, lse[i].x, lsu[i].x, lss[i].x, xa);
+    syn(1, lsw[i].y, ok ? m.y : 0.f, lse[i].y, lsu[i].y, lss[i].y, xa);
+    syn(2, lsw[i].z, ok ? m.z : 0.f, lse[i].z, lsu[i].z, lss[i].z, xa);
+    syn(3, lsw[i].w, ok ? m.w : 0.f, lse[i].w, lsu[i].w, lss[i].w, xa);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    an[j] = group_sum4(an[j]);
+    ad[j] = group_sum4(ad[j]);
+  }
+  if (w > 0 && lane < 16) {
+    part[w - 1][0][lane] = make_float4(an[0], an[1], an[2], an[3]);
+    part[w - 1][1][lane] = make_float4(ad[0], ad[1], ad[2], ad[3]);
+  }
+  __syncthreads();
+  if (w > 0) return;
+  if (lane < 16) {
+    float4 tn = make_float4(an[0], an[1], an[2], an[3]);
+    float4 td = make_float4(ad[0], ad[1], ad[2], ad[3]);
+#pragma unroll
+    for (int q = 0; q < NW - 1; ++q) {
+      const float4 vn = part[q][0][lane], vd = part[q][1][lane];
+      tn = make_float4(tn.x + vn.x, tn.y + vn.y, tn.z + vn.z, tn.w + vn.w);
+      td = make_float4(td.x + vd.x, td.y + vd.y, td.z + vd.z, td.w + vd.w);
+    }
+    *reinterpret_cast<float4*>(sn + (long long)row * Hp + h) = tn;
+    *reinterpret_cast<float4*>(sd + (long long)row * Hp + h) = td;
+  }
+  if (hb == 0) {
+    float* xrow = ln.xa + (long long)row * D;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      if (lane + 64 * c < D) xrow[lane + 64 * c] = xo[c];
+    if (lane == 0) {
+      ln.stats[2LL * row] = mean;
+      ln.stats[2LL * row + 1] = rstd;
+    }
+  }
+}
+
 // Parameter images from the leaves (same flat segments as prep_kernel), plus
-// LayerNorm + affine of the (b,t) rows in trailing blocks of the same launch:
-// one wave per row, the row held in registers (D <= kModuleMaxD), two-pass
-// mean/variance, xa = ((x - mean)*rstd*ln_w + ln_b)*input_w + input_b.
+// LayerNorm + affine of the (b,t) rows in trailing blocks of the same launch
+// (ln_row; D <= kModuleMaxD), one wave per row, or with FS one block per
+// (row, 64 neurons) that also forms the row's sensory sums (ln_sens_row).
 // recb: 0 no chain image, 1 plain {S', c', WE, WP} (fused chain), 2 folded
 // {S', c', S'*WE, S'*WP}; sensf / sensb: write the forward / backward
 // sensory image. recF and the neuron vector are always written.
 // CPL: row values each lane keeps (D <= 64 * CPL <= kModuleMaxD).
-template <int CPL>
-__global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
+template <int CPL, bool FS>
+__global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(LeafParams lp, Prepped pp, int H, int D,
                                                         int Hp, int Dp, int recb, int sensf,
                                                         int sensb, int nprep_blocks, int ncmp_blocks,
                                                         int nchf, int nchb, LnBuf ln, int T,
                                                         int BT, unsigned long long* clr,
-                                                        long long nclr) {
+                                                        long long nclr, float* sn, float* sd) {
   if ((int)blockIdx.x >= nprep_blocks && (int)blockIdx.x < nprep_blocks + ncmp_blocks) {
     // Compacted columns, one per wave: forward (synapses whose w_pos or w_erev
     // is nonzero), then chain (synapses whose mask entry is nonzero).
     const int lane = threadIdx.x & 63;
-    int col = ((int)blockIdx.x - nprep_blocks) * 4 + (int)(threadIdx.x >> 6);
+    int col = ((int)blockIdx.x - nprep_blocks) * (int)(blockDim.x >> 6) + (int)(threadIdx.x >> 6);
     auto operand = [&](int i, int j, float4& v) {
       const long long e = (long long)i * H + j;
       const float S = lp.sigma[e], M = lp.mu[e];
@@ -2293,43 +2487,20 @@ __global__ __launch_bounds__(256) void prep_leaf_kernel(LeafParams lp, Prepped p
   }
   if ((int)blockIdx.x >= nprep_blocks) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int row = ((int)blockIdx.x - nprep_blocks - ncmp_blocks) * 4 + w;
+    const int blk = (int)blockIdx.x - nprep_blocks - ncmp_blocks;
+    if constexpr (FS) {
+      const int hbn = Hp / 64;
+      ln_sens_row<CPL>(lp, ln, blk / hbn, blk - (blk / hbn) * hbn, H, D, Hp, T, sn, sd);
+      return;
+    }
+    const int row = blk * 4 + w;
     if (row >= BT) return;
-    const int b = row / T, t = row - b * T;
-    const float* xr = ln.x + b * ln.xs.b + t * ln.xs.t;
-    // The row and the four per-column vectors load together, so one memory
-    // round trip precedes the two reductions.
-    float xv[CPL], lw[CPL], lb[CPL], iw[CPL], ib[CPL];
-    float sum = 0.f;
+    float xo[CPL], mean, rstd;
+    ln_row<CPL>(lp, ln, row, D, T, xo, mean, rstd);
+    float* xrow = ln.xa + (long long)row * D;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int d = lane + 64 * c;
-      const bool in = d < D;
-      xv[c] = in ? xr[d * ln.xs.c] : 0.f;
-      lw[c] = in ? lp.ln_w[d] : 0.f;
-      lb[c] = in ? lp.ln_b[d] : 0.f;
-      iw[c] = in ? lp.input_w[d] : 0.f;
-      ib[c] = in ? lp.input_b[d] : 0.f;
-      sum += xv[c];
-    }
-    const float mean = wave_sum(sum) / (float)D;
-    float sq = 0.f;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int d = lane + 64 * c;
-      const float dv = d < D ? xv[c] - mean : 0.f;
-      sq = fmaf(dv, dv, sq);
-    }
-    const float rstd = 1.0f / sqrtf(wave_sum(sq) / (float)D + lp.ln_eps);
-    float* xo = ln.xa + (long long)row * D;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int d = lane + 64 * c;
-      if (d < D) {
-        const float xn = (xv[c] - mean) * rstd * lw[c] + lb[c];
-        xo[d] = xn * iw[c] + ib[c];
-      }
-    }
+    for (int c = 0; c < CPL; ++c)
+      if (lane + 64 * c < D) xrow[lane + 64 * c] = xo[c];
     if (lane == 0) {
       ln.stats[2LL * row] = mean;
       ln.stats[2LL * row + 1] = rstd;
@@ -3564,13 +3735,9 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
   const int BT = p.B * p.T;
   const int hb = p.Hp / 64;
   const dim3 block(256);
-  // Many rows: 4 row groups per workgroup sharing operands through L1.
-  // Few rows: split D over the waves instead, so each thread's chain of
-  // dependent operand loads is 4x shorter.
-  const bool split_d = (long long)hb * ((BT + 3) / 4) < 512;
-  int rpw = 8;
-  const int rows_of = split_d ? 1 : 4;
-  while (rpw > 1 && (long long)hb * ((BT + rows_of * rpw - 1) / (rows_of * rpw)) < 1024) rpw >>= 1;
+  const SensGeom geo = sens_fwd_geom(p);
+  const bool split_d = geo.split_d;
+  const int rpw = geo.rpw, rows_of = split_d ? 1 : 4;
   const dim3 grid(hb, (BT + rows_of * rpw - 1) / (rows_of * rpw));
 #define LTC_SENS(R, DSV) hipLaunchKernelGGL((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd)
   if (split_d) {
@@ -3758,26 +3925,35 @@ hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpar
 
 hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
                             const LnBuf* ln, hipStream_t s, unsigned long long* clear_words,
-                            long long nclear) {
+                            long long nclear, float* sn, float* sd) {
   if (clear_words == nullptr) nclear = 0;
+  const bool fs = sn != nullptr;
+  if (fs && (ln == nullptr || sd == nullptr || !prep_sens_fused(p))) return hipErrorInvalidValue;
+  const int threads = fs ? kPrepSensThreads : 256;
   const long long total =
       (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp + nclear;
-  const int nprep = (int)((total + 255) / 256);
+  const int nprep = (int)((total + threads - 1) / threads);
   const int BT = p.B * p.T;
-  const int nln = ln ? (BT + 3) / 4 : 0;
+  const int nln = ln ? (fs ? BT * (p.Hp / 64) : (BT + 3) / 4) : 0;
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   const bool bwd = (images & kLeafBwdImages) != 0;
-  const int ncmp = (cmp_columns(pp, p.Hp, true, bwd) + 3) / 4;
-#define LTC_PREPL(C)                                                                           \
-  hipLaunchKernelGGL((prep_leaf_kernel<C>), dim3(nprep + ncmp + nln), dim3(256), 0, s, lp, pp, \
-                     p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0,                          \
-                     (images & kLeafFwdImages) ? 1 : 0, bwd ? 1 : 0, nprep, ncmp,          \
-                     cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT, clear_words, nclear)
-  if (nln == 0 || p.D <= 64) LTC_PREPL(1);
-  else if (p.D <= 128) LTC_PREPL(2);
-  else if (p.D <= 256) LTC_PREPL(4);
-  else if (p.D <= 512) LTC_PREPL(8);
-  else LTC_PREPL(16);
+  const int wpb = threads / 64;  // compacted columns per block, one per wave
+  const int ncmp = (cmp_columns(pp, p.Hp, true, bwd) + wpb - 1) / wpb;
+  // With the sensory sums formed in the row blocks, nothing reads sensF.
+  const int sensf = (images & kLeafFwdImages) && !fs ? 1 : 0;
+#define LTC_PREPL(C, F)                                                                           \
+  hipLaunchKernelGGL((prep_leaf_kernel<C, F>), dim3(nprep + ncmp + nln), dim3(threads), 0, s, lp, pp, \
+                     p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, sensf, bwd ? 1 : 0, nprep, \
+                     ncmp, cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT, clear_words,       \
+                     nclear, sn, sd)
+  if (fs) {
+    if (p.D <= 64) LTC_PREPL(1, true);
+    else LTC_PREPL(2, true);
+  } else if (nln == 0 || p.D <= 64) LTC_PREPL(1, false);
+  else if (p.D <= 128) LTC_PREPL(2, false);
+  else if (p.D <= 256) LTC_PREPL(4, false);
+  else if (p.D <= 512) LTC_PREPL(8, false);
+  else LTC_PREPL(16, false);
 #undef LTC_PREPL
   return hipGetLastError();
 }

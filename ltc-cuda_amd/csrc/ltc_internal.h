@@ -174,11 +174,41 @@ hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long
 // (sensF) and backward (recB, sensB) images; recF and neuron are always built.
 constexpr int kLeafFwdImages = 1;
 constexpr int kLeafBwdImages = 2;
+// With sn != nullptr (only when prep_sens_fused(p)), the row blocks also
+// compute every row's sensory sums into sn / sd, forming the sensory operands
+// from the leaves, and the separate sensory launch is skipped.
 hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& pp, int images,
                             const LnBuf* ln, hipStream_t s, unsigned long long* clear_words = nullptr,
-                            long long nclear = 0);
+                            long long nclear = 0, float* sn = nullptr, float* sd = nullptr);
 hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            float* sn, float* sd, hipStream_t s);
+// Geometry of the sensory forward launch: rows per wave, and whether the
+// four waves split D (few rows) instead of taking a row group each.
+struct SensGeom {
+  int rpw;
+  bool split_d;
+};
+inline SensGeom sens_fwd_geom(const Plan& p) {
+  const long long BT = (long long)p.B * p.T, hb = p.Hp / 64;
+  // Many rows: 4 row groups per workgroup sharing operands through L1.
+  // Few rows: split D over the waves instead, so each thread's chain of
+  // dependent operand loads is 4x shorter.
+  const bool split_d = hb * ((BT + 3) / 4) < 512;
+  const int rows_of = split_d ? 1 : 4;
+  int rpw = 8;
+  while (rpw > 1 && hb * ((BT + rows_of * rpw - 1) / (rows_of * rpw)) < 1024) rpw >>= 1;
+  return {rpw, split_d};
+}
+// The module forward's sensory sums inside the prep launch: when a block
+// per (row, 64 neurons) fits the chip at once (at most 256 of them) and a
+// row fits two 64-input chunks, such blocks of the prep launch normalise
+// their row and form its sums themselves, which saves a dependent launch.
+// They read the sensory leaves as 16-byte rows of four neurons, so H % 4 == 0
+// here and the caller also checks that the five sensory leaves are 16-byte
+// aligned.
+inline bool prep_sens_fused(const Plan& p) {
+  return (long long)p.B * p.T * (p.Hp / 64) <= 256 && p.D >= 1 && p.D <= 128 && p.H % 4 == 0;
+}
 // Cluster path scratch: exchange words and a status word (nonzero after a
 // cluster member gave up waiting for its partners), plus the wait budget of
 // every exchange in ticks of the 100 MHz wall clock (<= 0: a member gives up

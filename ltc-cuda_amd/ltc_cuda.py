@@ -74,7 +74,7 @@ class CApi:
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
                    "threads_bwd", "CP", "NCL", "CPB", "NBB", "ode_workgroups_bwd",
-                   "cmp_fwd", "cmp_bwd")
+                   "cmp_fwd", "cmp_bwd", "module_sens_in_prep", "module_row_bwd_fused")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path
@@ -829,7 +829,11 @@ class CapturedStep:
     * the captured gradients are then installed as the parameters' `.grad`,
       and every replay rewrites them in place. Zeroing or replacing `.grad`
       between replays detaches them from the graph; `install_grads()` puts
-      them back.
+      them back;
+    * a scalar loss's seed gradient (the 1 that `loss.backward()` starts
+      from) is a tensor made once before capture, so the graph holds no fill
+      kernel for it; a non-scalar loss is seeded with ones of its shape, as
+      `loss.backward(torch.ones_like(loss))` would be.
 
     `inputs` are static: copy new data into them (`step.inputs[0].copy_(x)`)
     before `replay()`. `outputs` and `loss` are detached views of the graph's
@@ -842,17 +846,22 @@ class CapturedStep:
         self.params = [p for p in module.parameters() if p.requires_grad]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
+        seed = None
         with torch.cuda.stream(side):
             for _ in range(max(1, int(warmup))):
                 loss = loss_fn(module(*self.inputs))
-                torch.autograd.grad(loss, self.params, allow_unused=True)
+                if seed is None:
+                    seed = torch.ones_like(loss)
+                torch.autograd.grad(loss, self.params, grad_outputs=seed, allow_unused=True)
                 del loss
         torch.cuda.current_stream().wait_stream(side)
+        self._seed = seed
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             out = module(*self.inputs)
             loss = loss_fn(out)
-            grads = torch.autograd.grad(loss, self.params, allow_unused=True)
+            grads = torch.autograd.grad(loss, self.params, grad_outputs=self._seed,
+                                        allow_unused=True)
             # a parameter the loss does not reach gets zeros, as backward() leaves none
             grads = [torch.zeros_like(p) if g is None else g for p, g in zip(self.params, grads)]
         self.outputs = _detach_tree(out)
