@@ -31,6 +31,9 @@ FWD_SHAPES = [
     (1100, 2, 8, 24), (2100, 1, 4, 8), (4100, 1, 4, 8),
     (600, 2, 8, 150),  # two rows per workgroup, operands streamed in groups of four rows
     (2100, 1, 128, 8),  # row-group sensory form over two full input chunks
+    # two and four rows per workgroup at Hp = 64 with the compacted image,
+    # rows past B in the last workgroup and columns past H
+    (1001, 3, 20, 64), (2050, 2, 16, 60), (4097, 2, 8, 33),
 ]
 
 
@@ -52,6 +55,7 @@ BWD_SHAPES = [
     (32, 16, 128, 128),  # C2 at full size
     (24, 8, 128, 64), (8, 4, 32, 128), (2, 2, 16, 192), (2, 2, 8, 256), (1, 2, 8, 512),
     (520, 2, 8, 16), (1030, 1, 4, 8), (4100, 1, 4, 8), (1, 1, 1, 1),
+    (1001, 2, 8, 60), (2050, 1, 8, 64),  # 2 and 4 rows per workgroup, rows past B
 ]
 
 
