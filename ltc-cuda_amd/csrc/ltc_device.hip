@@ -1214,28 +1214,52 @@ template <int NS>
 __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&preg)[16],
                                                   const int (&ix)[16], float* vsh, int j, bool lead,
                                                   bool col, float v) {
-  constexpr int HP = 64;
+  constexpr int HP = 64, TS = kRowSensSteps;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int b0 = blockIdx.x;
   const float C = k.neuron[j], G = k.neuron[HP + j], L = k.neuron[2 * HP + j];
   const float GL = G * L, CG = C + G;
-  float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
-  auto load_sens = [&](int t, float& a, float& d) {
-    const long long e = ((long long)b0 * T + t) * HP + j;
-    a = k.sn[e];
-    d = k.sd[e];
+  // The row's sensory sums go through LDS, TS steps at a time: loaded into
+  // registers a step ahead, their wait would be a vmcnt(0) at every step
+  // boundary (the compiler cannot count the stores issued since across the
+  // loop), which also waits for every vsave/densave/out store in flight.
+  float* ssh = vsh + 2 * HP;  // [2][TS][64]: sn, sd of the staged steps
+  // All of a thread's loads are issued before any of them is waited for.
+  auto stage = [&](int t0) {
+    constexpr int PER = 2 * TS * HP / 256;
+    const int n = min(T - t0, TS) * HP;
+    const long long base = ((long long)b0 * T + t0) * HP;
+    float tmp[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int r = (int)threadIdx.x + 256 * (i % (PER / 2));
+      tmp[i] = r < n ? (i < PER / 2 ? k.sn : k.sd)[base + r] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) ssh[(int)threadIdx.x + 256 * i] = tmp[i];
   };
-  if (T > 0) load_sens(0, snr, sdr);
-  // One wait for the operands and the first step's sums, before the loop
+  if (T > 0) stage(0);
+  // One wait for the operands and the first staged steps, before the loop
   // (see ode_fwd_row_kernel).
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();
+  float snr = 0.f, sdr = 0.f;
   int t = 0, u = 0;
   // One unfold reading state buffer P (compile-time, so the per-lane row
   // offsets are the whole LDS address) and writing buffer P ^ 1.
   auto unfold = [&](auto pc) {
     constexpr int P = decltype(pc)::value;
-    if (u == 0 && t + 1 < T) load_sens(t + 1, snn, sdn);
+    if (u == 0) {
+      const int ts = t % TS;
+      if (ts == 0 && t > 0) {
+        // every wave read the previous block's last step U unfolds ago
+        stage(t);
+        __builtin_amdgcn_s_waitcnt(0);
+        lds_barrier();
+      }
+      snr = ssh[ts * HP + j];
+      sdr = ssh[(TS + ts) * HP + j];
+    }
     const char* vr = reinterpret_cast<const char*>(vsh + P * HP);
     // Gates in phases (states, arguments, exponentials, reciprocals); the
     // sums keep their order.
@@ -1274,8 +1298,6 @@ __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&
     if (++u == U) {
       u = 0;
       ++t;
-      snr = snn;
-      sdr = sdn;
     }
   };
   const long long N = (long long)T * U;
@@ -1497,39 +1519,82 @@ template <int NS, bool FULL>
 __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&preg)[8],
                                                   const int (&jx)[8], float4 (&gacc)[8],
                                                   float2* abs_, int i, bool lead) {
-  constexpr int HP = 64;
+  constexpr int HP = 64, SU = kRowChainUnfolds;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int b0 = blockIdx.x;
   const bool col = FULL || i < H;
   const float C = k.neuron[i];
   float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + i] : 0.f;
   float pC = 0.f, pGv = 0.f, pA = 0.f;
-  const long long BHp = (long long)B * HP;
-  // Saved pre-state v^k (also v_i of the synapses), 1/den and v^{k+1} of
-  // column i for unfold n, software-pipelined one unfold ahead.
-  auto load = [&](long long n, float& vk, float& rd, float& vk1) {
-    const long long e = (n * B + b0) * HP + i;
-    vk = k.vsave[e];
-    rd = col ? k.densave[e] : 1.f;
-    vk1 = k.vsave[e + BHp];
+  // The row's saved pre-states v^k (also v_i of the synapses), 1/den and
+  // dL/dout go through LDS, SU unfolds at a time, so the loop issues no
+  // global load: waiting for one loaded a step ahead would be a vmcnt(0) (the
+  // compiler cannot count the word stores issued since), which also waits
+  // for every store in flight.
+  float* vst = reinterpret_cast<float*>(abs_ + 2 * HP);  // [SU + 1][64] v^n, n = n_lo...
+  float* rst = vst + (SU + 1) * HP;                     // [SU][64] 1/den
+  float* gst = rst + SU * HP;                           // [SU][64] dL/dout, steps t_lo...
+  long long n_lo = 0;
+  int t_lo = 0;
+  // Stages the block of unfolds ending at nhi: each wave copies whole 64-float
+  // rows (wave-uniform kinds) with direct global-to-LDS loads, which hold no
+  // registers; columns past H get 1/den = 1 and dL/dout = 0 by LDS stores.
+  // The 8 waves of the chain take rows w, w + 8, ...
+  auto stage = [&](long long nhi) {
+    n_lo = nhi - SU + 1 > 0 ? nhi - SU + 1 : 0;
+    t_lo = (int)(n_lo / U);
+    const int nu = (int)(nhi - n_lo + 1), nt = (int)(nhi / U) - t_lo + 1;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), c = threadIdx.x & 63;
+    const bool cl = FULL || c < H;
+    for (int r = w; r <= 2 * nu + nt; r += 8) {
+      const float* src;
+      float* dst;
+      bool ld = true;
+      float fill = 0.f;
+      if (r <= nu) {
+        src = k.vsave + ((n_lo + r) * B + b0) * HP + c;
+        dst = vst + r * HP;
+      } else if (r <= 2 * nu) {
+        const int rr = r - nu - 1;
+        src = k.densave + ((n_lo + rr) * B + b0) * HP + c;
+        dst = rst + rr * HP;
+        ld = cl;
+        fill = 1.f;
+      } else {
+        const int tt = r - 2 * nu - 1;
+        src = k.gout + (long long)b0 * k.gs.b + (long long)(t_lo + tt) * k.gs.t +
+              (long long)c * k.gs.c;
+        dst = gst + tt * HP;
+        ld = cl;
+      }
+      if (ld)
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+      else
+        dst[c] = fill;
+    }
   };
-  auto gout = [&](int t) {
-    return col ? k.gout[(long long)b0 * k.gs.b + (long long)t * k.gs.t + (long long)i * k.gs.c]
-               : 0.f;
-  };
-  float cvk, crd, cvk1, nvk = 0.f, nrd = 1.f, nvk1 = 0.f;
-  load((long long)T * U - 1, cvk, crd, cvk1);
-  float gcur = gout(T - 1), gnext = 0.f, accA = 0.f, accB = 0.f;
+  stage((long long)T * U - 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  float accA = 0.f, accB = 0.f;
   int t = T - 1, u = U - 1;
   auto unfold = [&](auto pc) {
     constexpr int P = decltype(pc)::value;
     const long long n = (long long)t * U + u;
-    if (u == U - 1) {
-      if (t > 0) gnext = gout(t - 1);
-      accA = accB = 0.f;
-      g += gcur;
+    if (n < n_lo) {
+      // every wave read the previous block's rows before this unfold's barrier
+      stage(n);
+      __builtin_amdgcn_s_waitcnt(0);
+      lds_barrier();
     }
-    if (n > 0) load(n - 1, nvk, nrd, nvk1);
+    const int nr = (int)(n - n_lo);
+    const float cvk = vst[nr * HP + i], cvk1 = vst[(nr + 1) * HP + i];
+    const float crd = rst[nr * HP + i];
+    if (u == U - 1) {
+      accA = accB = 0.f;
+      g += gst[(t - t_lo) * HP + i];
+    }
     float al = 0.f, be = 0.f;
     if (col) {
       al = g * crd;  // saved 1/den
@@ -1573,11 +1638,6 @@ __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&
     }
     const float sum = group_sum8(acc);
     g = col ? fmaf(kNegLn2, sum, gdir) : 0.f;
-    if (n > 0) {
-      cvk = nvk;
-      crd = nrd;
-      cvk1 = nvk1;
-    }
     if (u == 0) {
       if (lead) {
         const long long e = ((long long)b0 * T + t) * HP + i;
@@ -1589,7 +1649,6 @@ __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&
           k.dsd[e] = accB;
         }
       }
-      gcur = gnext;
       --t;
       u = U - 1;
     } else {

@@ -321,12 +321,23 @@ inline long long cluster_fwd_lds(const Plan& p) {
 }
 // Dynamic LDS of the single-workgroup forward: state rows and the KS
 // partials, or the single-row kernel's two partial buffers.
+// Steps of sensory sums the single-row forward stages in LDS at a time, and
+// unfolds of saved states the single-row chain stages.
+constexpr int kRowSensSteps = 32;
+constexpr int kRowChainUnfolds = 48;
 inline long long fwd_lds(const Plan& p) {
   // with the compacted image, the slot table: one int per slot per thread
   const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8 +
                          (generic_fwd_cmp(p) ? (long long)p.Hp * p.KS * p.RC * 4 : 0);
-  // single-row kernel: two partial buffers and each wave's copy of the state
-  const long long row = row_kernels(p) ? 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4 : 0;
+  // single-row kernels: two partial buffers and each wave's copy of the state,
+  // or (wave-owned form, RC = 16) the double-buffered state and the staged
+  // sensory sums
+  long long row = 0;
+  if (row_kernels(p)) {
+    row = 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4;
+    const long long wave = 2LL * p.Hp * 4 + 2LL * kRowSensSteps * p.Hp * 4;
+    if (p.RC == 16 && wave > row) row = wave;
+  }
   return base > row ? base : row;
 }
 
@@ -339,8 +350,12 @@ inline long long chain_lds(const Plan& p) {
   // with the compacted image, the slot table: one int per slot per thread
   long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4 +
                    (generic_bwd_cmp(p) ? (long long)p.Hp * p.KSB * p.RCB * 4 : 0);
-  // single-row chain: two partial buffers and each wave's copy of alpha/beta
-  const long long rowb = 2LL * p.KSB * p.Hp * 4 + (long long)p.KSB * p.Hp * 8;
+  // single-row chain: two partial buffers and each wave's copy of alpha/beta;
+  // the wave-owned form (FUSE, RCB = 8) alpha/beta by parity and the staged
+  // v^k, 1/den and dL/dout rows
+  long long rowb = 2LL * p.KSB * p.Hp * 4 + (long long)p.KSB * p.Hp * 8;
+  const long long waveb = 2LL * p.Hp * 8 + (3LL * kRowChainUnfolds + 1) * p.Hp * 4;
+  if (p.FUSE && p.RCB == 8 && waveb > rowb) rowb = waveb;
   if (row_kernels(p) && rowb > base) base = rowb;
   const long long plane =
       p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;

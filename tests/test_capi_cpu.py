@@ -221,10 +221,18 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
             base += Hp * KSB * p["RCB"] * 4
         if NB == 1 and Hp == 64:
             # single-row kernels: two partial buffers and every wave's own copy
-            # of the row state (forward) or of alpha/beta (chain)
-            base = max(base, 2 * KSB * Hp * 4 + KSB * Hp * 8)
-            assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8,
-                                       2 * p["KS"] * Hp * 8 + p["KS"] * Hp * 4)
+            # of the row state (forward) or of alpha/beta (chain); the
+            # wave-owned forms (forward RC = 16, fused chain RCB = 8) also
+            # stage 32 steps of sensory sums (forward) or 48 unfolds of saved
+            # v, 1/den and dL/dout rows (chain) in LDS
+            row_b = 2 * KSB * Hp * 4 + KSB * Hp * 8
+            if p["fuse"] and p["RCB"] == 8:
+                row_b = max(row_b, 2 * Hp * 8 + (3 * 48 + 1) * Hp * 4)
+            base = max(base, row_b)
+            row_f = 2 * p["KS"] * Hp * 8 + p["KS"] * Hp * 4
+            if p["RC"] == 16:
+                row_f = max(row_f, 2 * Hp * 4 + 2 * 32 * Hp * 4)
+            assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8, row_f)
         planes = 4 if (NB == 1 and Hp == 64) else 1
         plane = planes * Hp * (Hp + 1) * 4 if p["fuse"] else 0
         assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
