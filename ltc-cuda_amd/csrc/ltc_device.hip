@@ -1210,11 +1210,30 @@ __global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
 // reads its slots' rows back. A buffer is rewritten one unfold after it was
 // read, across that barrier. (8 waves of 8 columns, summed with group_sum8,
 // measured slower at C1: 27.1 against 25.9 us.)
-template <int NS>
-__device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&preg)[16],
-                                                  const int (&ix)[16], float* vsh, int j, bool lead,
-                                                  bool col, float v) {
-  constexpr int HP = 64, TS = kRowSensSteps;
+// Wave-owned single-row forward layouts: waves of 16 columns with 4 row
+// groups per column (group_sum4); HP = 64 runs 4 waves of 16 slots per lane,
+// HP = 128 8 waves of 32 (two waves per SIMD, so each wave has 256
+// registers for its slots' operands).
+template <int HP>
+struct RowWave {
+  static_assert(HP == 64 || HP == 128, "single-row wave layouts");
+  static constexpr int kGroups = 4;
+  static constexpr int kSlots = HP / kGroups;
+  static constexpr int kThreads = HP * kGroups;
+};
+
+// Byte offset of slot r from offsets packed two per register (16 bits each).
+template <int N>
+__device__ __forceinline__ int slot_offset(const unsigned (&ix)[N], int r) {
+  return (int)((r & 1) ? (ix[r >> 1] >> 16) : (ix[r >> 1] & 0xFFFFu));
+}
+
+template <int NS, int HP>
+__device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k,
+                                                  const float4 (&preg)[RowWave<HP>::kSlots],
+                                                  const unsigned (&ix)[RowWave<HP>::kSlots / 2],
+                                                  float* vsh, int j, bool lead, bool col, float v) {
+  constexpr int TS = kRowSensSteps, NT = RowWave<HP>::kThreads;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int b0 = blockIdx.x;
   const float C = k.neuron[j], G = k.neuron[HP + j], L = k.neuron[2 * HP + j];
@@ -1223,20 +1242,20 @@ __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&
   // registers a step ahead, their wait would be a vmcnt(0) at every step
   // boundary (the compiler cannot count the stores issued since across the
   // loop), which also waits for every vsave/densave/out store in flight.
-  float* ssh = vsh + 2 * HP;  // [2][TS][64]: sn, sd of the staged steps
-  // All of a thread's loads are issued before any of them is waited for.
+  float* ssh = vsh + 2 * HP;  // [2][TS][HP]: sn, sd of the staged steps
+  // Direct global-to-LDS copies of 64-float segments (no registers held),
+  // the waves taking segments in turn.
   auto stage = [&](int t0) {
-    constexpr int PER = 2 * TS * HP / 256;
-    const int n = min(T - t0, TS) * HP;
+    const int nseg = min(T - t0, TS) * HP / 64;
     const long long base = ((long long)b0 * T + t0) * HP;
-    float tmp[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int r = (int)threadIdx.x + 256 * (i % (PER / 2));
-      tmp[i] = r < n ? (i < PER / 2 ? k.sn : k.sd)[base + r] : 0.f;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    for (int q = w; q < 2 * nseg; q += NT / 64) {
+      const int a = q >= nseg ? 1 : 0, sg = q - a * nseg;
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>((a ? k.sd : k.sn) + base + sg * 64 + lane),
+          (__attribute__((address_space(3))) void*)(ssh + a * TS * HP + sg * 64), 4, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) ssh[(int)threadIdx.x + 256 * i] = tmp[i];
   };
   if (T > 0) stage(0);
   // One wait for the operands and the first staged steps, before the loop
@@ -1261,22 +1280,33 @@ __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&
       sdr = ssh[(TS + ts) * HP + j];
     }
     const char* vr = reinterpret_cast<const char*>(vsh + P * HP);
-    // Gates in phases (states, arguments, exponentials, reciprocals); the
-    // sums keep their order.
-    float z[NS];
-#pragma unroll
-    for (int rr = 0; rr < NS; ++rr) z[rr] = *reinterpret_cast<const float*>(vr + ix[rr]);
-#pragma unroll
-    for (int rr = 0; rr < NS; ++rr) z[rr] = fmaf(preg[rr].x, z[rr], preg[rr].y);
-#pragma unroll
-    for (int rr = 0; rr < NS; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
-#pragma unroll
-    for (int rr = 0; rr < NS; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
+    // Gates in phases (states, arguments, exponentials, reciprocals), in
+    // groups of at most ZG slots; the sums keep their order.
+    constexpr int ZG = HP == 64 ? 16 : 8;
     float na = 0.f, qa = 0.f;
 #pragma unroll
-    for (int rr = 0; rr < NS; ++rr) {
-      na = fmaf(z[rr], preg[rr].z, na);
-      qa = fmaf(z[rr], preg[rr].w, qa);
+    for (int r0 = 0; r0 < NS; r0 += ZG) {
+      constexpr int Z = NS < ZG ? NS : ZG;
+      float z[Z];
+#pragma unroll
+      for (int q = 0; q < Z; ++q)
+        if (r0 + q < NS) z[q] = *reinterpret_cast<const float*>(vr + slot_offset(ix, r0 + q));
+#pragma unroll
+      for (int q = 0; q < Z; ++q)
+        if (r0 + q < NS) z[q] = fmaf(preg[r0 + q].x, z[q], preg[r0 + q].y);
+#pragma unroll
+      for (int q = 0; q < Z; ++q)
+        if (r0 + q < NS) z[q] = 1.0f + __builtin_amdgcn_exp2f(z[q]);
+#pragma unroll
+      for (int q = 0; q < Z; ++q)
+        if (r0 + q < NS) z[q] = __builtin_amdgcn_rcpf(z[q]);
+#pragma unroll
+      for (int q = 0; q < Z; ++q) {
+        if (r0 + q < NS) {
+          na = fmaf(z[q], preg[r0 + q].z, na);
+          qa = fmaf(z[q], preg[r0 + q].w, qa);
+        }
+      }
     }
     na = group_sum4(na);
     qa = group_sum4(qa);
@@ -1313,39 +1343,56 @@ __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k, const float4 (&
   }
 }
 
-__global__ __launch_bounds__(256) void ode_fwd_row_wave_kernel(FwdK k) {
-  constexpr int HP = 64, RC = 16;
+template <int HP>
+__global__ __launch_bounds__(RowWave<HP>::kThreads) void ode_fwd_row_wave_kernel(FwdK k) {
+  constexpr int RC = RowWave<HP>::kSlots, G = RowWave<HP>::kGroups, CW = 64 / G;
   extern __shared__ float4 lds4[];
-  float* vsh = reinterpret_cast<float*>(lds4);  // [2][64], the state by unfold parity
+  float* vsh = reinterpret_cast<float*>(lds4);  // [2][HP], the state by unfold parity
   const int H = k.H;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int g = lane >> 4;
-  const int j = (tid >> 6) * 16 + (lane & 15);  // output column of this lane
-  const bool lead = g == 0;                     // one lane per column stores
+  const int g = lane / CW;
+  const int j = (tid >> 6) * CW + (lane & (CW - 1));  // output column of this lane
+  const bool lead = g == 0;                           // one lane per column stores
   const bool col = j < H;
   const int cnt = k.ccnt[j];
-  const int nslot = wave_max(cnt > g ? (cnt - 1 - g) / 4 + 1 : 0);
+  const int nslot = wave_max(cnt > g ? (cnt - 1 - g) / G + 1 : 0);
   float4 preg[RC];
-  int ix[RC];
+  unsigned ix[RC / 2];  // LDS byte offsets of the slots' rows, two 16-bit halves each
 #pragma unroll
-  for (int rr = 0; rr < RC; ++rr) {
+  for (int rr = 0; rr < RC; rr += 2) {
     const long long a = (long long)(g * RC + rr) * HP + j;
     preg[rr] = k.cimg[a];
-    ix[rr] = k.cidx[a] * 4;
+    preg[rr + 1] = k.cimg[a + HP];
+    ix[rr / 2] = (unsigned)(k.cidx[a] * 4) | ((unsigned)(k.cidx[a + HP] * 4) << 16);
   }
   const float v = (k.state0 != nullptr && col) ? k.state0[(long long)blockIdx.x * H + j] : 0.f;
   if (lead) vsh[j] = v;
-  switch ((nslot + 1) >> 1) {
-    case 0:
-    case 1: fwd_row_wave_loop<2>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 2: fwd_row_wave_loop<4>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 3: fwd_row_wave_loop<6>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 4: fwd_row_wave_loop<8>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 5: fwd_row_wave_loop<10>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 6: fwd_row_wave_loop<12>(k, preg, ix, vsh, j, lead, col, v); break;
-    case 7: fwd_row_wave_loop<14>(k, preg, ix, vsh, j, lead, col, v); break;
-    default: fwd_row_wave_loop<16>(k, preg, ix, vsh, j, lead, col, v); break;
+  if constexpr (HP == 64) {
+    switch ((nslot + 1) >> 1) {
+      case 0:
+      case 1: fwd_row_wave_loop<2, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 2: fwd_row_wave_loop<4, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 3: fwd_row_wave_loop<6, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 4: fwd_row_wave_loop<8, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 5: fwd_row_wave_loop<10, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 6: fwd_row_wave_loop<12, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 7: fwd_row_wave_loop<14, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      default: fwd_row_wave_loop<16, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+    }
+  } else {
+    // slots rounded up to a multiple of four (padding slots add zeros)
+    switch ((nslot + 3) >> 2) {
+      case 0:
+      case 1: fwd_row_wave_loop<4, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 2: fwd_row_wave_loop<8, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 3: fwd_row_wave_loop<12, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 4: fwd_row_wave_loop<16, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 5: fwd_row_wave_loop<20, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 6: fwd_row_wave_loop<24, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 7: fwd_row_wave_loop<28, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      default: fwd_row_wave_loop<32, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+    }
   }
 }
 
@@ -3639,8 +3686,12 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   const size_t lds = fwd_lds_bytes(p);
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
   if constexpr (NB == 1) {
+    if (row_wave128_fwd(p)) {
+      hipLaunchKernelGGL((ode_fwd_row_wave_kernel<128>), grid, dim3(512), lds, s, a);
+      return hipGetLastError();
+    }
     if (row_kernels(p) && rcp > 0) {
-      if (rcp == 16) hipLaunchKernelGGL(ode_fwd_row_wave_kernel, grid, dim3(256), lds, s, a);
+      if (rcp == 16) hipLaunchKernelGGL((ode_fwd_row_wave_kernel<64>), grid, dim3(256), lds, s, a);
       else if (rcp == 4) hipLaunchKernelGGL((ode_fwd_row_kernel<4>), grid, block, lds, s, a);
       else hipLaunchKernelGGL((ode_fwd_row_kernel<8>), grid, block, lds, s, a);
       return hipGetLastError();

@@ -276,6 +276,11 @@ inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp =
 // column's entries are dealt over.
 // The single-workgroup forward with register-resident operands (RC of 4, 8 or
 // 16) reads one too, its entries dealt over its KS row chunks.
+// One row per workgroup at Hp = 128: the wave-owned single-row forward (8
+// waves of 16 columns, the compacted image in 4 chunks of 32 slots).
+inline bool row_wave128_fwd(const Plan& p) {
+  return p.CP == 0 && p.NB == 1 && p.Hp == 128 && p.KS == 8 && p.RC == 16;
+}
 inline bool generic_fwd_cmp(const Plan& p) {
   return p.CP == 0 && !row_kernels(p) && (p.RC == 4 || p.RC == 8 || p.RC == 16);
 }
@@ -302,7 +307,7 @@ inline bool row_bwd_fused(const Plan& p) {
 }
 inline long long row_bwd_words(const Plan& p) { return (long long)p.B * p.T * 128 + 1; }
 inline int cmp_chunks_fwd(const Plan& p) {
-  return row_kernels(p) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
+  return (row_kernels(p) || row_wave128_fwd(p)) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
 }
 inline int cmp_chunks_bwd(const Plan& p) {
   return row_kernels(p) ? 8 : (p.CP > 0 ? kCmpChunks : p.KSB);
@@ -333,11 +338,12 @@ inline long long fwd_lds(const Plan& p) {
   // or (wave-owned form, RC = 16) the double-buffered state and the staged
   // sensory sums
   long long row = 0;
+  const long long wave = 2LL * p.Hp * 4 + 2LL * kRowSensSteps * p.Hp * 4;
   if (row_kernels(p)) {
     row = 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4;
-    const long long wave = 2LL * p.Hp * 4 + 2LL * kRowSensSteps * p.Hp * 4;
     if (p.RC == 16 && wave > row) row = wave;
   }
+  if (row_wave128_fwd(p)) return wave;
   return base > row ? base : row;
 }
 
