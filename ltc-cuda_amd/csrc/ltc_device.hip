@@ -1562,6 +1562,56 @@ __global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
 // column go to a double-buffered LDS row and, after the unfold's one barrier,
 // every lane reads its slots' pairs back. The unfold loop runs in pairs so
 // that the buffer of each unfold is known at compile time.
+// Stages, for one row's single-workgroup chain, the block of unfolds ending at
+// nhi (at most kRowChainUnfolds of them, down to unfold 0): v^n for n = n_lo
+// ... nhi + 1, 1/den and dL/dout of the steps they cover, as rows of HP
+// floats at vst ([SU + 1][HP] v, then [SU][HP] 1/den, then [SU][HP]
+// dL/dout). Each wave copies 64-float segments (wave-uniform kinds) with
+// direct global-to-LDS loads, which hold no registers; columns past H get
+// 1/den = 1 and dL/dout = 0 by LDS stores. NT threads take part; nothing
+// waits here (the caller waits for vmcnt(0), then a workgroup barrier).
+template <int HP, int NT, bool FULL>
+__device__ __forceinline__ void chain_stage(const BwdK& k, int b0, long long nhi, float* vst,
+                                            long long& n_lo, int& t_lo) {
+  constexpr int SU = kRowChainUnfolds, SPR = HP / 64;
+  const int H = k.H, B = k.B, U = k.U;
+  float* rst = vst + (SU + 1) * HP;
+  float* gst = rst + SU * HP;
+  n_lo = nhi - SU + 1 > 0 ? nhi - SU + 1 : 0;
+  t_lo = (int)(n_lo / U);
+  const int nu = (int)(nhi - n_lo + 1), nt = (int)(nhi / U) - t_lo + 1;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+  for (int q = w; q < (2 * nu + nt + 1) * SPR; q += NT / 64) {
+    const int r = q / SPR, c = (q - r * SPR) * 64 + lane;
+    const bool cl = FULL || c < H;
+    const float* src;
+    float* dst;
+    bool ld = true;
+    float fill = 0.f;
+    if (r <= nu) {
+      src = k.vsave + ((n_lo + r) * B + b0) * HP + c;
+      dst = vst + r * HP + (c - lane);
+    } else if (r <= 2 * nu) {
+      const int rr = r - nu - 1;
+      src = k.densave + ((n_lo + rr) * B + b0) * HP + c;
+      dst = rst + rr * HP + (c - lane);
+      ld = cl;
+      fill = 1.f;
+    } else {
+      const int tt = r - 2 * nu - 1;
+      src = k.gout + (long long)b0 * k.gs.b + (long long)(t_lo + tt) * k.gs.t +
+            (long long)c * k.gs.c;
+      dst = gst + tt * HP + (c - lane);
+      ld = cl;
+    }
+    if (ld)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+    else
+      dst[lane] = fill;
+  }
+}
+
 template <int NS, bool FULL>
 __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&preg)[8],
                                                   const int (&jx)[8], float4 (&gacc)[8],
@@ -1583,43 +1633,8 @@ __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&
   float* gst = rst + SU * HP;                           // [SU][64] dL/dout, steps t_lo...
   long long n_lo = 0;
   int t_lo = 0;
-  // Stages the block of unfolds ending at nhi: each wave copies whole 64-float
-  // rows (wave-uniform kinds) with direct global-to-LDS loads, which hold no
-  // registers; columns past H get 1/den = 1 and dL/dout = 0 by LDS stores.
-  // The 8 waves of the chain take rows w, w + 8, ...
   auto stage = [&](long long nhi) {
-    n_lo = nhi - SU + 1 > 0 ? nhi - SU + 1 : 0;
-    t_lo = (int)(n_lo / U);
-    const int nu = (int)(nhi - n_lo + 1), nt = (int)(nhi / U) - t_lo + 1;
-    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), c = threadIdx.x & 63;
-    const bool cl = FULL || c < H;
-    for (int r = w; r <= 2 * nu + nt; r += 8) {
-      const float* src;
-      float* dst;
-      bool ld = true;
-      float fill = 0.f;
-      if (r <= nu) {
-        src = k.vsave + ((n_lo + r) * B + b0) * HP + c;
-        dst = vst + r * HP;
-      } else if (r <= 2 * nu) {
-        const int rr = r - nu - 1;
-        src = k.densave + ((n_lo + rr) * B + b0) * HP + c;
-        dst = rst + rr * HP;
-        ld = cl;
-        fill = 1.f;
-      } else {
-        const int tt = r - 2 * nu - 1;
-        src = k.gout + (long long)b0 * k.gs.b + (long long)(t_lo + tt) * k.gs.t +
-              (long long)c * k.gs.c;
-        dst = gst + tt * HP;
-        ld = cl;
-      }
-      if (ld)
-        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
-                                         (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
-      else
-        dst[c] = fill;
-    }
+    chain_stage<HP, 512, FULL>(k, b0, nhi, vst, n_lo, t_lo);
   };
   stage((long long)T * U - 1);
   __builtin_amdgcn_s_waitcnt(0);
@@ -1784,6 +1799,151 @@ __device__ __forceinline__ void bwd_row_wave_body(const BwdK& k) {
 template <bool FULL>
 __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
   bwd_row_wave_body<FULL>(k);
+}
+
+// Single-row chain at Hp = 128, unfused (the recurrent parameter gradients
+// come from rec_grad_kernel over the saved alpha/beta): 8 waves; wave w owns
+// the presynaptic neurons i = 16w + (lane & 15), and the lane's group
+// jg = lane >> 4 holds the folded compacted entries jg, jg + 4, ... of row i
+// (the postsynaptic j with S'*WE or S'*WP nonzero, at most 32), with their
+// operands and LDS offsets in registers. As in the Hp = 64 chain: one barrier
+// and one LDS round trip per unfold, dL/dv_i summed inside the wave
+// (group_sum4), the saved rows staged in LDS; alpha/beta of each unfold
+// also go to absave.
+template <int NS, bool FULL>
+__device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4 (&preg)[32],
+                                                     const unsigned (&jx)[16], float2* abs_, int i,
+                                                     bool lead) {
+  constexpr int HP = 128, SU = kRowChainUnfolds;
+  const int H = k.H, B = k.B, T = k.T, U = k.U;
+  const int b0 = blockIdx.x;
+  const bool col = FULL || i < H;
+  const float C = k.neuron[i];
+  float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + i] : 0.f;
+  float pC = 0.f, pGv = 0.f, pA = 0.f;
+  float* vst = reinterpret_cast<float*>(abs_ + 2 * HP);  // [SU + 1][HP] v^n, n = n_lo...
+  float* rst = vst + (SU + 1) * HP;                     // [SU][HP] 1/den
+  float* gst = rst + SU * HP;                           // [SU][HP] dL/dout, steps t_lo...
+  long long n_lo = 0;
+  int t_lo = 0;
+  chain_stage<HP, 512, FULL>(k, b0, (long long)T * U - 1, vst, n_lo, t_lo);
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  float accA = 0.f, accB = 0.f;
+  int t = T - 1, u = U - 1;
+  auto unfold = [&](auto pc) {
+    constexpr int P = decltype(pc)::value;
+    const long long n = (long long)t * U + u;
+    if (n < n_lo) {
+      // every wave read the previous block's rows before this unfold's barrier
+      chain_stage<HP, 512, FULL>(k, b0, n, vst, n_lo, t_lo);
+      __builtin_amdgcn_s_waitcnt(0);
+      lds_barrier();
+    }
+    const int nr = (int)(n - n_lo);
+    const float cvk = vst[nr * HP + i], cvk1 = vst[(nr + 1) * HP + i];
+    const float crd = rst[nr * HP + i];
+    if (u == U - 1) {
+      accA = accB = 0.f;
+      g += gst[(t - t_lo) * HP + i];
+    }
+    float al = 0.f, be = 0.f;
+    if (col) {
+      al = g * crd;  // saved 1/den
+      be = -g * cvk1 * crd;
+    }
+    if (lead) {
+      abs_[P * HP + i] = make_float2(al, be);
+      k.absave[(n * B + b0) * HP + i] = make_float2(al, be);
+      accA += al;
+      accB += be;
+      pC += al * (cvk - cvk1);
+      pGv += al * cvk1;
+      pA += al;
+    }
+    const float gdir = al * C;
+    // The gates depend on v^k only: evaluated in phases ahead of the barrier.
+    float ga[NS];
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
+    lds_barrier();
+    const char* ar = reinterpret_cast<const char*>(abs_ + P * HP);
+    float acc = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < NS; ++rr) {
+      const float2 c = *reinterpret_cast<const float2*>(ar + slot_offset(jx, rr));
+      const float a = ga[rr];
+      const float a2 = fmaf(-a, a, a);
+      acc = fmaf(fmaf(c.x, preg[rr].z, c.y * preg[rr].w), a2, acc);
+    }
+    const float sum = group_sum4(acc);
+    g = col ? fmaf(kNegLn2, sum, gdir) : 0.f;
+    if (u == 0) {
+      if (lead) {
+        const long long e = ((long long)b0 * T + t) * HP + i;
+        k.dsn[e] = accA;
+        k.dsd[e] = accB;
+      }
+      --t;
+      u = U - 1;
+    } else {
+      --u;
+    }
+  };
+  const long long N = (long long)T * U;
+  long long m = 0;
+  for (; m + 1 < N; m += 2) {
+    unfold(std::integral_constant<int, 0>{});
+    unfold(std::integral_constant<int, 1>{});
+  }
+  if (m < N) unfold(std::integral_constant<int, 0>{});
+  if (lead) {
+    if (k.gstate != nullptr && col) k.gstate[(long long)b0 * H + i] = g;
+    float* np = k.npart + (long long)b0 * 3 * HP + i;
+    np[0] = pC;
+    np[HP] = pGv;
+    np[2 * HP] = pA;
+  }
+}
+
+template <bool FULL>
+__global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k) {
+  constexpr int HP = 128, RC = 32;
+  extern __shared__ float4 lds4[];
+  float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][128] alpha/beta by unfold parity
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int jg = lane >> 4;
+  const int i = (tid >> 6) * 16 + (lane & 15);  // presynaptic neuron of this lane
+  const bool lead = jg == 0;                    // one lane per neuron keeps the sums and stores
+  const int cnt = k.ccnt[i];
+  const int nslot = wave_max(cnt > jg ? (cnt - 1 - jg) / 4 + 1 : 0);
+  float4 preg[RC];
+  unsigned jx[RC / 2];  // LDS byte offsets of the slots' alpha/beta, two 16-bit halves each
+#pragma unroll
+  for (int rr = 0; rr < RC; rr += 2) {
+    const long long a = (long long)(jg * RC + rr) * HP + i;
+    preg[rr] = k.cimg[a];
+    preg[rr + 1] = k.cimg[a + HP];
+    jx[rr / 2] = (unsigned)(k.cidx[a] * 8) | ((unsigned)(k.cidx[a + HP] * 8) << 16);
+  }
+  if (k.T == 0) return;
+  // slots rounded up to a multiple of four (padding slots add zeros)
+  switch ((nslot + 3) >> 2) {
+    case 0:
+    case 1: bwd_row_wave128_loop<4, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 2: bwd_row_wave128_loop<8, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 3: bwd_row_wave128_loop<12, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 4: bwd_row_wave128_loop<16, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 5: bwd_row_wave128_loop<20, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 6: bwd_row_wave128_loop<24, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 7: bwd_row_wave128_loop<28, FULL>(k, preg, jx, abs_, i, lead); break;
+    default: bwd_row_wave128_loop<32, FULL>(k, preg, jx, abs_, i, lead); break;
+  }
 }
 
 // Companion of the fused row backward for batch row b (module path): the
@@ -3718,6 +3878,13 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
         hipLaunchKernelGGL((ode_bwd_row_wave_kernel<true>), grid, block, lds, s, a);
       else
         hipLaunchKernelGGL((ode_bwd_row_wave_kernel<false>), grid, block, lds, s, a);
+      return hipGetLastError();
+    }
+    if (row_wave128_bwd(p)) {
+      if (p.H == 128)
+        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a);
+      else
+        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, dim3(512), lds, s, a);
       return hipGetLastError();
     }
   }

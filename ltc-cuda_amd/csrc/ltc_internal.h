@@ -281,6 +281,11 @@ inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp =
 inline bool row_wave128_fwd(const Plan& p) {
   return p.CP == 0 && p.NB == 1 && p.Hp == 128 && p.KS == 8 && p.RC == 16;
 }
+// The unfused single-row chain at Hp = 128 (ode_bwd_row_wave128_kernel: 8
+// waves of 16 neurons, the folded compacted image in 4 chunks of 32 slots).
+inline bool row_wave128_bwd(const Plan& p) {
+  return p.CP == 0 && p.NB == 1 && p.Hp == 128 && !p.FUSE && p.KSB == 8 && p.RCB == 16;
+}
 inline bool generic_fwd_cmp(const Plan& p) {
   return p.CP == 0 && !row_kernels(p) && (p.RC == 4 || p.RC == 8 || p.RC == 16);
 }
@@ -310,7 +315,7 @@ inline int cmp_chunks_fwd(const Plan& p) {
   return (row_kernels(p) || row_wave128_fwd(p)) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
 }
 inline int cmp_chunks_bwd(const Plan& p) {
-  return row_kernels(p) ? 8 : (p.CP > 0 ? kCmpChunks : p.KSB);
+  return row_kernels(p) ? 8 : (row_wave128_bwd(p) ? 4 : (p.CP > 0 ? kCmpChunks : p.KSB));
 }
 // Dynamic LDS of a cluster chain member (cluster_chain_lds) plus, with the
 // compacted image, its slot table.
@@ -365,6 +370,9 @@ inline long long chain_lds(const Plan& p) {
   if (row_kernels(p) && rowb > base) base = rowb;
   const long long plane =
       p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;
+  // the unfused single-row chain at Hp = 128: alpha/beta by parity and the
+  // staged rows
+  if (row_wave128_bwd(p)) return 2LL * p.Hp * 8 + (3LL * kRowChainUnfolds + 1) * p.Hp * 4;
   return base > plane ? base : plane;
 }
 

@@ -239,7 +239,12 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
             assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8, row_f)
         planes = 4 if (NB == 1 and Hp == 64) else 1
         plane = planes * Hp * (Hp + 1) * 4 if p["fuse"] else 0
-        assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
+        if NB == 1 and Hp == 128 and not p["fuse"] and KSB == 8 and p["RCB"] == 16:
+            # the unfused wave-owned single-row chain: alpha/beta by parity and
+            # 48 unfolds of staged v, 1/den and dL/dout rows
+            assert p["lds_bwd"] == 2 * Hp * 8 + (3 * 48 + 1) * Hp * 4 <= 159 * 1024
+        else:
+            assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
     assert 1 <= p["NRC"] <= 64
     if p["CP"] > 0:
         # Cluster path: CP members of 64 columns each, the whole grid resident
