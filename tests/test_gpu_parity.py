@@ -171,10 +171,13 @@ def test_cluster_path_graph_replay_matches_eager():
         torch.cuda.synchronize()
 
 
-def test_long_sequence_backward_matches_oracle():
-    """480 unfolds (T = 80): the chain's one-unfold-ahead operand pipeline and
-    the per-step output-gradient loads over a long reverse walk."""
-    B, T, D, H = 4, 80, 8, 16
+@pytest.mark.parametrize("shape", [(4, 80, 8, 16), (3, 40, 8, 100)],
+                         ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_long_sequence_backward_matches_oracle(shape):
+    """480 and 240 unfolds at Hp = 64 and 128 (one row per workgroup): the
+    single-row forward restages its sensory sums in LDS every 32 steps and the
+    chain its saved rows every 48 unfolds, over a long reverse walk."""
+    B, T, D, H = shape
     args = boundary(B, T, D, H, seed=9)
     dev_args, (out, h, saved) = gpu_forward(args, save=True)
     g = torch.Generator().manual_seed(10)
