@@ -2083,6 +2083,11 @@ __device__ __forceinline__ void row_companion(const BwdK& k, const RowCompanion&
       }
     }
   }
+  // The row's words back to tag 0, every step consumed: another backward
+  // over the same forward (whose prep launch cleared them) then waits for its
+  // own chain's words instead of reading these.
+  for (int e = tid; e < T * 2 * HP; e += (int)blockDim.x)
+    xch_put(c.words + (long long)b * T * 2 * HP + e, 0.f, 0u);
   if (*flag) {
     if (tid == 0)
       __hip_atomic_store(reinterpret_cast<int*>(c.words + (long long)k.B * T * 128), 1,

@@ -564,6 +564,40 @@ def test_hip_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60)],
+                         ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_module_backward_twice_over_one_forward(shape):
+    """Two backward passes over one forward (retain_graph) with different
+    output gradients: each must match the float64 oracle for its own output
+    gradient. At these shapes the backward hands each step's dL/dsn, dL/dsd to
+    companion workgroups as words, which the forward clears; the second pass
+    must not read the first pass's words."""
+    B, T, D, H = shape
+    assert ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)["module_row_bwd_fused"] == 1
+    m = _perturbed_module(D, H, seed=B + H).to(DEV)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, T, D, generator=g)
+    h0 = torch.randn(B, H, generator=g) * 0.2
+    Gs = [torch.randn(B, T, H, generator=g) for _ in range(2)]
+    Gh = torch.zeros(B, H)
+    xg = x.to(DEV).requires_grad_(True)
+    hg = h0.to(DEV).requires_grad_(True)
+    out, (h, _) = m(xg, (hg, hg))
+    names = ["x", "h0"] + [n for n, _ in m.named_parameters()]
+    for r, G in enumerate(Gs):
+        xg.grad = hg.grad = None
+        m.zero_grad(set_to_none=True)
+        (out * G.to(DEV)).sum().backward(retain_graph=(r == 0))
+        _, _, r_g, r_gx, r_gh = _oracle_module_grads(m, x, h0, G, Gh)
+        got = [xg.grad.cpu(), hg.grad.cpu()] + [p.grad.cpu() for _, p in m.named_parameters()]
+        ref = [r_gx, r_gh] + [r_g[n] for n, _ in m.named_parameters()]
+        for n, a, rf in zip(names, got, ref):
+            rf = rf.double()
+            err = (a.double() - rf).abs().max().item()
+            assert torch.isfinite(a).all(), (r, n)
+            assert err <= 2e-3 * rf.abs().max().item() + 1e-6, f"pass {r} {n}: err {err:.2e}"
+
+
 def test_whole_step_capture_replays_match_eager():
     """ltc_cuda.CapturedStep: forward, loss and backward of the C1-shaped layer in
     one HIP graph. Every replay, with eager work and synchronisations between
