@@ -1093,111 +1093,6 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Single-row kernels at Hp = 64 (NB = 1: one wave spans all columns).
-// Every wave keeps the row's per-column state in lane o and updates it from
-// the same KS partials in the same fixed order, so the copies agree bitwise;
-// a wave reads the values of its own synapse rows back from its private LDS
-// copy, with no barrier. That leaves one barrier per unfold: the partials alternate
-// between two LDS buffers by unfold parity, and a buffer is rewritten two
-// unfolds later, after every wave has passed the barrier that follows its
-// reads. The forward's results are bitwise those of ode_fwd_kernel; the
-// chain's match ode_bwd_kernel's to the rounding of the multiply-adds the
-// compiler contracts differently in the two bodies.
-// ---------------------------------------------------------------------------
-template <int RCP>
-__global__ __launch_bounds__(64 * (64 / RCP)) void ode_fwd_row_kernel(FwdK k) {
-  constexpr int HP = 64, KS = HP / RCP;
-  extern __shared__ float4 lds4[];
-  float2* red = reinterpret_cast<float2*>(lds4);  // [2][KS][64]
-  // Each wave's own copy of the row state, [KS][64]: a wave writes it and
-  // reads its synapse rows back as broadcasts (all lanes one address), so the
-  // values reach the VALU without a v_readlane per synapse; the LDS orders one
-  // wave's accesses, so no barrier is needed.
-  float* vw = reinterpret_cast<float*>(red + 2 * KS * HP);
-  const int H = k.H, B = k.B, T = k.T, U = k.U;
-  const int tid = threadIdx.x;
-  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
-  const int b0 = blockIdx.x;
-  const int r0 = ks * RCP;
-  const bool col = o < H;
-  const float C = k.neuron[o], G = k.neuron[HP + o], L = k.neuron[2 * HP + o];
-  const float GL = G * L, CG = C + G;
-  float4 preg[RCP];
-#pragma unroll
-  for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recF[(long long)(r0 + rr) * HP + o];
-  float v = (k.state0 != nullptr && col) ? k.state0[(long long)b0 * H + o] : 0.f;
-  float snr = 0.f, sdr = 0.f, snn = 0.f, sdn = 0.f;
-  auto load_sens = [&](int t, float& a, float& d) {
-    const long long e = ((long long)b0 * T + t) * HP + o;
-    a = k.sn[e];
-    d = k.sd[e];
-  };
-  if (T > 0) load_sens(0, snr, sdr);
-  // Wait for the operands and the first step's sums here, once: otherwise the
-  // unfold loop's first use of sdr carries a vmcnt(0) wait every unfold, and
-  // on gfx9 that also waits for the previous unfold's vsave/densave stores
-  // (C1 forward 27.1 -> 26.8 us).
-  __builtin_amdgcn_s_waitcnt(0);
-  int par = 0;
-  for (int t = 0; t < T; ++t) {
-    if (t + 1 < T) load_sens(t + 1, snn, sdn);
-    for (int u = 0; u < U; ++u) {
-      // The gates of all RCP synapses in phases (arguments, exponentials,
-      // reciprocals), so that each transcendental's result is consumed
-      // several instructions later; the sums keep their order.
-      float* vme = vw + ks * HP;
-      vme[o] = v;
-      float vi[RCP];
-#pragma unroll
-      for (int q = 0; q < RCP; q += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(vme + r0 + q);
-        vi[q] = w4.x;
-        vi[q + 1] = w4.y;
-        vi[q + 2] = w4.z;
-        vi[q + 3] = w4.w;
-      }
-      float z[RCP];
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) z[rr] = fmaf(preg[rr].x, vi[rr], preg[rr].y);
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) z[rr] = 1.0f + __builtin_amdgcn_exp2f(z[rr]);
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) z[rr] = __builtin_amdgcn_rcpf(z[rr]);
-      float na = 0.f, qa = 0.f;
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) {
-        na = fmaf(z[rr], preg[rr].z, na);
-        qa = fmaf(z[rr], preg[rr].w, qa);
-      }
-      float2* rb = red + par * KS * HP;
-      rb[ks * HP + o] = make_float2(na, qa);
-      lds_barrier();
-      const float2 nq = tree_sum<KS>(rb + o, HP);
-      const float den = CG + (nq.y + sdr) + k.eps;
-      const float num = C * v + GL + (nq.x + snr);
-      const float rden = __builtin_amdgcn_rcpf(den);
-      const float vnew = col ? num * rden : 0.f;
-      if (ks == 0) {
-        if (k.vsave != nullptr) {
-          const long long e = ((long long)(t * U + u) * B + b0) * HP + o;
-          k.vsave[e] = v;
-          k.densave[e] = rden;
-        }
-        if (u == U - 1 && col) k.out[((long long)b0 * T + t) * H + o] = vnew;
-      }
-      v = vnew;
-      par ^= 1;
-    }
-    snr = snn;
-    sdr = sdn;
-  }
-  if (ks == 0) {
-    if (col) k.hfin[(long long)b0 * H + o] = v;
-    if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0) * HP + o] = v;
-  }
-}
-
 // Single-row forward at Hp = 64 with wave-owned columns: 4 waves, wave w owns
 // the 16 output columns j = 16w + (lane & 15), and the lane's row group
 // g = lane >> 4 holds the compacted entries g, g + 4, ... of column j (the
@@ -1258,8 +1153,10 @@ __device__ __forceinline__ void fwd_row_wave_loop(const FwdK& k,
     }
   };
   if (T > 0) stage(0);
-  // One wait for the operands and the first staged steps, before the loop
-  // (see ode_fwd_row_kernel).
+  // One wait for the operands and the first staged steps, before the loop:
+  // otherwise the loop's first use of them carries a vmcnt(0) wait every
+  // unfold, which on gfx9 also waits for the previous unfold's vsave/densave
+  // stores.
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();
   float snr = 0.f, sdr = 0.f;
@@ -1396,172 +1293,6 @@ __global__ __launch_bounds__(RowWave<HP>::kThreads) void ode_fwd_row_wave_kernel
   }
 }
 
-// Fused chain (FUSE) of one row at Hp = 64: thread (ks, o) holds the RCP
-// synapses (i = o, j = ks*RCP + rr) with their four gradient sums. Launched
-// with RCP = 8 (8 waves): 33.9 us at C1 against 36.5 us at RCP = 4 (rocprofv3
-// kernel trace, 200 launches).
-// FULL: H == 64, so every column is live and no lane needs masking.
-template <int RCP, bool FULL>
-__global__ __launch_bounds__(1024) void ode_bwd_row_kernel(BwdK k) {
-  constexpr int HP = 64, KS = HP / RCP;
-  extern __shared__ float4 lds4[];
-  float* red = reinterpret_cast<float*>(lds4);  // [2][KS][64]
-  // Each wave's own copy of alpha/beta, [KS][64] float2, read back as
-  // broadcasts (see ode_fwd_row_kernel).
-  float2* abw = reinterpret_cast<float2*>(red + 2 * KS * HP);
-  const int H = k.H, B = k.B, T = k.T, U = k.U;
-  const int tid = threadIdx.x;
-  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
-  const int b0 = blockIdx.x;
-  const int r0 = ks * RCP;
-  const bool col = FULL || o < H;
-  const float C = k.neuron[o];
-  float4 preg[RCP], gacc[RCP];
-#pragma unroll
-  for (int rr = 0; rr < RCP; ++rr) {
-    preg[rr] = k.recB[(long long)(r0 + rr) * HP + o];
-    gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  float g = (k.ghfin != nullptr && col) ? k.ghfin[(long long)b0 * H + o] : 0.f;
-  float pC = 0.f, pGv = 0.f, pA = 0.f;
-  if (T == 0) return;
-  const long long BHp = (long long)B * HP;
-  // Saved pre-state v^k (also v_i of the synapses), 1/den and v^{k+1} of
-  // column o for unfold n, software-pipelined one unfold ahead.
-  auto load = [&](long long n, float& vk, float& rd, float& vk1) {
-    const long long e = (n * B + b0) * HP + o;
-    vk = k.vsave[e];
-    rd = col ? k.densave[e] : 1.f;
-    vk1 = k.vsave[e + BHp];
-  };
-  auto gout = [&](int t) {
-    return col ? k.gout[(long long)b0 * k.gs.b + (long long)t * k.gs.t + (long long)o * k.gs.c]
-               : 0.f;
-  };
-  float cvk, crd, cvk1, nvk = 0.f, nrd = 1.f, nvk1 = 0.f;
-  load((long long)T * U - 1, cvk, crd, cvk1);
-  float gcur = gout(T - 1), gnext = 0.f;
-  int par = 0;
-  for (int t = T - 1; t >= 0; --t) {
-    if (t > 0) gnext = gout(t - 1);
-    float accA = 0.f, accB = 0.f;
-    g += gcur;
-    for (int u = U - 1; u >= 0; --u) {
-      const long long n = (long long)t * U + u;
-      if (n > 0) load(n - 1, nvk, nrd, nvk1);
-      float al = 0.f, be = 0.f;
-      if (col) {
-        al = g * crd;  // saved 1/den
-        be = -g * cvk1 * crd;
-      }
-      // Every wave forms alpha/beta of the whole row (it needs them all), but
-      // only wave 0 keeps the per-step and per-row sums it alone writes out.
-      if (ks == 0) {
-        accA += al;
-        accB += be;
-        pC += al * (cvk - cvk1);
-        pGv += al * cvk1;
-        pA += al;
-      }
-      const float gdir = al * C;
-      // The RCP gates depend on v^k only: evaluated in phases (arguments,
-      // exponentials, reciprocals) ahead of the alpha/beta products.
-      float ga[RCP];
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) ga[rr] = fmaf(preg[rr].x, cvk, preg[rr].y);
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) ga[rr] = 1.0f + __builtin_amdgcn_exp2f(ga[rr]);
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) ga[rr] = __builtin_amdgcn_rcpf(ga[rr]);
-      float2* abme = abw + ks * HP;
-      abme[o] = make_float2(al, be);
-      float2 abj[RCP];
-#pragma unroll
-      for (int q = 0; q < RCP; q += 2) {
-        const float4 w4 = *reinterpret_cast<const float4*>(abme + r0 + q);
-        abj[q] = make_float2(w4.x, w4.y);
-        abj[q + 1] = make_float2(w4.z, w4.w);
-      }
-      float acc = 0.f;
-#pragma unroll
-      for (int rr = 0; rr < RCP; ++rr) {
-        const float4 p = preg[rr];
-        const float cx = abj[rr].x, cy = abj[rr].y;
-        const float a = ga[rr];
-        const float a2 = fmaf(-a, a, a);
-        const float dl = fmaf(cx, p.z, cy * p.w) * a2;
-        acc = fmaf(dl, p.x, acc);
-        gacc[rr].x = fmaf(cx, a, gacc[rr].x);
-        gacc[rr].y = fmaf(cy, a, gacc[rr].y);
-        gacc[rr].z += dl;
-        gacc[rr].w = fmaf(dl, cvk, gacc[rr].w);
-      }
-      float* rb = red + par * KS * HP;
-      rb[ks * HP + o] = acc;
-      lds_barrier();
-      const float s = tree_sum<KS>(rb + o, HP);
-      g = col ? fmaf(kNegLn2, s, gdir) : 0.f;
-      par ^= 1;
-      if (n > 0) {
-        cvk = nvk;
-        crd = nrd;
-        cvk1 = nvk1;
-      }
-    }
-    if (ks == 0) {
-      const long long e = ((long long)b0 * T + t) * HP + o;
-      k.dsn[e] = accA;
-      k.dsd[e] = accB;
-    }
-    gcur = gnext;
-  }
-  if (ks == 0) {
-    if (k.gstate != nullptr && col) k.gstate[(long long)b0 * H + o] = g;
-    float* np = k.npart + (long long)b0 * 3 * HP + o;
-    np[0] = pC;
-    np[HP] = pGv;
-    np[2 * HP] = pA;
-  }
-  // Recurrent-gradient partials through four padded [64][65] LDS planes at
-  // once, whole rows out (layout [workgroup][4][i][j], as ode_bwd_kernel's):
-  // one barrier pair, and each thread's reads all in flight before its stores.
-  constexpr int TLD = HP + 1, PL = HP * TLD;
-  constexpr int NT = KS * 64, PER = 4 * HP * HP / NT;
-  float* tile = reinterpret_cast<float*>(lds4);
-  float* out = k.rpart + (long long)blockIdx.x * 4 * HP * HP;
-  __syncthreads();
-#pragma unroll
-  for (int rr = 0; rr < RCP; ++rr) {
-    const float4 w = gacc[rr];
-    const int e = o * TLD + r0 + rr;
-    tile[e] = w.x;
-    tile[PL + e] = w.y;
-    tile[2 * PL + e] = w.z;
-    tile[3 * PL + e] = w.w;
-  }
-  __syncthreads();
-  float vals[PER];
-#pragma unroll
-  for (int q = 0; q < PER; ++q) {
-    const int e = tid + q * NT;
-    const int pl = e >> 12, i = (e >> 6) & 63, j = e & 63;
-    vals[q] = tile[pl * PL + i * TLD + j];
-  }
-#pragma unroll
-  for (int q = 0; q < PER; ++q) out[tid + q * NT] = vals[q];
-}
-
-// Fused single-row chain at Hp = 64 with wave-owned presynaptic neurons: 8
-// waves, wave w owns i = 8w + (lane & 7), and the lane's group jg = lane >> 3
-// holds the compacted entries jg, jg + 8, ... of column i (its postsynaptic
-// j: every real synapse on the boundary, those with a nonzero mask entry on
-// the module path), with their operands, four gradient sums and LDS offsets
-// in registers. The wave runs NS slots, its fullest lane's count rounded up
-// to even, in a loop unrolled for that NS. dL/dv_i finishes inside the wave
-// (group_sum8), so an unfold has one LDS round trip: alpha/beta of every
-// column go to a double-buffered LDS row and, after the unfold's one barrier,
-// every lane reads its slots' pairs back. The unfold loop runs in pairs so
-// that the buffer of each unfold is known at compile time.
 // Stages, for one row's single-workgroup chain, the block of unfolds ending at
 // nhi (at most kRowChainUnfolds of them, down to unfold 0): v^n for n = n_lo
 // ... nhi + 1, 1/den and dL/dout of the steps they cover, as rows of HP
@@ -1612,6 +1343,17 @@ __device__ __forceinline__ void chain_stage(const BwdK& k, int b0, long long nhi
   }
 }
 
+// Fused single-row chain at Hp = 64 with wave-owned presynaptic neurons: 8
+// waves, wave w owns i = 8w + (lane & 7), and the lane's group jg = lane >> 3
+// holds the compacted entries jg, jg + 8, ... of column i (its postsynaptic
+// j: every real synapse on the boundary, those with a nonzero mask entry on
+// the module path), with their operands, four gradient sums and LDS offsets
+// in registers. The wave runs NS slots, its fullest lane's count rounded up
+// to even, in a loop unrolled for that NS. dL/dv_i finishes inside the wave
+// (group_sum8), so an unfold has one LDS round trip: alpha/beta of every
+// column go to a double-buffered LDS row and, after the unfold's one barrier,
+// every lane reads its slots' pairs back. The unfold loop runs in pairs so
+// that the buffer of each unfold is known at compile time.
 template <int NS, bool FULL>
 __device__ __forceinline__ void bwd_row_wave_loop(const BwdK& k, const float4 (&preg)[8],
                                                   const int (&jx)[8], float4 (&gacc)[8],
@@ -3855,10 +3597,10 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
       hipLaunchKernelGGL((ode_fwd_row_wave_kernel<128>), grid, dim3(512), lds, s, a);
       return hipGetLastError();
     }
-    if (row_kernels(p) && rcp > 0) {
-      if (rcp == 16) hipLaunchKernelGGL((ode_fwd_row_wave_kernel<64>), grid, dim3(256), lds, s, a);
-      else if (rcp == 4) hipLaunchKernelGGL((ode_fwd_row_kernel<4>), grid, block, lds, s, a);
-      else hipLaunchKernelGGL((ode_fwd_row_kernel<8>), grid, block, lds, s, a);
+    if (row_kernels(p)) {
+      // the launch plan gives every single-row forward at Hp = 64 RC = 16
+      if (rcp != 16) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((ode_fwd_row_wave_kernel<64>), grid, dim3(256), lds, s, a);
       return hipGetLastError();
     }
   }
@@ -3878,7 +3620,9 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   const int rcp = (p.RCB == 4 || p.RCB == 8 || p.RCB == 16) ? p.RCB : 0;
 #define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
   if constexpr (NB == 1) {
-    if (row_kernels(p) && p.FUSE && rcp == 8) {
+    if (row_kernels(p)) {
+      // the launch plan gives every single-row chain at Hp = 64 FUSE, RCB = 8
+      if (!p.FUSE || rcp != 8) return hipErrorInvalidValue;
       if (p.H == 64)
         hipLaunchKernelGGL((ode_bwd_row_wave_kernel<true>), grid, block, lds, s, a);
       else

@@ -22,7 +22,7 @@ constexpr int ode_owned_rows(int nb) { return nb <= 2 ? nb : nb / 4; }
 // gradient accumulators of every register-resident operand without spilling
 // at the register budget __launch_bounds__(ode_max_threads(NB)) leaves
 // (checked against the compiled code objects: zero scratch). One row at
-// Hp = 64 uses the single-row chain instead (ode_bwd_row_kernel).
+// Hp = 64 uses the single-row chain instead (ode_bwd_row_wave_kernel).
 constexpr bool ode_fuse_ok(int nb, int rc) {
   return (nb == 4 && (rc == 4 || rc == 8)) || (nb == 8 && (rc == 4 || rc == 8)) ||
          (nb == 16 && rc == 4);
@@ -266,8 +266,8 @@ inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.
 inline bool chain_prefetches(const Plan& p) { return p.FUSE && p.CP > 0 && p.Hp == 256; }
-// One row per workgroup at Hp = 64: the single-row kernels (every wave keeps
-// the row's state, one barrier per unfold, partials double-buffered).
+// One row per workgroup at Hp = 64: the wave-owned single-row forward
+// (RC = 16) and fused chain (RCB = 8), one barrier per unfold.
 inline bool row_kernels(const Plan& p) { return p.CP == 0 && p.NB == 1 && p.Hp == 64; }
 // Kernels that read compacted images: the cluster forward and the fused
 // cluster chain with register-resident operands (16 rows per thread,
@@ -330,7 +330,7 @@ inline long long cluster_fwd_lds(const Plan& p) {
          (cmp_fwd(p) ? cmp_index_lds(64 * p.KS) : 0);
 }
 // Dynamic LDS of the single-workgroup forward: state rows and the KS
-// partials, or the single-row kernel's two partial buffers.
+// partials, or the wave-owned single-row forward's state and staged sums.
 // Steps of sensory sums the single-row forward stages in LDS at a time, and
 // unfolds of saved states the single-row chain stages.
 constexpr int kRowSensSteps = 32;
@@ -339,40 +339,30 @@ inline long long fwd_lds(const Plan& p) {
   // with the compacted image, the slot table: one int per slot per thread
   const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8 +
                          (generic_fwd_cmp(p) ? (long long)p.Hp * p.KS * p.RC * 4 : 0);
-  // single-row kernels: two partial buffers and each wave's copy of the state,
-  // or (wave-owned form, RC = 16) the double-buffered state and the staged
-  // sensory sums
-  long long row = 0;
+  // the wave-owned single-row forms: the double-buffered state and the
+  // staged sensory sums
   const long long wave = 2LL * p.Hp * 4 + 2LL * kRowSensSteps * p.Hp * 4;
-  if (row_kernels(p)) {
-    row = 2LL * p.KS * p.Hp * 8 + (long long)p.KS * p.Hp * 4;
-    if (p.RC == 16 && wave > row) row = wave;
-  }
   if (row_wave128_fwd(p)) return wave;
+  const long long row = row_kernels(p) ? wave : 0;
   return base > row ? base : row;
 }
 
 // Dynamic LDS of the single-workgroup chain (ode_bwd_kernel): alpha/beta rows
-// and the KS partials (two buffers in the single-row kernel); with FUSE at
-// least one padded [Hp][Hp+1] plane (all four in the single-row kernel),
-// through which the recurrent-gradient partials are transposed for coalesced
-// stores.
+// and the KS partials, or the wave-owned single-row chain's alpha/beta and
+// staged rows; with FUSE at least one padded [Hp][Hp+1] plane (all four in
+// the single-row chain at Hp = 64), through which the recurrent-gradient
+// partials are transposed for coalesced stores.
 inline long long chain_lds(const Plan& p) {
   // with the compacted image, the slot table: one int per slot per thread
   long long base = (long long)p.NB * p.Hp * 8 + (long long)p.KSB * p.NB * p.Hp * 4 +
                    (generic_bwd_cmp(p) ? (long long)p.Hp * p.KSB * p.RCB * 4 : 0);
-  // single-row chain: two partial buffers and each wave's copy of alpha/beta;
-  // the wave-owned form (FUSE, RCB = 8) alpha/beta by parity and the staged
+  // the wave-owned single-row chains: alpha/beta by parity and the staged
   // v^k, 1/den and dL/dout rows
-  long long rowb = 2LL * p.KSB * p.Hp * 4 + (long long)p.KSB * p.Hp * 8;
   const long long waveb = 2LL * p.Hp * 8 + (3LL * kRowChainUnfolds + 1) * p.Hp * 4;
-  if (p.FUSE && p.RCB == 8 && waveb > rowb) rowb = waveb;
-  if (row_kernels(p) && rowb > base) base = rowb;
+  if (row_wave128_bwd(p)) return waveb;
+  if (row_kernels(p) && waveb > base) base = waveb;
   const long long plane =
       p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;
-  // the unfused single-row chain at Hp = 128: alpha/beta by parity and the
-  // staged rows
-  if (row_wave128_bwd(p)) return 2LL * p.Hp * 8 + (3LL * kRowChainUnfolds + 1) * p.Hp * 4;
   return base > plane ? base : plane;
 }
 
