@@ -2718,78 +2718,119 @@ __device__ __forceinline__ void finalize_leaf_poison(const FinLeafK& k, long lon
   if (tid < k.ns && k.gstate != nullptr) k.gstate[tid] = nan;
 }
 
+// One plane's sum over n partials at stride `stride`, in partial order, up to
+// 32 loads in flight at once. Indices past n reload the last partial and add
+// zero, which leaves the sum bitwise unchanged (it starts at +0 and a
+// round-to-nearest sum is never -0 unless both terms are).
+__device__ __forceinline__ float sum_partials_plane(const float* p, long long stride, int n) {
+  float acc = 0.f;
+  for (int z = 0; z < n; z += 32) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int zi = z + i < n ? z + i : n - 1;
+      v[i] = p[(long long)zi * stride];
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc += z + i < n ? v[i] : 0.f;
+  }
+  return acc;
+}
+
+// Lane L's value of each group of four lanes (DPP quad permute).
+template <int L>
+__device__ __forceinline__ float quad_lane(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), L * 0x55, 0xf, 0xf, false));
+}
+
+// Four threads per output element: lane q of the quad sums partial plane q,
+// the quad exchanges the sums, and lane q writes the element's q-th
+// gradient. The sums run in partial order, so the results are those of one
+// thread summing all planes, with a quarter of its dependent loads. With a
+// gave-up status, one thread per output (every leaf gradient, dL/dx, dL/dh0)
+// writes NaN instead.
 __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
-  long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (k.status != nullptr &&
       __hip_atomic_load(k.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-    finalize_leaf_poison(k, tid);
+    finalize_leaf_poison(k, gid);
     return;
   }
   const int H = k.H, D = k.D, Hp = k.Hp, Dp = k.Dp;
   const long long nrec = (long long)H * H, nsens = (long long)D * H;
-  if (tid < nrec) {
-    const int i = (int)(tid / H), j = (int)(tid - (long long)i * H);
+  // every branch below is uniform over a quad: its lanes share e
+  long long e = gid >> 2;
+  const int q = (int)(gid & 3);
+  if (e < nrec) {
+    const int i = (int)(e / H), j = (int)(e - (long long)i * H);
     const long long HH = (long long)Hp * Hp;
-    const float mk = k.lp.mask[tid];
+    const float mk = k.lp.mask[e];
     if (mk == 0.f) {
       // A masked synapse's four gradients are zero; the compacted chain
       // leaves its partials unwritten.
-      k.g.w[tid] = k.g.erev[tid] = k.g.mu[tid] = k.g.sigma[tid] = 0.f;
+      float* dst = q == 0 ? k.g.w : (q == 1 ? k.g.erev : (q == 2 ? k.g.mu : k.g.sigma));
+      dst[e] = 0.f;
       return;
     }
-    const float* src = k.rpart + (long long)i * Hp + j;
-    float sp[4];
-    sum_partials_planes<4>(src, HH, 4 * HH, k.NCH, sp);
-    const float dwe = sp[0], dwp = sp[1], sd = sp[2], sdv = sp[3];
-    const float wv = k.lp.w[tid], ev = k.lp.erev[tid];
-    const float wpos = softplus_t(wv) * mk;
-    // w_pos feeds the synapse directly and through w_erev = w_pos * erev.
-    k.g.w[tid] = (dwp + dwe * ev) * mk * softplus_grad(wv);
-    k.g.erev[tid] = dwe * wpos;
-    k.g.mu[tid] = -k.lp.sigma[tid] * sd;
-    k.g.sigma[tid] = sdv - k.lp.mu[tid] * sd;
+    const float s = sum_partials_plane(k.rpart + q * HH + (long long)i * Hp + j, 4 * HH, k.NCH);
+    const float dwe = quad_lane<0>(s), dwp = quad_lane<1>(s);
+    const float sd = quad_lane<2>(s), sdv = quad_lane<3>(s);
+    const float wv = k.lp.w[e];
+    if (q == 0) {
+      // w_pos feeds the synapse directly and through w_erev = w_pos * erev.
+      k.g.w[e] = (dwp + dwe * k.lp.erev[e]) * mk * softplus_grad(wv);
+    } else if (q == 1) {
+      k.g.erev[e] = dwe * (softplus_t(wv) * mk);
+    } else if (q == 2) {
+      k.g.mu[e] = -k.lp.sigma[e] * sd;
+    } else {
+      k.g.sigma[e] = sdv - k.lp.mu[e] * sd;
+    }
     return;
   }
-  tid -= nrec;
-  if (tid < nsens) {
-    const int h = (int)(tid / D), d = (int)(tid - (long long)h * D);
+  e -= nrec;
+  if (e < nsens) {
+    const int h = (int)(e / D), d = (int)(e - (long long)h * D);
     const long long DH = (long long)Dp * Hp;
-    const float* src = k.spart + (long long)h * Dp + d;
-    float sp[4];
-    sum_partials_planes<4>(src, DH, 4 * DH, k.NRC, sp);
-    const float s1 = sp[0], s2 = sp[1], s3 = sp[2], s4 = sp[3];
-    const long long e = (long long)d * H + h;
-    const float sw = k.lp.s_w[e], mk = k.lp.s_mask[e];
-    const float Ws = softplus_t(sw) * mk, Ss = k.lp.s_sigma[e], Ms = k.lp.s_mu[e];
-    k.g.s_w[e] = s1 * mk * softplus_grad(sw);
-    k.g.s_erev[e] = Ws * s2;
-    k.g.s_mu[e] = -Ss * Ws * s3;
-    k.g.s_sigma[e] = Ws * (s4 - Ms * s3);
+    const float s = sum_partials_plane(k.spart + q * DH + (long long)h * Dp + d, 4 * DH, k.NRC);
+    const float s1 = quad_lane<0>(s), s2 = quad_lane<1>(s);
+    const float s3 = quad_lane<2>(s), s4 = quad_lane<3>(s);
+    const long long o = (long long)d * H + h;
+    const float sw = k.lp.s_w[o], mk = k.lp.s_mask[o];
+    const float Ws = softplus_t(sw) * mk;
+    if (q == 0) {
+      k.g.s_w[o] = s1 * mk * softplus_grad(sw);
+    } else if (q == 1) {
+      k.g.s_erev[o] = Ws * s2;
+    } else if (q == 2) {
+      k.g.s_mu[o] = -k.lp.s_sigma[o] * Ws * s3;
+    } else {
+      k.g.s_sigma[o] = Ws * (s4 - k.lp.s_mu[o] * s3);
+    }
     return;
   }
-  tid -= nsens;
-  if (tid < H) {
-    const int j = (int)tid;
-    const float* src = k.npart + j;
-    float sp[3];
-    sum_partials_planes<3>(src, Hp, 3LL * Hp, k.B, sp);
-    const float c = sp[0], gv = sp[1], ga = sp[2];
+  e -= nsens;
+  if (e < H) {
+    const int j = (int)e;
+    // three planes: C, G*v and the G*L term
+    const float s = q < 3 ? sum_partials_plane(k.npart + q * Hp + j, 3LL * Hp, k.B) : 0.f;
+    const float c = quad_lane<0>(s), gv = quad_lane<1>(s), ga = quad_lane<2>(s);
     const float gl = k.lp.gleak[j];
-    k.g.cm[j] = c / k.lp.dtU * softplus_grad(k.lp.cm[j]);
-    k.g.gleak[j] = (k.lp.vleak[j] * ga - gv) * softplus_grad(gl);
-    k.g.vleak[j] = softplus_t(gl) * ga;
+    if (q == 0)
+      k.g.cm[j] = c / k.lp.dtU * softplus_grad(k.lp.cm[j]);
+    else if (q == 1)
+      k.g.gleak[j] = (k.lp.vleak[j] * ga - gv) * softplus_grad(gl);
+    else if (q == 2)
+      k.g.vleak[j] = softplus_t(gl) * ga;
     return;
   }
-  tid -= H;
-  if (tid < D) {
-    const int d = (int)tid;
-    const float* src = k.lnpart + d;
-    float sp[4];
-    sum_partials_planes<4>(src, Dp, 4LL * Dp, k.NLN, sp);
-    k.g.input_w[d] = sp[0];
-    k.g.input_b[d] = sp[1];
-    k.g.ln_w[d] = sp[2];
-    k.g.ln_b[d] = sp[3];
+  e -= H;
+  if (e < D) {
+    const int d = (int)e;
+    const float s = sum_partials_plane(k.lnpart + q * Dp + d, 4LL * Dp, k.NLN);
+    float* dst = q == 0 ? k.g.input_w : (q == 1 ? k.g.input_b : (q == 2 ? k.g.ln_w : k.g.ln_b));
+    dst[d] = s;
   }
 }
 
@@ -4026,7 +4067,8 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
   }
   FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
              pt.nrec, p.NRC, nln, nullptr, nullptr, 0, 0};
-  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
+  // four threads per output element
+  const long long total = 4 * ((long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D);
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
@@ -4045,7 +4087,10 @@ hipError_t launch_finalize_leaf_fused(const Plan& p, const LeafParams& lp, const
   // one sensory and one LayerNorm partial per batch row (B <= 64)
   FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
              pt.nrec, p.B, p.B, status, gstate, nx, ns};
-  const long long total = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D + nx + ns;
+  // four threads per output element, or one per output (every leaf gradient,
+  // dL/dx and dL/dh0) when a gave-up status turns them all into NaN
+  const long long nel = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
+  const long long total = 4 * nel > nel + nx + ns ? 4 * nel : nel + nx + ns;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
