@@ -400,6 +400,15 @@ ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
   return pp;
 }
 
+// The compacted sensory forward image of the module forward (in its
+// workspace; nothing after the forward reads it).
+void carve_sens_cmp(const ltc::Plan& p, Carver& c, ltc::Prepped& pp) {
+  const long long n = (long long)p.Dp * p.Hp;
+  pp.sF = c.take<float4>(n);
+  pp.sFi = c.take<int>(n);
+  pp.sFn = c.take<int>((long long)(p.Dp / 64) * p.Hp);
+}
+
 // The fused row backward's exchange words and status word, after the images
 // in the module's saved buffer (cleared by the forward's prep launch).
 unsigned long long* carve_row_words(const ltc::Plan& p, Carver& c) {
@@ -784,6 +793,8 @@ long long ltc_module_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unf
   Carver c{nullptr};
   carve_fwd(p, c);
   carve_ln(p, c);  // used when nothing is saved (inference)
+  ltc::Prepped sc{};
+  carve_sens_cmp(p, c, sc);
   return round_up(c.off, 256);
 }
 
@@ -836,6 +847,8 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   Carver need{nullptr};
   carve_fwd(p, need);
   carve_ln(p, need);
+  ltc::Prepped scmp{};
+  carve_sens_cmp(p, need, scmp);
   if (workspace_bytes < need.off || (need.off > 0 && !workspace))
     return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
@@ -873,6 +886,8 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   auto al16 = [](const float* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   const bool sens_in_prep = ltc::prep_sens_fused(p) && al16(sensory_w) && al16(sensory_erev) &&
                             al16(sensory_mask) && al16(sensory_mu) && al16(sensory_sigma);
+  // otherwise the sensory launch reads the compacted image
+  if (!sens_in_prep) carve_sens_cmp(p, c, pp);
   hipError_t e;
   e = timed(ltc::K_PREP, s, [&] {
     return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s, row_words,

@@ -232,15 +232,16 @@ __device__ __forceinline__ void stream_rows(__amdgpu_buffer_rsrc_t rs, int lane_
 // active rows their entry numbers in ascending row order. With nch chunks,
 // entry e goes to chunk e % nch, slot e / nch, so a dense column gives every
 // chunk the rows ks, ks + nch, ... and all lanes of a chunk the same row per
-// slot. Slots past the column's count get zero operands and row 0.
+// slot. Slots past the column's count get zero operands and row 0. The image
+// has nrows rows (slots of all chunks) of `stride` columns.
 // ---------------------------------------------------------------------------
 template <class Op>
-__device__ __forceinline__ void compact_column(int col, int Hp, int nch, int lane, float4* cimg,
-                                               int* cidx, int* ccnt, Op op) {
-  const int sc = Hp / nch;
-  auto at = [&](int e) { return (long long)((e % nch) * sc + e / nch) * Hp + col; };
+__device__ __forceinline__ void compact_column(int col, int nrows, int stride, int nch, int lane,
+                                               float4* cimg, int* cidx, int* ccnt, Op op) {
+  const int sc = nrows / nch;
+  auto at = [&](int e) { return (long long)((e % nch) * sc + e / nch) * stride + col; };
   int n = 0;
-  for (int r0 = 0; r0 < Hp; r0 += 64) {
+  for (int r0 = 0; r0 < nrows; r0 += 64) {
     const int r = r0 + lane;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     bool act = false;
@@ -253,7 +254,7 @@ __device__ __forceinline__ void compact_column(int col, int Hp, int nch, int lan
     }
     n += __popcll(m);
   }
-  for (int e = n + lane; e < Hp; e += 64) {
+  for (int e = n + lane; e < nrows; e += 64) {
     const long long a = at(e);
     cimg[a] = make_float4(0.f, 0.f, 0.f, 0.f);
     cidx[a] = 0;
@@ -263,8 +264,9 @@ __device__ __forceinline__ void compact_column(int col, int Hp, int nch, int lan
 
 // Compacted columns a prep launch builds: Hp forward columns when cF is set,
 // then Hp chain columns when the chain image is built and cB is set.
-__host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, bool fwd, bool bwd) {
-  return ((fwd && pp.cF != nullptr) ? Hp : 0) + ((bwd && pp.cB != nullptr) ? Hp : 0);
+__host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, int Dp, bool fwd, bool bwd) {
+  return ((fwd && pp.cF != nullptr) ? Hp : 0) + ((bwd && pp.cB != nullptr) ? Hp : 0) +
+         ((fwd && pp.sF != nullptr) ? (Dp / 64) * Hp : 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -286,7 +288,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
     if (fwd_c) {
       if (col < Hp) {
         const int j = col;
-        compact_column(j, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+        compact_column(j, Hp, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
           if (i < H && j < H) {
             operand(i, j, v);
             act = v.z != 0.f || v.w != 0.f;
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
       // parameter gradients); the unfused one (bwd == 2, folded operands) only
       // those that add to dL/dv.
       const int i = col;
-      compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+      compact_column(i, Hp, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
         if (i < H && j < H) {
           operand(i, j, v);
           if (bwd == 2) {
@@ -462,6 +464,154 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
           const float a = gate(fmaf(pq[i].x, xr[r], pq[i].y));
           an[r] = fmaf(a, pq[i].z, an[r]);
           ad[r] = fmaf(a, pq[i].w, ad[r]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if constexpr (DS != 1) {
+    if (w > 0) {
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) part[w - 1][r][lane] = make_float2(an[r], ad[r]);
+    }
+    __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const float2 v = part[q][r][lane];
+        an[r] += v.x;
+        ad[r] += v.y;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int row = row0 + rw + r;
+    if (row < BT) {
+      sn[(long long)row * Hp + h] = an[r];
+      sd[(long long)row * Hp + h] = ad[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sensory forward over the compacted image (module path): sens_fwd_kernel's
+// layout and staging (lane -> neuron h, 64-input chunks of the rows staged in
+// LDS one chunk ahead), but in each chunk a lane walks only the inputs whose
+// weight is nonzero (sF, sFi: [chunk][64 slots][Hp], ascending input within
+// the chunk; sFn: [chunk][Hp] counts), so a wave runs as many slots as its
+// fullest neuron has entries in the chunk instead of 64, and each lane reads
+// its slot's input at its own LDS address. With DS = 4 the four waves take
+// quarters of each chunk's slots. Slots past a count hold zero operands
+// (input 0) and add zero.
+// ---------------------------------------------------------------------------
+template <int RPW, int DS>
+__global__ __launch_bounds__(256) void sens_fwd_cmp_kernel(const float* __restrict__ x, Strides3 xs,
+                                                           int T, int D, int BT, int Hp,
+                                                           const float4* __restrict__ sF,
+                                                           const int* __restrict__ sFi,
+                                                           const int* __restrict__ sFn,
+                                                           float* __restrict__ sn,
+                                                           float* __restrict__ sd) {
+  constexpr int ROWS = (DS == 1 ? 4 : 1) * RPW;
+  constexpr int XLD = ROWS + 4;  // padded staged row, 16-byte aligned
+  __shared__ __align__(16) float xsh[64 * XLD];
+  __shared__ float2 part[DS == 1 ? 1 : 3][RPW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane;
+  const int row0 = blockIdx.y * ROWS;
+  const int rw = DS == 1 ? w * RPW : 0;
+  float an[RPW], ad[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
+  // x staging as in sens_fwd_kernel: lane l of wave w loads input d0 + l of
+  // rows w, w + 4, ... one chunk ahead
+  constexpr int NXF = (ROWS + 3) / 4;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const float* xrow[NXF];
+#pragma unroll
+  for (int i = 0; i < NXF; ++i) {
+    const int r = wu + 4 * i, row = row0 + r;
+    xrow[i] = nullptr;
+    if (r < ROWS && row < BT) {
+      const int b = row / T, t = row - b * T;
+      xrow[i] = x + b * xs.b + t * xs.t;
+    }
+  }
+  float xv[NXF];
+  auto fetch = [&](int d0) {
+    const int d = d0 + lane;
+    const long long off = (long long)d * xs.c;
+#pragma unroll
+    for (int i = 0; i < NXF; ++i) xv[i] = *((xrow[i] != nullptr && d < D) ? xrow[i] + off : x);
+  };
+  if (D > 0) fetch(0);
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    const bool dok = d0 + lane < D;
+#pragma unroll
+    for (int i = 0; i < NXF; ++i)
+      if (wu + 4 * i < ROWS)
+        xsh[lane * XLD + wu + 4 * i] = (dok && xrow[i] != nullptr) ? xv[i] : 0.f;
+    const long long cb = (long long)(d0 >> 6) * 64 * Hp;
+    // this chunk's slots of the wave, in groups of four
+    const int nsw = (wave_max(sFn[(d0 >> 6) * Hp + h]) + 3) & ~3;
+    int s0 = 0, s1 = nsw;
+    if constexpr (DS != 1) {
+      const int q = ((nsw + 4 * DS - 1) / (4 * DS)) * 4;
+      s0 = min(nsw, w * q);
+      s1 = min(nsw, s0 + q);
+    }
+    __syncthreads();
+    fetch(d0 + 64);
+    if (s0 < s1) {
+      const float4* pcol = sF + cb + h;
+      const int* icol = sFi + cb + h;
+      float4 pc[4], pn[4];
+      int dc[4], dn[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pc[i] = pcol[(long long)(s0 + i) * Hp];
+        dc[i] = icol[(long long)(s0 + i) * Hp];
+      }
+      for (int s = s0; s < s1; s += 4) {
+        // the next group's operands travel while this one is evaluated (the
+        // last group reloads itself)
+        const int sn4 = s + 4 < s1 ? s + 4 : s;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pn[i] = pcol[(long long)(sn4 + i) * Hp];
+          dn[i] = icol[(long long)(sn4 + i) * Hp];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float* xr = xsh + dc[i] * XLD + rw;
+          float xq[RPW];
+          if constexpr (RPW % 4 == 0) {
+#pragma unroll
+            for (int r = 0; r < RPW; r += 4) {
+              const float4 q4 = *reinterpret_cast<const float4*>(xr + r);
+              xq[r] = q4.x;
+              xq[r + 1] = q4.y;
+              xq[r + 2] = q4.z;
+              xq[r + 3] = q4.w;
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) xq[r] = xr[r];
+          }
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) {
+            const float a = gate(fmaf(pc[i].x, xq[r], pc[i].y));
+            an[r] = fmaf(a, pc[i].z, an[r]);
+            ad[r] = fmaf(a, pc[i].w, ad[r]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pc[i] = pn[i];
+          dc[i] = dn[i];
         }
       }
     }
@@ -2468,7 +2618,7 @@ __global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(
     if (pp.cF != nullptr) {
       if (col < Hp) {
         const int j = col;
-        compact_column(j, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
+        compact_column(j, Hp, Hp, nchf, lane, pp.cF, pp.cFi, pp.cFn, [&](int i, float4& v, bool& act) {
           if (i < H && j < H) {
             operand(i, j, v);
             act = v.z != 0.f || v.w != 0.f;
@@ -2478,21 +2628,42 @@ __global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(
       }
       col -= Hp;
     }
-    if (recb && pp.cB != nullptr && col < Hp) {
-      // The fused chain (recb == 1) keeps the synapses whose mask entry is
-      // nonzero; the unfused one (recb == 2, folded operands) those that add
-      // to dL/dv.
-      const int i = col;
-      compact_column(i, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
-        if (i < H && j < H) {
-          if (recb == 2) {
-            operand(i, j, v);
-            v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
-            act = v.z != 0.f || v.w != 0.f;
-          } else if (lp.mask[(long long)i * H + j] != 0.f) {
-            operand(i, j, v);
-            act = true;
+    if (recb && pp.cB != nullptr) {
+      if (col < Hp) {
+        // The fused chain (recb == 1) keeps the synapses whose mask entry is
+        // nonzero; the unfused one (recb == 2, folded operands) those that
+        // add to dL/dv.
+        const int i = col;
+        compact_column(i, Hp, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+          if (i < H && j < H) {
+            if (recb == 2) {
+              operand(i, j, v);
+              v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
+              act = v.z != 0.f || v.w != 0.f;
+            } else if (lp.mask[(long long)i * H + j] != 0.f) {
+              operand(i, j, v);
+              act = true;
+            }
           }
+        });
+        return;
+      }
+      col -= Hp;
+    }
+    if (pp.sF != nullptr && col < (Dp / 64) * Hp) {
+      // Sensory forward, one wave per (64-input chunk, neuron h): the inputs
+      // of the chunk whose weight for h is nonzero.
+      const int c = col / Hp, h = col - c * Hp;
+      const long long cb = (long long)c * 64 * Hp;
+      compact_column(h, 64, Hp, 1, lane, pp.sF + cb, pp.sFi + cb, pp.sFn + (long long)c * Hp,
+                     [&](int dl, float4& v, bool& act) {
+        const int d = c * 64 + dl;
+        if (d < D && h < H) {
+          const long long e = (long long)d * H + h;
+          const float Ss = lp.s_sigma[e], Ms = lp.s_mu[e];
+          const float Ws = softplus_t(lp.s_w[e]) * lp.s_mask[e];
+          v = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * lp.s_erev[e], Ws);
+          act = Ws != 0.f;
         }
       });
     }
@@ -3753,7 +3924,7 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   if (total == 0) return hipSuccess;
   const int nflat = (int)((total + 255) / 256);
   const bool rec = (segs & kPrepRec) != 0;
-  const int ncmp = (cmp_columns(pp, p.Hp, rec, rec && bwd) + 3) / 4;
+  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, rec, rec && bwd) + 3) / 4;
   hipLaunchKernelGGL(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
                      p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat, cmp_chunks_fwd(p),
                      cmp_chunks_bwd(p));
@@ -3806,7 +3977,16 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
   const bool split_d = geo.split_d;
   const int rpw = geo.rpw, rows_of = split_d ? 1 : 4;
   const dim3 grid(hb, (BT + rows_of * rpw - 1) / (rows_of * rpw));
-#define LTC_SENS(R, DSV) hipLaunchKernelGGL((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, p.Hp, pp.sensF, sn, sd)
+#define LTC_SENS(R, DSV)                                                                        \
+  do {                                                                                          \
+    if (pp.sF != nullptr)                                                                       \
+      hipLaunchKernelGGL((sens_fwd_cmp_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
+                         p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd);                                  \
+    else                                                                                        \
+      hipLaunchKernelGGL((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT,     \
+                         p.Hp, pp.sensF, sn, sd);                                               \
+  } while (0)
+  if (pp.sF != nullptr && (pp.sFi == nullptr || pp.sFn == nullptr)) return hipErrorInvalidValue;
   if (split_d) {
     switch (rpw) {
       case 8: LTC_SENS(8, 4); break;
@@ -4005,9 +4185,10 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   const bool bwd = (images & kLeafBwdImages) != 0;
   const int wpb = threads / 64;  // compacted columns per block, one per wave
-  const int ncmp = (cmp_columns(pp, p.Hp, true, bwd) + wpb - 1) / wpb;
-  // With the sensory sums formed in the row blocks, nothing reads sensF.
-  const int sensf = (images & kLeafFwdImages) && !fs ? 1 : 0;
+  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, true, bwd) + wpb - 1) / wpb;
+  // With the sensory sums formed in the row blocks, or the sensory launch
+  // reading the compacted image, nothing reads sensF.
+  const int sensf = (images & kLeafFwdImages) && !fs && pp.sF == nullptr ? 1 : 0;
 #define LTC_PREPL(C, F)                                                                           \
   hipLaunchKernelGGL((prep_leaf_kernel<C, F>), dim3(nprep + ncmp + nln), dim3(threads), 0, s, lp, pp, \
                      p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, sensf, bwd ? 1 : 0, nprep, \

@@ -94,6 +94,13 @@ struct Prepped {
   float4* cB;
   int* cBi;
   int* cBn;
+  // Compacted sensory forward image (module path): per 64-input chunk and
+  // neuron h, the chunk's inputs whose sensory weight for h is nonzero,
+  // ascending, as [chunk][64 slots][Hp] operands and input indices within
+  // the chunk, and [chunk][Hp] counts.
+  float4* sF;
+  int* sFi;
+  int* sFn;
 };
 // Chunks (and slots per chunk) of a compacted image column at Hp = 256.
 constexpr int kCmpChunks = 16;

@@ -1,0 +1,97 @@
+"""The module forward's sensory launch over the compacted sensory image.
+
+When the sensory sums are not formed in the prep launch, ltc_module_forward
+builds, per 64-input chunk and neuron, the list of inputs whose sensory weight
+is nonzero (in the prep launch) and the sensory launch walks only those. These
+tests set the sensory mask so that the lists take every edge the layout has:
+a neuron with no input at all, a neuron with every input, a chunk that is
+full for one neuron and empty for the next, a ragged last chunk (D not a
+multiple of 64) and a single input, on both thread layouts of the launch (four
+row groups per workgroup, and few rows with the inputs split over the waves),
+with contiguous and strided x. Forward and gradients are compared with the
+float64 oracle at the reference's bars (forward max-abs 1e-3, gradients rtol
+5e-2 / atol 1e-2, plus the per-tensor bar of 2e-3 of the largest entry).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import ltc_cuda
+from _gpu_common import DEV, _native, _oracle_module_grads, _perturbed_module  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+# (B, T, D, H, strided x)
+CASES = [
+    (40, 8, 130, 72, False),  # four row groups per workgroup, ragged third chunk
+    (40, 8, 130, 72, True),
+    (2, 3, 200, 40, False),   # few rows: the inputs split over the waves
+    (300, 2, 1, 8, False),    # one input
+]
+
+
+def _edge_mask(D, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    m = (torch.rand(D, H, generator=g) < 0.5).float()
+    m[:, 0] = 0.0          # a neuron with no input
+    if H > 1:
+        m[:, 1] = 1.0      # a neuron with every input
+    if D > 64 and H > 6:
+        m[64:128, 5] = 1.0  # second chunk full for neuron 5 ...
+        m[64:128, 6] = 0.0  # ... and empty for neuron 6
+    return m
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "B%dT%dD%dH%d%s" % (c[:4] + ("s" if c[4] else "",)))
+def test_compacted_sensory_forward_matches_oracle(case):
+    B, T, D, H, strided = case
+    plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
+    assert plan["module_sens_in_prep"] == 0, plan
+    m = _perturbed_module(D, H, seed=5 * D + H).to(DEV)
+    with torch.no_grad():
+        m.sensory_sparsity_mask.copy_(_edge_mask(D, H, seed=D + H).to(DEV))
+    g = torch.Generator().manual_seed(B * T + D)
+    x = torch.randn(B, T, D, generator=g)
+    h0 = torch.randn(B, H, generator=g) * 0.2
+    G = torch.randn(B, T, H, generator=g)
+    Gh = torch.randn(B, H, generator=g)
+    if strided:
+        wide = torch.zeros(B, T, 2 * D)
+        wide[:, :, 0::2] = x
+        xg = wide.to(DEV)[:, :, 0::2].requires_grad_(True)
+        assert not xg.is_contiguous()
+    else:
+        xg = x.to(DEV).requires_grad_(True)
+    hg = h0.to(DEV).requires_grad_(True)
+    out, (h, _) = m(xg, (hg, hg))
+    ((out * G.to(DEV)).sum() + (h * Gh.to(DEV)).sum()).backward()
+    r_out, r_h, r_g, r_gx, r_gh = _oracle_module_grads(m, x, h0, G, Gh)
+    e_out = (out.detach().cpu().double() - r_out).abs().max().item()
+    e_h = (h.detach().cpu().double() - r_h).abs().max().item()
+    print(f"compacted sensory {case}: out err {e_out:.2e} h err {e_h:.2e}", flush=True)
+    assert e_out <= 1e-3 and e_h <= 1e-3
+    names = ["x", "h0"] + [n for n, _ in m.named_parameters()]
+    got = [xg.grad.cpu(), hg.grad.cpu()] + [p.grad.cpu() for _, p in m.named_parameters()]
+    ref = [r_gx, r_gh] + [r_g[n] for n, _ in m.named_parameters()]
+    for n, a, r in zip(names, got, ref):
+        r = r.double()
+        err = (a.double() - r).abs().max().item()
+        assert torch.isfinite(a).all(), n
+        assert torch.allclose(a.double(), r, rtol=5e-2, atol=1e-2), f"{n}: err {err:.2e}"
+        assert err <= 2e-3 * r.abs().max().item() + 1e-6, f"{n}: err {err:.2e}"
+
+
+def test_compacted_sensory_forward_no_grad_matches_training_forward():
+    """The no-grad forward (its images in the workspace, C5's form) and the
+    training forward (images in the saved buffer) read the same compacted
+    sensory image and agree bit for bit."""
+    B, T, D, H = 128, 4, 96, 64
+    assert ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)["module_sens_in_prep"] == 0
+    m = _perturbed_module(D, H, seed=11).to(DEV)
+    x = torch.randn(B, T, D, generator=torch.Generator().manual_seed(12)).to(DEV)
+    with torch.no_grad():
+        a, (ha, _) = m(x)
+    b, (hb, _) = m(x.clone().requires_grad_(True))
+    assert torch.equal(a, b.detach()) and torch.equal(ha, hb.detach())
