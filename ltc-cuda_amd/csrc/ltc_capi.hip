@@ -308,7 +308,19 @@ struct FwdWs {
   ltc::ClusterBuf cb;
 };
 
-FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
+// The compacted sensory forward image (per 64-input chunk and neuron, the
+// inputs with a nonzero sensory weight), which the forward's sensory launch
+// reads instead of the dense image.
+void carve_sens_cmp(const ltc::Plan& p, Carver& c, ltc::Prepped& pp) {
+  const long long n = (long long)p.Dp * p.Hp;
+  pp.sF = c.take<float4>(n);
+  pp.sFi = c.take<int>(n);
+  pp.sFn = c.take<int>((long long)(p.Dp / 64) * p.Hp);
+}
+
+// sens: with the compacted sensory image (every forward that runs the
+// sensory launch).
+FwdWs carve_fwd(const ltc::Plan& p, Carver& c, bool sens = true) {
   FwdWs w{};
   w.pp.recF = c.take<float4>(image_rows(p) * p.Hp);
   w.pp.sensF = c.take<float4>((long long)p.Dp * p.Hp);
@@ -317,6 +329,7 @@ FwdWs carve_fwd(const ltc::Plan& p, Carver& c) {
   w.sn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.sd = c.take<float>((long long)p.B * p.T * p.Hp);
   w.cb = carve_cluster(p, c, false);
+  if (sens) carve_sens_cmp(p, c, w.pp);
   return w;
 }
 
@@ -398,15 +411,6 @@ ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
   pp.neuron = c.take<float>(3LL * p.Hp);
   carve_cmp(p, c, pp, true, true);
   return pp;
-}
-
-// The compacted sensory forward image of the module forward (in its
-// workspace; nothing after the forward reads it).
-void carve_sens_cmp(const ltc::Plan& p, Carver& c, ltc::Prepped& pp) {
-  const long long n = (long long)p.Dp * p.Hp;
-  pp.sF = c.take<float4>(n);
-  pp.sFi = c.take<int>(n);
-  pp.sFn = c.take<int>((long long)(p.Dp / 64) * p.Hp);
 }
 
 // The fused row backward's exchange words and status word, after the images
@@ -793,8 +797,6 @@ long long ltc_module_fwd_workspace_bytes(int B, int T, int D, int H, int ode_unf
   Carver c{nullptr};
   carve_fwd(p, c);
   carve_ln(p, c);  // used when nothing is saved (inference)
-  ltc::Prepped sc{};
-  carve_sens_cmp(p, c, sc);
   return round_up(c.off, 256);
 }
 
@@ -847,8 +849,6 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   Carver need{nullptr};
   carve_fwd(p, need);
   carve_ln(p, need);
-  ltc::Prepped scmp{};
-  carve_sens_cmp(p, need, scmp);
   if (workspace_bytes < need.off || (need.off > 0 && !workspace))
     return fail(LTC_EINVAL, "workspace too small: need " + std::to_string(need.off) + " bytes");
   if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
@@ -886,8 +886,10 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   auto al16 = [](const float* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
   const bool sens_in_prep = ltc::prep_sens_fused(p) && al16(sensory_w) && al16(sensory_erev) &&
                             al16(sensory_mask) && al16(sensory_mu) && al16(sensory_sigma);
-  // otherwise the sensory launch reads the compacted image
-  if (!sens_in_prep) carve_sens_cmp(p, c, pp);
+  // otherwise the sensory launch reads the compacted image (in the workspace)
+  pp.sF = sens_in_prep ? nullptr : wfw.pp.sF;
+  pp.sFi = sens_in_prep ? nullptr : wfw.pp.sFi;
+  pp.sFn = sens_in_prep ? nullptr : wfw.pp.sFn;
   hipError_t e;
   e = timed(ltc::K_PREP, s, [&] {
     return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s, row_words,
@@ -1086,7 +1088,7 @@ struct UnfoldWs {
 
 UnfoldWs carve_unfold(const ltc::Plan& p, Carver& c, bool bwd) {
   UnfoldWs w{};
-  w.f = carve_fwd(p, c);
+  w.f = carve_fwd(p, c, false);
   if (bwd) {
     w.b = carve_bwd(p, c);
     w.hscr = c.take<float>((long long)p.B * p.H);

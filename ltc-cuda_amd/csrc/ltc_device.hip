@@ -264,9 +264,28 @@ __device__ __forceinline__ void compact_column(int col, int nrows, int stride, i
 
 // Compacted columns a prep launch builds: Hp forward columns when cF is set,
 // then Hp chain columns when the chain image is built and cB is set.
-__host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, int Dp, bool fwd, bool bwd) {
+__host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, int Dp, bool fwd, bool bwd,
+                                            bool sens) {
   return ((fwd && pp.cF != nullptr) ? Hp : 0) + ((bwd && pp.cB != nullptr) ? Hp : 0) +
-         ((fwd && pp.sF != nullptr) ? (Dp / 64) * Hp : 0);
+         ((sens && pp.sF != nullptr) ? (Dp / 64) * Hp : 0);
+}
+
+// Compacted sensory forward column (one wave per 64-input chunk c and neuron
+// h): the chunk's inputs whose sensory weight for h is nonzero, with the
+// forward operands op(d) gives.
+template <class Op>
+__device__ __forceinline__ void compact_sens_column(const Prepped& pp, int col, int Hp, int D,
+                                                    int H, int lane, Op op) {
+  const int c = col / Hp, h = col - c * Hp;
+  const long long cb = (long long)c * 64 * Hp;
+  compact_column(h, 64, Hp, 1, lane, pp.sF + cb, pp.sFi + cb, pp.sFn + (long long)c * Hp,
+                 [&](int dl, float4& v, bool& act) {
+                   const int d = c * 64 + dl;
+                   if (d < D && h < H) {
+                     v = op((long long)d * H + h);
+                     act = v.w != 0.f;
+                   }
+                 });
 }
 
 // ---------------------------------------------------------------------------
@@ -298,21 +317,31 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
       }
       col -= Hp;
     }
-    if (bwd && (segs & kPrepRec) && pp.cB != nullptr && col < Hp) {
-      // The fused chain (bwd == 1) keeps every real synapse (it also forms the
-      // parameter gradients); the unfused one (bwd == 2, folded operands) only
-      // those that add to dL/dv.
-      const int i = col;
-      compact_column(i, Hp, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
-        if (i < H && j < H) {
-          operand(i, j, v);
-          if (bwd == 2) {
-            v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
-            act = v.z != 0.f || v.w != 0.f;
-          } else {
-            act = true;
+    if (bwd && (segs & kPrepRec) && pp.cB != nullptr) {
+      if (col < Hp) {
+        // The fused chain (bwd == 1) keeps every real synapse (it also forms
+        // the parameter gradients); the unfused one (bwd == 2, folded
+        // operands) only those that add to dL/dv.
+        const int i = col;
+        compact_column(i, Hp, Hp, nchb, lane, pp.cB, pp.cBi, pp.cBn, [&](int j, float4& v, bool& act) {
+          if (i < H && j < H) {
+            operand(i, j, v);
+            if (bwd == 2) {
+              v = make_float4(v.x, v.y, v.x * v.z, v.x * v.w);
+              act = v.z != 0.f || v.w != 0.f;
+            } else {
+              act = true;
+            }
           }
-        }
+        });
+        return;
+      }
+      col -= Hp;
+    }
+    if ((segs & kPrepSens) && pp.sF != nullptr && col < (Dp / 64) * Hp) {
+      compact_sens_column(pp, col, Hp, D, H, lane, [&](long long e) {
+        const float Ss = rp.s_sigma[e], Ms = rp.s_mu[e], Ws = rp.s_wpos[e];
+        return make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * rp.s_erev[e], Ws);
       });
     }
     return;
@@ -346,7 +375,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
     }
     if (bwd)
       pp.sensB[(long long)h * Dp + d] = g;
-    else
+    else if (pp.sF == nullptr)  // the compacted image replaces the dense one
       pp.sensF[tid] = f;
     return;
   }
@@ -2651,20 +2680,10 @@ __global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(
       col -= Hp;
     }
     if (pp.sF != nullptr && col < (Dp / 64) * Hp) {
-      // Sensory forward, one wave per (64-input chunk, neuron h): the inputs
-      // of the chunk whose weight for h is nonzero.
-      const int c = col / Hp, h = col - c * Hp;
-      const long long cb = (long long)c * 64 * Hp;
-      compact_column(h, 64, Hp, 1, lane, pp.sF + cb, pp.sFi + cb, pp.sFn + (long long)c * Hp,
-                     [&](int dl, float4& v, bool& act) {
-        const int d = c * 64 + dl;
-        if (d < D && h < H) {
-          const long long e = (long long)d * H + h;
-          const float Ss = lp.s_sigma[e], Ms = lp.s_mu[e];
-          const float Ws = softplus_t(lp.s_w[e]) * lp.s_mask[e];
-          v = make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * lp.s_erev[e], Ws);
-          act = Ws != 0.f;
-        }
+      compact_sens_column(pp, col, Hp, D, H, lane, [&](long long e) {
+        const float Ss = lp.s_sigma[e], Ms = lp.s_mu[e];
+        const float Ws = softplus_t(lp.s_w[e]) * lp.s_mask[e];
+        return make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * lp.s_erev[e], Ws);
       });
     }
     return;
@@ -3924,7 +3943,7 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   if (total == 0) return hipSuccess;
   const int nflat = (int)((total + 255) / 256);
   const bool rec = (segs & kPrepRec) != 0;
-  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, rec, rec && bwd) + 3) / 4;
+  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, rec, rec && bwd, (segs & kPrepSens) != 0) + 3) / 4;
   hipLaunchKernelGGL(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
                      p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat, cmp_chunks_fwd(p),
                      cmp_chunks_bwd(p));
@@ -4185,7 +4204,7 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   LnBuf lb = ln ? *ln : LnBuf{nullptr, {0, 0, 0}, nullptr, nullptr};
   const bool bwd = (images & kLeafBwdImages) != 0;
   const int wpb = threads / 64;  // compacted columns per block, one per wave
-  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, true, bwd) + wpb - 1) / wpb;
+  const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, true, bwd, true) + wpb - 1) / wpb;
   // With the sensory sums formed in the row blocks, or the sensory launch
   // reading the compacted image, nothing reads sensF.
   const int sensf = (images & kLeafFwdImages) && !fs && pp.sF == nullptr ? 1 : 0;

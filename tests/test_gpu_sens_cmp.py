@@ -1,8 +1,9 @@
-"""The module forward's sensory launch over the compacted sensory image.
+"""The sensory launch over the compacted sensory image.
 
-When the sensory sums are not formed in the prep launch, ltc_module_forward
-builds, per 64-input chunk and neuron, the list of inputs whose sensory weight
-is nonzero (in the prep launch) and the sensory launch walks only those. These
+When the sensory sums are not formed in the prep launch, the forward
+(ltc_module_forward, and ltc_full_forward behind the eval-mode module) builds,
+per 64-input chunk and neuron, the list of inputs whose sensory weight is
+nonzero (in the prep launch) and the sensory launch walks only those. These
 tests set the sensory mask so that the lists take every edge the layout has:
 a neuron with no input at all, a neuron with every input, a chunk that is
 full for one neuron and empty for the next, a ragged last chunk (D not a
@@ -95,3 +96,25 @@ def test_compacted_sensory_forward_no_grad_matches_training_forward():
         a, (ha, _) = m(x)
     b, (hb, _) = m(x.clone().requires_grad_(True))
     assert torch.equal(a, b.detach()) and torch.equal(ha, hb.detach())
+
+
+@pytest.mark.parametrize("shape", [(40, 8, 130, 72), (2, 3, 200, 40)], ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_compacted_sensory_forward_boundary_path_matches_oracle(shape):
+    """The same edge masks through ltc_full_forward: in eval mode the module
+    calls the boundary with its cached transforms, whose prep launch builds
+    the compacted lists from the masked sensory weights."""
+    B, T, D, H = shape
+    m = _perturbed_module(D, H, seed=3 * D + H).to(DEV)
+    with torch.no_grad():
+        m.sensory_sparsity_mask.copy_(_edge_mask(D, H, seed=2 * D + H).to(DEV))
+    m.eval()
+    g = torch.Generator().manual_seed(B + T + D)
+    x = torch.randn(B, T, D, generator=g)
+    h0 = torch.randn(B, H, generator=g) * 0.2
+    with torch.no_grad():
+        out, (h, _) = m(x.to(DEV), (h0.to(DEV), h0.to(DEV)))
+    r_out, r_h, _, _, _ = _oracle_module_grads(m, x, h0, torch.zeros(B, T, H), torch.zeros(B, H))
+    e_out = (out.cpu().double() - r_out).abs().max().item()
+    e_h = (h.cpu().double() - r_h).abs().max().item()
+    print(f"compacted sensory, boundary {shape}: out err {e_out:.2e} h err {e_h:.2e}", flush=True)
+    assert e_out <= 1e-3 and e_h <= 1e-3
