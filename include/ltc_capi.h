@@ -302,12 +302,14 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * the module path's chain), then two module-path fields: 1 when the
  * forward's parameter-image launch also forms the sensory sums (few rows,
  * D <= 128, H a multiple of 4, and 16-byte aligned sensory leaves at the
- * call: no separate sensory launch), and 1 when the backward runs the
- * sensory and LayerNorm backward inside the chain launch. Returns the number
- * of values written, or -1 for invalid sizes. The plan depends on the
- * current device's CU count.
+ * call: no separate sensory launch), 1 when the backward runs the sensory
+ * and LayerNorm backward inside the chain launch (Hp = 64), and 1 when it
+ * forms the recurrent parameter-gradient sums inside the chain launch
+ * (Hp = 128: no separate recurrent-gradient launch). Returns the number of
+ * values written, or -1 for invalid sizes. The plan depends on the current
+ * device's CU count.
  */
-#define LTC_PLAN_FIELDS 24
+#define LTC_PLAN_FIELDS 25
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

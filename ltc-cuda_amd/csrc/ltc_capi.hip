@@ -362,7 +362,10 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
   w.dsn = c.take<float>((long long)p.B * p.T * p.Hp);
   w.dsd = c.take<float>((long long)p.B * p.T * p.Hp);
   w.npart = c.take<float>((long long)p.B * 3 * p.Hp);
-  w.rpart = c.take<float>((long long)p.NCH * 4 * p.Hp * p.Hp);
+  // recurrent partials: NCH chunks, or one per batch row (Hp = 128 chain with
+  // recurrent-gradient companions)
+  const long long nch = ltc::row128_rec_fused(p) && p.B > p.NCH ? p.B : p.NCH;
+  w.rpart = c.take<float>(nch * 4 * p.Hp * p.Hp);
   // sensory partials: NRC row chunks, or one per batch row (fused row backward)
   const long long nrc = ltc::row_bwd_fused(p) && p.B > p.NRC ? p.B : p.NRC;
   w.spart = c.take<float>(nrc * 4 * p.Dp * p.Hp);
@@ -416,7 +419,8 @@ ltc::Prepped carve_images(const ltc::Plan& p, Carver& c) {
 // The fused row backward's exchange words and status word, after the images
 // in the module's saved buffer (cleared by the forward's prep launch).
 unsigned long long* carve_row_words(const ltc::Plan& p, Carver& c) {
-  return ltc::row_bwd_fused(p) ? c.take<unsigned long long>(ltc::row_bwd_words(p)) : nullptr;
+  const long long n = ltc::row_bwd_words(p);
+  return n > 0 ? c.take<unsigned long long>(n) : nullptr;
 }
 
 long long module_saved_floats(const ltc::Plan& p) {
@@ -989,7 +993,7 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   const float* vsave = saved;
   const float* densave = saved + ((long long)T * ode_unfolds + 1) * B * p.Hp;
   hipError_t e;
-  if (row_words != nullptr) {
+  if (ltc::row_bwd_fused(p)) {
     // The sensory and LayerNorm backward run inside the chain launch.
     const ltc::RowCompanion rc{lw.xa, ln, input_w, ln_weight, ln_bias, wb.spart, lnpart,
                                grad_x, row_words, g_spin.load(std::memory_order_relaxed)};
@@ -1006,15 +1010,33 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     if (e != hipSuccess) return hip_fail("finalize launch", e);
     return LTC_OK;
   }
-  e = timed(ltc::K_ODE_BWD, s, [&] {
-    return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.absave,
-                               wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, wb.cb, s);
-  });
-  if (e != hipSuccess) return hip_fail("ODE backward launch", e);
-  if (!p.FUSE) {
-    e = timed(ltc::K_REC_GRAD, s,
-              [&] { return ltc::launch_rec_grad(p, wb.pp, vsave, wb.absave, wb.rpart, s); });
-    if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+  // At Hp = 128 (one row per workgroup) the recurrent-gradient sums are formed
+  // inside the chain launch by companion workgroups: one partial per row.
+  ltc::Plan pf = p;
+  const int* status = nullptr;
+  if (ltc::row128_rec_fused(p)) {
+    unsigned long long* words = row_words;
+    e = timed(ltc::K_ODE_BWD, s, [&] {
+      return ltc::launch_ode_bwd_row128_rec(p, wb.pp, vsave, densave, grad_out, gs,
+                                            grad_h_final, wb.dsn, wb.dsd, wb.npart, grad_state,
+                                            wb.rpart, words,
+                                            g_spin.load(std::memory_order_relaxed), s);
+    });
+    if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+    pf.NCH = p.B;
+    status = reinterpret_cast<const int*>(words + ltc::row_bwd_words(p) - 1);
+  } else {
+    e = timed(ltc::K_ODE_BWD, s, [&] {
+      return ltc::launch_ode_bwd(p, wb.pp, vsave, densave, grad_out, gs, grad_h_final,
+                                 wb.absave, wb.dsn, wb.dsd, wb.npart, grad_state, wb.rpart, wb.cb,
+                                 s);
+    });
+    if (e != hipSuccess) return hip_fail("ODE backward launch", e);
+    if (!p.FUSE) {
+      e = timed(ltc::K_REC_GRAD, s,
+                [&] { return ltc::launch_rec_grad(p, wb.pp, vsave, wb.absave, wb.rpart, s); });
+      if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
+    }
   }
   e = timed(ltc::K_SENS_BWD, s, [&] {
     return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s);
@@ -1024,7 +1046,8 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
             [&] { return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s); });
   if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
   e = timed(ltc::K_FINALIZE, s, [&] {
-    return ltc::launch_finalize_leaf(p, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s);
+    return ltc::launch_finalize_leaf(pf, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s,
+                                     status, grad_state);
   });
   if (e != hipSuccess) return hip_fail("finalize launch", e);
   if (p.CP > 0) {
@@ -1412,7 +1435,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,
       ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0, ltc::prep_sens_fused(p) ? 1 : 0,
-      ltc::row_bwd_fused(p) ? 1 : 0};
+      ltc::row_bwd_fused(p) ? 1 : 0, ltc::row128_rec_fused(p) ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -966,9 +966,15 @@ struct BwdK {
   const float4* cimg;
   const int* cidx;
   const int* ccnt;
-  // Fused row backward: dL/dsn, dL/dsd of each (row, step) go out as words
-  // [B*T][2][64] with tag 1 instead of into dsn / dsd.
+  // Exchange words with tag 1: the fused row backward (Hp = 64) sends dL/dsn,
+  // dL/dsd of each (row, step) as [B*T][2][64] words instead of into dsn /
+  // dsd; the Hp = 128 chain with recurrent-gradient companions sends each
+  // unfold's alpha/beta as [B][T*U][2][128] words instead of into absave.
   unsigned long long* rbw;
+  // The recurrent-gradient companions: the forward image {S', c', WE, WP} and
+  // their wait budget.
+  const float4* recF;
+  long long spin;
 };
 
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
@@ -1775,7 +1781,13 @@ __device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4
     }
     if (lead) {
       abs_[P * HP + i] = make_float2(al, be);
-      k.absave[(n * B + b0) * HP + i] = make_float2(al, be);
+      if (k.rbw != nullptr) {
+        unsigned long long* wd = k.rbw + ((long long)b0 * T * U + n) * 2 * HP + i;
+        xch_put(wd, al, 1u);
+        xch_put(wd + HP, be, 1u);
+      } else {
+        k.absave[(n * B + b0) * HP + i] = make_float2(al, be);
+      }
       accA += al;
       accB += be;
       pC += al * (cvk - cvk1);
@@ -1831,9 +1843,118 @@ __device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4
   }
 }
 
+// Companion of the Hp = 128 chain for batch row b and the postsynaptic
+// neurons j in [64 jt, 64 jt + 64) (module path): the recurrent
+// parameter-gradient sums of rec_grad_kernel for the row, formed while the
+// row's chain workgroup publishes each unfold's alpha/beta (latest unfold
+// first). 8 waves; lane l of wave w holds the 16 synapses (i = 16w + s,
+// j = 64 jt + l) with their forward operands and the four sums
+// {sum alpha*a, sum beta*a, sum d, sum d*v_i}, d = (alpha*WE + beta*WP) a(1-a),
+// in registers. Per unfold 128 threads wait for the 64 alpha/beta pairs while
+// 128 others stage v_i of the unfold's pre-state; one barrier per unfold (two
+// LDS buffers by unfold parity). At the end the companion writes its half of
+// the row's partial [b][4][Hp][Hp] and returns its words to tag 0, so a second
+// backward over the same forward waits for its own. A wait that runs out of
+// the budget sets the status word (after the words) and the companion writes
+// no partial; the finalize then writes NaN into every output.
+template <bool FULL>
+__device__ __forceinline__ void rec_companion128(const BwdK& k, int b, int jt) {
+  constexpr int HP = 128;
+  extern __shared__ float4 lds4[];
+  float2* ab = reinterpret_cast<float2*>(lds4);       // [2][64] alpha/beta of the unfold
+  float* vv = reinterpret_cast<float*>(ab + 2 * 64);  // [2][HP] v_i of the unfold
+  int* flag = reinterpret_cast<int*>(vv + 2 * HP);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int j = jt * 64 + lane;
+  const long long N = (long long)k.T * k.U;
+  const int B = k.B;
+  float4 q[16], acc[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    q[r] = k.recF[(long long)(16 * w + r) * HP + j];
+    acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tid == 0) *flag = 0;
+  __syncthreads();
+  unsigned long long* words = k.rbw + (long long)b * N * 2 * HP;
+  for (long long n = N - 1; n >= 0; --n) {
+    const int par = (int)(n & 1);
+    if (tid < 128) {
+      const int qq = tid >> 6;  // 0: alpha, 1: beta
+      unsigned long long* wd = words + (n * 2 + qq) * HP + jt * 64 + lane;
+      bool ok = k.spin > 0;
+      unsigned long long v = 0;
+      if (ok) {
+        v = xch_get(wd);
+        const long long t0 = wall_clock64();
+        while ((unsigned)(v >> 32) != 1u) {
+          if (wall_clock64() - t0 > k.spin) {
+            ok = false;
+            break;
+          }
+          v = xch_get(wd);
+        }
+      }
+      reinterpret_cast<float*>(ab + par * 64)[lane * 2 + qq] = __uint_as_float((unsigned)v);
+      if (!ok) *flag = 1;
+    } else if (tid < 256) {
+      const int i = tid - 128;
+      vv[par * HP + i] = k.vsave[(n * B + b) * HP + i];
+    }
+    __syncthreads();
+    if (*flag) break;
+    const float2 c = ab[par * 64 + lane];
+    const float* vr = vv + par * HP + 16 * w;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float vi = vr[r];
+      const float a = gate(fmaf(q[r].x, vi, q[r].y));
+      const float a2 = fmaf(-a, a, a);
+      acc[r].x = fmaf(c.x, a, acc[r].x);
+      acc[r].y = fmaf(c.y, a, acc[r].y);
+      const float dl = fmaf(c.x, q[r].z, c.y * q[r].w) * a2;
+      acc[r].z += dl;
+      acc[r].w = fmaf(dl, vi, acc[r].w);
+    }
+  }
+  const bool gave_up = *flag != 0;
+  if (!gave_up) {
+    const long long HH = (long long)HP * HP;
+    float* out = k.rpart + (long long)b * 4 * HH;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const long long e = (long long)(16 * w + r) * HP + j;
+      out[e] = acc[r].x;
+      out[HH + e] = acc[r].y;
+      out[2 * HH + e] = acc[r].z;
+      out[3 * HH + e] = acc[r].w;
+    }
+  }
+  // this companion's words back to tag 0, every unfold consumed
+  for (long long e = tid; e < N * 128; e += (long long)blockDim.x) {
+    const long long n = e >> 7;
+    const int r = (int)(e & 127);
+    xch_put(words + (n * 2 + (r >> 6)) * HP + jt * 64 + (r & 63), 0.f, 0u);
+  }
+  if (gave_up && tid == 0)
+    __hip_atomic_store(reinterpret_cast<int*>(k.rbw + (long long)B * N * 2 * HP), 1,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <bool FULL>
 __global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k) {
   constexpr int HP = 128, RC = 32;
+  // With recurrent-gradient companions (k.recF set): workgroups [0, B) are
+  // the chains, [Bc, Bc + B) and [2 Bc, 2 Bc + B) the companions of the
+  // postsynaptic halves (Bc = B rounded up to 8, so that a row's companions
+  // run on its chain's XCD), the ones between return at once. The chains
+  // come first in the grid, so they are dispatched before their companions.
+  if (k.recF != nullptr && (int)blockIdx.x >= k.B) {
+    const int Bc = (k.B + 7) / 8 * 8, g = (int)blockIdx.x;
+    const int jt = g / Bc - 1, b = g % Bc;
+    if (jt >= 0 && jt < 2 && b < k.B) rec_companion128<FULL>(k, b, jt);
+    return;
+  }
   extern __shared__ float4 lds4[];
   float2* abs_ = reinterpret_cast<float2*>(lds4);  // [2][128] alpha/beta by unfold parity
   const int tid = threadIdx.x;
@@ -2757,8 +2878,16 @@ __global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(
     return;
   }
   tid -= 3LL * Hp;
-  // the fused row backward's exchange words and status word (tag 0)
-  if (tid < nclr) clr[tid] = 0ULL;
+  // the exchange words and status word of the fused backward forms (tag 0),
+  // four words per thread in two 16-byte stores (the words are 256-byte aligned)
+  const long long e = 4 * tid;
+  if (e + 4 <= nclr) {
+    uint4* q = reinterpret_cast<uint4*>(clr + e);
+    q[0] = make_uint4(0u, 0u, 0u, 0u);
+    q[1] = make_uint4(0u, 0u, 0u, 0u);
+  } else {
+    for (long long r = e; r < nclr; ++r) clr[r] = 0ULL;
+  }
 }
 
 // LayerNorm + affine backward. Block 256 = 4 waves, `rpb` rows per block (4
@@ -4094,6 +4223,27 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
   }
 }
 
+hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const float* vsave,
+                                     const float* densave, const float* gout, Strides3 gs,
+                                     const float* ghfin, float* dsn, float* dsd, float* npart,
+                                     float* gstate, float* rpart, unsigned long long* words,
+                                     long long spin, hipStream_t s) {
+  if (!row128_rec_fused(p) || pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr ||
+      pp.recF == nullptr || words == nullptr)
+    return hipErrorInvalidValue;
+  BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, nullptr, dsn, dsd, npart, gstate,
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, words, pp.recF,
+         spin};
+  const int Bc = (p.B + 7) / 8 * 8;
+  const dim3 grid((unsigned)(2 * Bc + p.B)), block(512);
+  const size_t lds = bwd_lds_bytes(p);
+  if (p.H == 128)
+    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const float* vsave,
                                     const float* densave, const float* gout, Strides3 gs,
                                     const float* ghfin, float* npart, float* gstate, float* rpart,
@@ -4197,7 +4347,7 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   if (fs && (ln == nullptr || sd == nullptr || !prep_sens_fused(p))) return hipErrorInvalidValue;
   const int threads = fs ? kPrepSensThreads : 256;
   const long long total =
-      (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp + nclear;
+      (long long)p.Hp * p.Hp + (long long)p.Dp * p.Hp + 3LL * p.Hp + (nclear + 3) / 4;
   const int nprep = (int)((total + threads - 1) / threads);
   const int BT = p.B * p.T;
   const int nln = ln ? (fs ? BT * (p.Hp / 64) : (BT + 3) / 4) : 0;
@@ -4250,7 +4400,8 @@ hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
 
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
                                 const float* spart, const float* npart, const float* lnpart,
-                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s) {
+                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s,
+                                const int* status, float* gstate) {
   Partials pt;
   hipError_t e = presum(p, rpart, npart, ps, s, pt);
   if (e != hipSuccess) return e;
@@ -4265,10 +4416,14 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
     lnpart = ps.ln;
     nln = parts;
   }
+  const long long nx = status ? (long long)p.B * p.T * p.D : 0;
+  const long long ns = status && gstate ? (long long)p.B * p.H : 0;
   FinLeafK a{lp, pt.rpart, spart, pt.npart, lnpart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp,
-             pt.nrec, p.NRC, nln, nullptr, nullptr, 0, 0};
-  // four threads per output element
-  const long long total = 4 * ((long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D);
+             pt.nrec, p.NRC, nln, status, gstate, nx, ns};
+  // four threads per output element, or one per output when a gave-up status
+  // turns them all into NaN
+  const long long nel = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
+  const long long total = 4 * nel > nel + nx + ns ? 4 * nel : nel + nx + ns;
   const unsigned blocks = (unsigned)((total + 255) / 256);
   hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();

@@ -317,7 +317,24 @@ inline bool cmp_bwd(const Plan& p) {
 inline bool row_bwd_fused(const Plan& p) {
   return row_kernels(p) && p.FUSE && p.RCB == 8 && p.Dp <= 128 && p.B >= 1 && p.B <= 64;
 }
-inline long long row_bwd_words(const Plan& p) { return (long long)p.B * p.T * 128 + 1; }
+// Module-path backward at Hp = 128 with one row per workgroup (the unfused
+// single-row chain) and B <= 64: the recurrent parameter-gradient sums are
+// formed inside the chain launch, in two companion workgroups per batch row
+// (64 postsynaptic neurons each) that take each unfold's alpha/beta from the
+// row's chain workgroup as {value, tag} words ([B][T*U][2][128], then a
+// status word), instead of by rec_grad_kernel afterwards: one recurrent
+// partial per row.
+inline bool row128_rec_fused(const Plan& p) {
+  return row_wave128_bwd(p) && p.B >= 1 && p.B <= 64;
+}
+// Exchange words of the fused row backward (row_bwd_fused) or of the Hp = 128
+// chain with recurrent-gradient companions (row128_rec_fused); the last one
+// is the status word.
+inline long long row_bwd_words(const Plan& p) {
+  if (row_bwd_fused(p)) return (long long)p.B * p.T * 128 + 1;
+  if (row128_rec_fused(p)) return (long long)p.B * p.T * p.U * 256 + 1;
+  return 0;
+}
 inline int cmp_chunks_fwd(const Plan& p) {
   return (row_kernels(p) || row_wave128_fwd(p)) ? 4 : (p.CP > 0 ? kCmpChunks : p.KS);
 }
@@ -448,9 +465,12 @@ struct LeafGrads {
 int ln_bwd_blocks(const Plan& p);
 hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
                          const float* dxpart, float* gx, float* lnpart, hipStream_t s);
+// With a status word (the companions of a row128_rec_fused chain), every
+// output (also dL/dx and dL/dh0 = gstate) becomes NaN when it is set.
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
                                 const float* spart, const float* npart, const float* lnpart,
-                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s);
+                                const PresumBuf& ps, const LeafGrads& g, hipStream_t s,
+                                const int* status = nullptr, float* gstate = nullptr);
 
 // Fused row backward (row_bwd_fused): the chain of every batch row plus one
 // companion workgroup per row for its sensory and LayerNorm backward. The
@@ -469,6 +489,14 @@ struct RowCompanion {
   unsigned long long* words;  // row_bwd_words(p), cleared before the launch
   long long spin;
 };
+// The Hp = 128 chain with recurrent-gradient companions (row128_rec_fused):
+// rpart receives one partial per batch row, [B][4][Hp][Hp]; a companion that
+// runs out of its wait budget sets the status word after the words.
+hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const float* vsave,
+                                     const float* densave, const float* gout, Strides3 gs,
+                                     const float* ghfin, float* dsn, float* dsd, float* npart,
+                                     float* gstate, float* rpart, unsigned long long* words,
+                                     long long spin, hipStream_t s);
 hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const float* vsave,
                                     const float* densave, const float* gout, Strides3 gs,
                                     const float* ghfin, float* npart, float* gstate, float* rpart,

@@ -74,7 +74,8 @@ class CApi:
     PLAN_FIELDS = ("Hp", "Dp", "NB", "KS", "RC", "threads", "lds_fwd", "lds_bwd", "NCH",
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
                    "threads_bwd", "CP", "NCL", "CPB", "NBB", "ode_workgroups_bwd",
-                   "cmp_fwd", "cmp_bwd", "module_sens_in_prep", "module_row_bwd_fused")
+                   "cmp_fwd", "cmp_bwd", "module_sens_in_prep", "module_row_bwd_fused",
+                   "module_row128_rec_fused")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path

@@ -303,24 +303,28 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     assert capi.plan(4096, 4, 64, 64, 6)["CP"] == 0     # C5
 
 
-@pytest.mark.parametrize("shape,sens_in_prep,row_bwd", [
-    ((24, 8, 128, 64, 6), 1, 1),     # C1: 192 row blocks, companions in the chain launch
-    ((3, 5, 40, 60, 6), 1, 1),
-    ((8, 16, 128, 128, 6), 1, 0),    # 2 blocks per row: 256 of them
-    ((32, 16, 128, 128, 6), 0, 0),   # C2: 1024 row blocks would not fit the chip at once
-    ((24, 8, 129, 64, 6), 0, 0),     # D > 128
-    ((24, 8, 128, 62, 6), 0, 1),     # H not a multiple of 4
-    ((4096, 4, 64, 64, 6), 0, 0),    # C5
-    ((256, 64, 256, 256, 6), 0, 0),  # C3
+@pytest.mark.parametrize("shape,sens_in_prep,row_bwd,rec128", [
+    ((24, 8, 128, 64, 6), 1, 1, 0),     # C1: 192 row blocks, companions in the chain launch
+    ((3, 5, 40, 60, 6), 1, 1, 0),
+    ((8, 16, 128, 128, 6), 1, 0, 1),    # 2 blocks per row: 256 of them
+    ((32, 16, 128, 128, 6), 0, 0, 1),   # C2: 1024 row blocks would not fit the chip at once
+    ((24, 8, 129, 64, 6), 0, 0, 0),     # D > 128
+    ((24, 8, 128, 62, 6), 0, 1, 0),     # H not a multiple of 4
+    ((5, 3, 40, 100, 6), 1, 0, 1),      # H below Hp = 128
+    ((65, 2, 40, 128, 6), 0, 0, 0),     # B > 64
+    ((4096, 4, 64, 64, 6), 0, 0, 0),    # C5
+    ((256, 64, 256, 256, 6), 0, 0, 0),  # C3
 ])
-def test_module_path_fusion_fields(capi, shape, sens_in_prep, row_bwd):
+def test_module_path_fusion_fields(capi, shape, sens_in_prep, row_bwd, rec128):
     """The plan reports when the module forward forms the sensory sums in its
     parameter-image launch (at most 256 (row, 64-neuron) blocks, D <= 128,
-    H % 4 == 0) and when the module backward runs the sensory and LayerNorm
+    H % 4 == 0), when the module backward runs the sensory and LayerNorm
     backward inside the chain launch (Hp = 64, one row per workgroup, D <= 128,
-    B <= 64)."""
+    B <= 64), and when it forms the recurrent parameter-gradient sums inside
+    the chain launch (Hp = 128, one row per workgroup, B <= 64)."""
     p = capi.plan(*shape)
-    assert (p["module_sens_in_prep"], p["module_row_bwd_fused"]) == (sens_in_prep, row_bwd)
+    got = (p["module_sens_in_prep"], p["module_row_bwd_fused"], p["module_row128_rec_fused"])
+    assert got == (sens_in_prep, row_bwd, rec128)
 
 
 def _ext_path():

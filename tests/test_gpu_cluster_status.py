@@ -121,3 +121,34 @@ def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi, D1):
         assert torch.isfinite(p.grad).all(), n
     capi.device_status()
 
+
+
+@pytest.mark.parametrize("shape", [(32, 4, 128, 128), (5, 3, 40, 100)], ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_recurrent_gradient_companions_give_up_sets_every_gradient_to_nan(capi, shape):
+    """At Hp = 128 the module backward forms the recurrent parameter-gradient
+    sums in companion workgroups that wait for the chain's alpha/beta words:
+    with a budget of 0 they leave at once, and the finalize writes NaN into
+    every gradient, dL/dx and dL/dh0; with the default budget again the
+    results are finite and the status clean."""
+    B1, T1, D1, H1 = shape
+    plan = capi.plan(B1, T1, D1, H1, 6)
+    assert plan["module_row128_rec_fused"] == 1, plan
+    m = _perturbed_module(D1, H1, seed=35).to(DEV)
+    x = torch.randn(B1, T1, D1, device=DEV, requires_grad=True)
+    h0 = (torch.randn(B1, H1, device=DEV) * 0.2).requires_grad_(True)
+    out, (h, _) = m(x, (h0, h0))
+    assert torch.isfinite(out).all()
+    with _NoWait(capi):
+        (out.sum() + h.sum()).backward()
+    assert torch.isnan(x.grad).all() and torch.isnan(h0.grad).all()
+    for n, p in m.named_parameters():
+        assert torch.isnan(p.grad).all(), n
+    _expect_fault(capi)
+    m.zero_grad(set_to_none=True)
+    x.grad = h0.grad = None
+    out, (h, _) = m(x, (h0, h0))
+    (out.sum() + h.sum()).backward()
+    assert torch.isfinite(x.grad).all() and torch.isfinite(h0.grad).all()
+    for n, p in m.named_parameters():
+        assert torch.isfinite(p.grad).all(), n
+    capi.device_status()

@@ -564,16 +564,18 @@ def test_hip_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60)],
+@pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60), (8, 4, 40, 128), (5, 3, 40, 100)],
                          ids=lambda s: "B%dT%dD%dH%d" % s)
 def test_module_backward_twice_over_one_forward(shape):
     """Two backward passes over one forward (retain_graph) with different
     output gradients: each must match the float64 oracle for its own output
-    gradient. At these shapes the backward hands each step's dL/dsn, dL/dsd to
-    companion workgroups as words, which the forward clears; the second pass
-    must not read the first pass's words."""
+    gradient. At these shapes the backward hands each step's dL/dsn, dL/dsd
+    (Hp = 64) or each unfold's alpha/beta (Hp = 128) to companion workgroups
+    as words, which the forward clears; the second pass must not read the
+    first pass's words."""
     B, T, D, H = shape
-    assert ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)["module_row_bwd_fused"] == 1
+    plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
+    assert plan["module_row_bwd_fused"] == 1 or plan["module_row128_rec_fused"] == 1
     m = _perturbed_module(D, H, seed=B + H).to(DEV)
     g = torch.Generator().manual_seed(3)
     x = torch.randn(B, T, D, generator=g)
