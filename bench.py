@@ -192,6 +192,9 @@ def roofline(c, ktimes, plan, traffic=None, counts=None):
     if plan.get("module_row_bwd_fused") and "ltc_sens_bwd" not in ktimes:
         # the fused row backward: the chain launch also runs the sensory backward
         fl["ltc_ode_bwd"] += fl["ltc_sens_bwd"]
+    if plan.get("module_row128_rec_fused") and "ltc_rec_grad" not in ktimes:
+        # the Hp = 128 chain launch also forms the recurrent parameter-gradient sums
+        fl["ltc_ode_bwd"] += fl["ltc_rec_grad"]
     if plan.get("module_sens_in_prep") and "ltc_sens_fwd" not in ktimes:
         # the prep launch forms the sensory sums of the module forward
         fl["ltc_prep"] += fl["ltc_sens_fwd"]
