@@ -4375,9 +4375,17 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   return hipGetLastError();
 }
 
-// Rows per LayerNorm-backward block: one per wave up to 1024 blocks (more
-// loads in flight), four per wave beyond (fewer column partials).
-int ln_rows_per_block(const Plan& p) { return (long long)p.B * p.T > 4096 ? 16 : 4; }
+// Rows per LayerNorm-backward block: one per wave (more loads in flight) up
+// to 4096 rows, four per wave beyond (fewer column partials).
+int ln_rows_per_block(const Plan& p) {
+  const long long BT = (long long)p.B * p.T;
+  if (BT > 4096) return 16;
+  // up to 1024 rows: the fewest rows per block that keep the column partials
+  // at 64 or fewer, which the finalize sums without a pre-sum launch
+  for (int rpb : {4, 8, 16})
+    if ((BT + rpb - 1) / rpb <= 64) return rpb;
+  return 4;
+}
 
 int ln_bwd_blocks(const Plan& p) {
   const int rpb = ln_rows_per_block(p);
