@@ -971,8 +971,11 @@ struct BwdK {
   // dsd; the Hp = 128 chain with recurrent-gradient companions sends each
   // unfold's alpha/beta as [B][T*U][2][128] words instead of into absave.
   unsigned long long* rbw;
-  // The recurrent-gradient companions: the forward image {S', c', WE, WP} and
-  // their wait budget.
+};
+
+// The recurrent-gradient companions of the Hp = 128 chain: the forward image
+// {S', c', WE, WP} and their wait budget (recF null: no companions).
+struct RecC {
   const float4* recF;
   long long spin;
 };
@@ -1858,7 +1861,7 @@ __device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4
 // the budget sets the status word (after the words) and the companion writes
 // no partial; the finalize then writes NaN into every output.
 template <bool FULL>
-__device__ __forceinline__ void rec_companion128(const BwdK& k, int b, int jt) {
+__device__ __forceinline__ void rec_companion128(const BwdK& k, const RecC& rc, int b, int jt) {
   constexpr int HP = 128;
   extern __shared__ float4 lds4[];
   float2* ab = reinterpret_cast<float2*>(lds4);       // [2][64] alpha/beta of the unfold
@@ -1871,7 +1874,7 @@ __device__ __forceinline__ void rec_companion128(const BwdK& k, int b, int jt) {
   float4 q[16], acc[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    q[r] = k.recF[(long long)(16 * w + r) * HP + j];
+    q[r] = rc.recF[(long long)(16 * w + r) * HP + j];
     acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (tid == 0) *flag = 0;
@@ -1882,13 +1885,13 @@ __device__ __forceinline__ void rec_companion128(const BwdK& k, int b, int jt) {
     if (tid < 128) {
       const int qq = tid >> 6;  // 0: alpha, 1: beta
       unsigned long long* wd = words + (n * 2 + qq) * HP + jt * 64 + lane;
-      bool ok = k.spin > 0;
+      bool ok = rc.spin > 0;
       unsigned long long v = 0;
       if (ok) {
         v = xch_get(wd);
         const long long t0 = wall_clock64();
         while ((unsigned)(v >> 32) != 1u) {
-          if (wall_clock64() - t0 > k.spin) {
+          if (wall_clock64() - t0 > rc.spin) {
             ok = false;
             break;
           }
@@ -1942,17 +1945,17 @@ __device__ __forceinline__ void rec_companion128(const BwdK& k, int b, int jt) {
 }
 
 template <bool FULL>
-__global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k) {
+__global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k, RecC rc) {
   constexpr int HP = 128, RC = 32;
-  // With recurrent-gradient companions (k.recF set): workgroups [0, B) are
+  // With recurrent-gradient companions (rc.recF set): workgroups [0, B) are
   // the chains, [Bc, Bc + B) and [2 Bc, 2 Bc + B) the companions of the
   // postsynaptic halves (Bc = B rounded up to 8, so that a row's companions
   // run on its chain's XCD), the ones between return at once. The chains
   // come first in the grid, so they are dispatched before their companions.
-  if (k.recF != nullptr && (int)blockIdx.x >= k.B) {
+  if (rc.recF != nullptr && (int)blockIdx.x >= k.B) {
     const int Bc = (k.B + 7) / 8 * 8, g = (int)blockIdx.x;
     const int jt = g / Bc - 1, b = g % Bc;
-    if (jt >= 0 && jt < 2 && b < k.B) rec_companion128<FULL>(k, b, jt);
+    if (jt >= 0 && jt < 2 && b < k.B) rec_companion128<FULL>(k, rc, b, jt);
     return;
   }
   extern __shared__ float4 lds4[];
@@ -3990,10 +3993,11 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
       return hipGetLastError();
     }
     if (row_wave128_bwd(p)) {
+      const RecC none{nullptr, 0};
       if (p.H == 128)
-        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a);
+        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a, none);
       else
-        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, dim3(512), lds, s, a);
+        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, dim3(512), lds, s, a, none);
       return hipGetLastError();
     }
   }
@@ -4232,15 +4236,15 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
       pp.recF == nullptr || words == nullptr)
     return hipErrorInvalidValue;
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, nullptr, dsn, dsd, npart, gstate,
-         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, words, pp.recF,
-         spin};
+         rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, words};
+  const RecC rc{pp.recF, spin};
   const int Bc = (p.B + 7) / 8 * 8;
   const dim3 grid((unsigned)(2 * Bc + p.B)), block(512);
   const size_t lds = bwd_lds_bytes(p);
   if (p.H == 128)
-    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, block, lds, s, a, rc);
   else
-    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, block, lds, s, a, rc);
   return hipGetLastError();
 }
 
