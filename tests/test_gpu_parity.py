@@ -564,7 +564,8 @@ def test_hip_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60), (8, 4, 40, 128), (5, 3, 40, 100)],
+@pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60), (8, 4, 40, 128), (5, 3, 40, 100),
+                                   (64, 2, 20, 65)],
                          ids=lambda s: "B%dT%dD%dH%d" % s)
 def test_module_backward_twice_over_one_forward(shape):
     """Two backward passes over one forward (retain_graph) with different
