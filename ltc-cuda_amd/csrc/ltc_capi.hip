@@ -894,14 +894,24 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   pp.sF = sens_in_prep ? nullptr : wfw.pp.sF;
   pp.sFi = sens_in_prep ? nullptr : wfw.pp.sFi;
   pp.sFn = sens_in_prep ? nullptr : wfw.pp.sFn;
+  // Without saving, nothing but the sensory launch reads the normalised rows:
+  // when they fit one 64-input chunk, it normalises them itself.
+  const bool ln_in_sens = !save_intermediates && !sens_in_prep && ltc::sens_fwd_ln_fusable(p);
   hipError_t e;
   e = timed(ltc::K_PREP, s, [&] {
-    return ltc::launch_prep_leaf(p, lp, pp, images, &ln, s, row_words,
+    return ltc::launch_prep_leaf(p, lp, pp, images, ln_in_sens ? nullptr : &ln, s, row_words,
                                  row_words ? ltc::row_bwd_words(p) : 0,
                                  sens_in_prep ? wfw.sn : nullptr, sens_in_prep ? wfw.sd : nullptr);
   });
   if (e != hipSuccess) return hip_fail("prep launch", e);
-  if (!sens_in_prep) {
+  if (ln_in_sens) {
+    const ltc::LnAff la{ln_weight, ln_bias, input_w, input_b, ln_eps};
+    e = timed(ltc::K_SENS_FWD, s, [&] {
+      return ltc::launch_sens_fwd_ln(p, x, ltc::Strides3{sxb, sxt, sxd}, pp, la, wfw.sn, wfw.sd,
+                                     s);
+    });
+    if (e != hipSuccess) return hip_fail("sensory forward launch", e);
+  } else if (!sens_in_prep) {
     e = timed(ltc::K_SENS_FWD, s,
               [&] { return ltc::launch_sens_fwd(p, lw.xa, xas, pp, wfw.sn, wfw.sd, s); });
     if (e != hipSuccess) return hip_fail("sensory forward launch", e);

@@ -536,14 +536,18 @@ __global__ __launch_bounds__(256) void sens_fwd_kernel(const float* __restrict__
 // quarters of each chunk's slots. Slots past a count hold zero operands
 // (input 0) and add zero.
 // ---------------------------------------------------------------------------
-template <int RPW, int DS>
+// LN (DS = 1, D <= 64): x is the raw input, and each wave applies the
+// module's LayerNorm + affine to its rows of the staged chunk in place, with
+// ln_row's arithmetic, so the sums are those over the prep launch's rows.
+template <int RPW, int DS, bool LN = false>
 __global__ __launch_bounds__(256) void sens_fwd_cmp_kernel(const float* __restrict__ x, Strides3 xs,
                                                            int T, int D, int BT, int Hp,
                                                            const float4* __restrict__ sF,
                                                            const int* __restrict__ sFi,
                                                            const int* __restrict__ sFn,
                                                            float* __restrict__ sn,
-                                                           float* __restrict__ sd) {
+                                                           float* __restrict__ sd, LnAff la = {}) {
+  static_assert(!LN || DS == 1, "the row normalisation runs in the row-group layout");
   constexpr int ROWS = (DS == 1 ? 4 : 1) * RPW;
   constexpr int XLD = ROWS + 4;  // padded staged row, 16-byte aligned
   __shared__ __align__(16) float xsh[64 * XLD];
@@ -594,6 +598,22 @@ __global__ __launch_bounds__(256) void sens_fwd_cmp_kernel(const float* __restri
     }
     __syncthreads();
     fetch(d0 + 64);
+    if constexpr (LN) {
+      // the only chunk (D <= 64): this wave's rows, lane = input
+      const bool in = lane < D;
+      const float lw = in ? la.ln_w[lane] : 0.f, lb = in ? la.ln_b[lane] : 0.f;
+      const float iw = in ? la.input_w[lane] : 0.f, ib = in ? la.input_b[lane] : 0.f;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        float* px = xsh + lane * XLD + rw + r;
+        const float v = *px;
+        const float mean = wave_sum(v) / (float)D;
+        const float dv = in ? v - mean : 0.f;
+        const float rstd = 1.0f / sqrtf(wave_sum(fmaf(dv, dv, 0.f)) / (float)D + la.eps);
+        const float xn = (v - mean) * rstd * lw + lb;
+        *px = in ? xn * iw + ib : 0.f;
+      }
+    }
     if (s0 < s1) {
       const float4* pcol = sF + cb + h;
       const int* icol = sFi + cb + h;
@@ -4155,6 +4175,26 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
     }
   }
 #undef LTC_SENS
+  return hipGetLastError();
+}
+
+hipError_t launch_sens_fwd_ln(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                              const LnAff& la, float* sn, float* sd, hipStream_t s) {
+  if (!sens_fwd_ln_fusable(p) || pp.sF == nullptr || pp.sFi == nullptr || pp.sFn == nullptr)
+    return hipErrorInvalidValue;
+  const int BT = p.B * p.T;
+  const SensGeom geo = sens_fwd_geom(p);
+  const dim3 grid(p.Hp / 64, (BT + 4 * geo.rpw - 1) / (4 * geo.rpw)), block(256);
+#define LTC_SENSLN(R)                                                                      \
+  hipLaunchKernelGGL((sens_fwd_cmp_kernel<R, 1, true>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
+                     p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd, la)
+  switch (geo.rpw) {
+    case 8: LTC_SENSLN(8); break;
+    case 4: LTC_SENSLN(4); break;
+    case 2: LTC_SENSLN(2); break;
+    default: LTC_SENSLN(1); break;
+  }
+#undef LTC_SENSLN
   return hipGetLastError();
 }
 

@@ -216,6 +216,20 @@ inline SensGeom sens_fwd_geom(const Plan& p) {
 inline bool prep_sens_fused(const Plan& p) {
   return (long long)p.B * p.T * (p.Hp / 64) <= 256 && p.D >= 1 && p.D <= 128 && p.H % 4 == 0;
 }
+// LayerNorm + affine of the raw input rows, applied by the compacted sensory
+// launch itself when the rows fit one 64-input chunk and the launch takes
+// four row groups per workgroup (the module's no-grad forward then skips the
+// prep launch's row normalisation, whose output nothing else reads).
+struct LnAff {
+  const float* ln_w;
+  const float* ln_b;
+  const float* input_w;
+  const float* input_b;
+  float eps;
+};
+inline bool sens_fwd_ln_fusable(const Plan& p) { return p.D <= 64 && !sens_fwd_geom(p).split_d; }
+hipError_t launch_sens_fwd_ln(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
+                              const LnAff& la, float* sn, float* sd, hipStream_t s);
 // Cluster path scratch: exchange words and a status word (nonzero after a
 // cluster member gave up waiting for its partners), plus the wait budget of
 // every exchange in ticks of the 100 MHz wall clock (<= 0: a member gives up

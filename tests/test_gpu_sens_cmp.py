@@ -118,3 +118,28 @@ def test_compacted_sensory_forward_boundary_path_matches_oracle(shape):
     e_h = (h.cpu().double() - r_h).abs().max().item()
     print(f"compacted sensory, boundary {shape}: out err {e_out:.2e} h err {e_h:.2e}", flush=True)
     assert e_out <= 1e-3 and e_h <= 1e-3
+
+
+@pytest.mark.parametrize("shape", [(512, 4, 40, 64), (1024, 4, 64, 64)], ids=lambda s: "B%dT%dD%dH%d" % s)
+def test_no_grad_forward_normalises_rows_in_the_sensory_launch(shape):
+    """A no-grad forward with D <= 64 and many rows (C5's form) normalises the
+    input rows inside the sensory launch instead of the prep launch. With
+    ln_row's arithmetic the outputs equal the training forward's (which keeps
+    the prep launch's rows for the backward) bit for bit, also for a strided
+    x, and match the float64 oracle."""
+    B, T, D, H = shape
+    m = _perturbed_module(D, H, seed=B + D).to(DEV)
+    g = torch.Generator().manual_seed(D + H)
+    wide = torch.randn(B, T, 2 * D, generator=g)
+    x = wide[:, :, 0::2]
+    xd = wide.to(DEV)[:, :, 0::2]
+    assert not xd.is_contiguous()
+    with torch.no_grad():
+        a, (ha, _) = m(xd)
+    b, (hb, _) = m(xd.clone().requires_grad_(True))
+    assert torch.equal(a, b.detach()) and torch.equal(ha, hb.detach())
+    h0 = torch.zeros(B, H)
+    r_out, r_h, _, _, _ = _oracle_module_grads(m, x.contiguous(), h0, torch.zeros(B, T, H), torch.zeros(B, H))
+    e_out = (a.cpu().double() - r_out).abs().max().item()
+    print(f"no-grad rows normalised in the sensory launch {shape}: out err {e_out:.2e}", flush=True)
+    assert e_out <= 1e-3
