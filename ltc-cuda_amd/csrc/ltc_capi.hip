@@ -366,8 +366,10 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
   // recurrent-gradient companions)
   const long long nch = ltc::row128_rec_fused(p) && p.B > p.NCH ? p.B : p.NCH;
   w.rpart = c.take<float>(nch * 4 * p.Hp * p.Hp);
-  // sensory partials: NRC row chunks, or one per batch row (fused row backward)
-  const long long nrc = ltc::row_bwd_fused(p) && p.B > p.NRC ? p.B : p.NRC;
+  // sensory partials: NRC row chunks, or one per batch row (fused row backward,
+  // or the sensory companions of the Hp = 128 chain)
+  const bool per_row = ltc::row_bwd_fused(p) || ltc::row128_sens_fused(p);
+  const long long nrc = per_row && p.B > p.NRC ? p.B : p.NRC;
   w.spart = c.take<float>(nrc * 4 * p.Dp * p.Hp);
   w.dxpart = c.take<float>((long long)(p.Hp / 32) * p.B * p.T * p.Dp);
   w.cb = carve_cluster(p, c, true);
@@ -1024,16 +1026,20 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   // inside the chain launch by companion workgroups: one partial per row.
   ltc::Plan pf = p;
   const int* status = nullptr;
+  const bool sens_comp = ltc::row128_sens_fused(p);
   if (ltc::row128_rec_fused(p)) {
+    // with D <= 128 the sensory backward runs in that launch too
     unsigned long long* words = row_words;
     e = timed(ltc::K_ODE_BWD, s, [&] {
-      return ltc::launch_ode_bwd_row128_rec(p, wb.pp, vsave, densave, grad_out, gs,
-                                            grad_h_final, wb.dsn, wb.dsd, wb.npart, grad_state,
-                                            wb.rpart, words,
-                                            g_spin.load(std::memory_order_relaxed), s);
+      return ltc::launch_ode_bwd_row128_rec(
+          p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.dsn, wb.dsd, wb.npart,
+          grad_state, wb.rpart, words, g_spin.load(std::memory_order_relaxed),
+          sens_comp ? lw.xa : nullptr, sens_comp ? wb.spart : nullptr,
+          sens_comp ? wb.dxpart : nullptr, s);
     });
     if (e != hipSuccess) return hip_fail("ODE backward launch", e);
     pf.NCH = p.B;
+    if (sens_comp) pf.NRC = p.B;
     status = reinterpret_cast<const int*>(words + ltc::row_bwd_words(p) - 1);
   } else {
     e = timed(ltc::K_ODE_BWD, s, [&] {
@@ -1048,12 +1054,15 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
       if (e != hipSuccess) return hip_fail("recurrent gradient launch", e);
     }
   }
-  e = timed(ltc::K_SENS_BWD, s, [&] {
-    return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s);
+  if (!sens_comp) {
+    e = timed(ltc::K_SENS_BWD, s, [&] {
+      return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s);
+    });
+    if (e != hipSuccess) return hip_fail("sensory backward launch", e);
+  }
+  e = timed(ltc::K_LN_BWD, s, [&] {
+    return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s, sens_comp ? 2 : 0);
   });
-  if (e != hipSuccess) return hip_fail("sensory backward launch", e);
-  e = timed(ltc::K_LN_BWD, s,
-            [&] { return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s); });
   if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
   e = timed(ltc::K_FINALIZE, s, [&] {
     return ltc::launch_finalize_leaf(pf, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s,

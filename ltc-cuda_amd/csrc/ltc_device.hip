@@ -998,6 +998,17 @@ struct BwdK {
 struct RecC {
   const float4* recF;
   long long spin;
+  int* status;  // the status word, after all words
+  // Sensory companions (sensB null: none): each step's dL/dsn, dL/dsd as
+  // words [B][T][2][128] from the chain (instead of dsn / dsd), the rows xa,
+  // the backward sensory image, and their outputs: one sensory partial per
+  // row [B][4][Hp][Dp] and dL/dxa partials [2][B*T][Dp] over 64 neurons each.
+  unsigned long long* sw;
+  const float* xa;
+  const float4* sensB;
+  float* spart;
+  float* dxpart;
+  int D, Dp;
 };
 
 // One synapse (i = o, j = r) of the chain for every row of the tile. With
@@ -1763,7 +1774,7 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave_kernel(BwdK k) {
 template <int NS, bool FULL>
 __device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4 (&preg)[32],
                                                      const unsigned (&jx)[16], float2* abs_, int i,
-                                                     bool lead) {
+                                                     bool lead, unsigned long long* sw) {
   constexpr int HP = 128, SU = kRowChainUnfolds;
   const int H = k.H, B = k.B, T = k.T, U = k.U;
   const int b0 = blockIdx.x;
@@ -1841,8 +1852,14 @@ __device__ __forceinline__ void bwd_row_wave128_loop(const BwdK& k, const float4
     if (u == 0) {
       if (lead) {
         const long long e = ((long long)b0 * T + t) * HP + i;
-        k.dsn[e] = accA;
-        k.dsd[e] = accB;
+        if (sw != nullptr) {
+          // to the row's sensory companions: [B][T][2][128] words
+          xch_put(sw + e + (long long)(b0 * T + t) * HP, accA, 1u);
+          xch_put(sw + e + (long long)(b0 * T + t + 1) * HP, accB, 1u);
+        } else {
+          k.dsn[e] = accA;
+          k.dsd[e] = accB;
+        }
       }
       --t;
       u = U - 1;
@@ -1960,11 +1977,128 @@ __device__ __forceinline__ void rec_companion128(const BwdK& k, const RecC& rc, 
     xch_put(words + (n * 2 + (r >> 6)) * HP + jt * 64 + (r & 63), 0.f, 0u);
   }
   if (gave_up && tid == 0)
-    __hip_atomic_store(reinterpret_cast<int*>(k.rbw + (long long)B * N * 2 * HP), 1,
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(rc.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <bool FULL>
+// Sensory companion of the Hp = 128 chain for batch row b and the neurons
+// h in [64 jt, 64 jt + 64) (module path, D <= 64 * DC <= 128): the sensory
+// backward of the row's T steps for those neurons, as the row's chain
+// workgroup publishes each step's dL/dsn, dL/dsd (latest step first), in
+// the fused row backward's layout (8 waves; lane l and wave w hold the DC*8
+// synapses d = l + 64*kk, h = 64 jt + 8w + m with their operands and four
+// gradient sums; the second 64 inputs' operands in LDS). Per step 128
+// threads wait for the step's 128 words while the others stage its row of
+// xa; after the synapses, the 8 per-wave partials of dL/dxa[d] are summed in
+// a fixed order into this half's partial dxpart[jt][row][d], from which the
+// LayerNorm backward launch continues. At the end the companion writes its
+// half of the row's sensory partial and returns its words to tag 0; a wait
+// that runs out sets the status word and no partial is written.
+template <int DC>
+__device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc, int b, int jt) {
+  constexpr int HP = 128, NX = 64 * DC;
+  extern __shared__ float4 lds4[];
+  float4* qsh = lds4;  // [8][8][64] operands of the second 64 inputs (DC = 2)
+  float2* absh = reinterpret_cast<float2*>(lds4 + (DC - 1) * 8 * 8 * 64);  // [64] of the step
+  float* xsh = reinterpret_cast<float*>(absh + 64);  // [NX] the step's xa row
+  float* dxr = xsh + NX;                             // [8][NX] per-wave dL/dxa partials
+  int* flag = reinterpret_cast<int*>(dxr + 8 * NX);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int T = k.T, D = rc.D, Dp = rc.Dp;
+  const int h0 = 64 * jt + 8 * w;
+  float4 q[8], sa[DC][8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    q[m] = rc.sensB[(long long)(h0 + m) * Dp + lane];
+    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = rc.sensB[(long long)(h0 + m) * Dp + lane + 64];
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk) sa[kk][m] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tid == 0) *flag = 0;
+  __syncthreads();
+  unsigned long long* words = rc.sw + (long long)b * T * 2 * HP;
+  const long long BT = (long long)k.B * T;
+  for (int t = T - 1; t >= 0; --t) {
+    const long long row = (long long)b * T + t;
+    if (tid < 128) {
+      const int qq = tid >> 6;  // 0: dL/dsn, 1: dL/dsd
+      unsigned long long* wd = words + ((long long)t * 2 + qq) * HP + 64 * jt + lane;
+      bool ok = rc.spin > 0;
+      unsigned long long v = 0;
+      if (ok) {
+        v = xch_get(wd);
+        const long long t0 = wall_clock64();
+        while ((unsigned)(v >> 32) != 1u) {
+          if (wall_clock64() - t0 > rc.spin) {
+            ok = false;
+            break;
+          }
+          v = xch_get(wd);
+        }
+      }
+      reinterpret_cast<float*>(absh)[lane * 2 + qq] = __uint_as_float((unsigned)v);
+      if (!ok) *flag = 1;
+    } else if (tid - 128 < NX) {
+      const int d = tid - 128;
+      xsh[d] = d < D ? rc.xa[row * D + d] : 0.f;
+    }
+    __syncthreads();
+    if (*flag) break;
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk) {
+      const float xv = xsh[lane + 64 * kk];
+      float dxp = 0.f;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const float2 cc = absh[8 * w + m];
+        const float4 p = kk == 0 ? q[m] : qsh[(w * 8 + m) * 64 + lane];
+        const float a = gate(fmaf(p.x, xv, p.y));
+        const float a2 = fmaf(-a, a, a);
+        const float gm = fmaf(cc.x, p.z, cc.y);
+        sa[kk][m].x = fmaf(gm, a, sa[kk][m].x);
+        sa[kk][m].y = fmaf(cc.x, a, sa[kk][m].y);
+        const float ga2 = gm * a2;
+        sa[kk][m].z += ga2;
+        sa[kk][m].w = fmaf(ga2, xv, sa[kk][m].w);
+        dxp = fmaf(ga2, p.w, dxp);
+      }
+      dxr[w * NX + lane + 64 * kk] = dxp;
+      // one block of 64 inputs at a time (keeps the live registers in bounds)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+    if (tid < NX) {
+      float sxa = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 8; ++ww) sxa += dxr[ww * NX + tid];
+      if (tid < Dp) rc.dxpart[((long long)jt * BT + row) * Dp + tid] = sxa;
+    }
+  }
+  const bool gave_up = *flag != 0;
+  if (!gave_up) {
+    // this half of the row's sensory partial, layout [4][Hp][Dp] as sens_bwd_kernel's
+    const long long DH = (long long)Dp * HP;
+    float* out = rc.spart + (long long)b * 4 * DH;
+#pragma unroll
+    for (int kk = 0; kk < DC; ++kk)
+#pragma unroll
+      for (int m = 0; m < 8; ++m) {
+        const long long e = (long long)(h0 + m) * Dp + lane + 64 * kk;
+        out[e] = sa[kk][m].x;
+        out[DH + e] = sa[kk][m].y;
+        out[2 * DH + e] = sa[kk][m].z;
+        out[3 * DH + e] = sa[kk][m].w;
+      }
+  }
+  // this companion's words back to tag 0, every step consumed
+  for (int e = tid; e < T * 128; e += (int)blockDim.x) {
+    const int t = e >> 7, r = e & 127;
+    xch_put(words + ((long long)t * 2 + (r >> 6)) * HP + 64 * jt + (r & 63), 0.f, 0u);
+  }
+  if (gave_up && tid == 0)
+    __hip_atomic_store(rc.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool FULL, int DC = 1>
 __global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k, RecC rc) {
   constexpr int HP = 128, RC = 32;
   // With recurrent-gradient companions (rc.recF set): workgroups [0, B) are
@@ -1973,9 +2107,16 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k, RecC r
   // run on its chain's XCD), the ones between return at once. The chains
   // come first in the grid, so they are dispatched before their companions.
   if (rc.recF != nullptr && (int)blockIdx.x >= k.B) {
+    // with sensory companions (rc.sensB set) also [3 Bc, 3 Bc + B) and
+    // [4 Bc, 4 Bc + B) for the two 64-neuron halves
     const int Bc = (k.B + 7) / 8 * 8, g = (int)blockIdx.x;
-    const int jt = g / Bc - 1, b = g % Bc;
-    if (jt >= 0 && jt < 2 && b < k.B) rec_companion128<FULL>(k, rc, b, jt);
+    const int kind = g / Bc, b = g % Bc;
+    if (b < k.B) {
+      if (kind == 1 || kind == 2)
+        rec_companion128<FULL>(k, rc, b, kind - 1);
+      else if ((kind == 3 || kind == 4) && rc.sensB != nullptr)
+        sens_companion128<DC>(k, rc, b, kind - 3);
+    }
     return;
   }
   extern __shared__ float4 lds4[];
@@ -2000,14 +2141,14 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k, RecC r
   // slots rounded up to a multiple of four (padding slots add zeros)
   switch ((nslot + 3) >> 2) {
     case 0:
-    case 1: bwd_row_wave128_loop<4, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 2: bwd_row_wave128_loop<8, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 3: bwd_row_wave128_loop<12, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 4: bwd_row_wave128_loop<16, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 5: bwd_row_wave128_loop<20, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 6: bwd_row_wave128_loop<24, FULL>(k, preg, jx, abs_, i, lead); break;
-    case 7: bwd_row_wave128_loop<28, FULL>(k, preg, jx, abs_, i, lead); break;
-    default: bwd_row_wave128_loop<32, FULL>(k, preg, jx, abs_, i, lead); break;
+    case 1: bwd_row_wave128_loop<4, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 2: bwd_row_wave128_loop<8, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 3: bwd_row_wave128_loop<12, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 4: bwd_row_wave128_loop<16, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 5: bwd_row_wave128_loop<20, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 6: bwd_row_wave128_loop<24, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    case 7: bwd_row_wave128_loop<28, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    default: bwd_row_wave128_loop<32, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
   }
 }
 
@@ -4013,7 +4154,7 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
       return hipGetLastError();
     }
     if (row_wave128_bwd(p)) {
-      const RecC none{nullptr, 0};
+      const RecC none{};
       if (p.H == 128)
         hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a, none);
       else
@@ -4271,20 +4412,33 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
                                      const float* densave, const float* gout, Strides3 gs,
                                      const float* ghfin, float* dsn, float* dsd, float* npart,
                                      float* gstate, float* rpart, unsigned long long* words,
-                                     long long spin, hipStream_t s) {
+                                     long long spin, const float* xa, float* spart,
+                                     float* dxpart, hipStream_t s) {
   if (!row128_rec_fused(p) || pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr ||
       pp.recF == nullptr || words == nullptr)
     return hipErrorInvalidValue;
+  const bool sens = xa != nullptr;
+  if (sens && (!row128_sens_fused(p) || pp.sensB == nullptr || spart == nullptr ||
+               dxpart == nullptr))
+    return hipErrorInvalidValue;
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, nullptr, dsn, dsd, npart, gstate,
          rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, words};
-  const RecC rc{pp.recF, spin};
+  const long long nrec = (long long)p.B * p.T * p.U * 256;
+  unsigned long long* sw = sens ? words + nrec : nullptr;
+  int* status = reinterpret_cast<int*>(words + row_bwd_words(p) - 1);
+  const RecC rc{pp.recF, spin, status, sw, xa, sens ? pp.sensB : nullptr, spart, dxpart, p.D,
+                p.Dp};
   const int Bc = (p.B + 7) / 8 * 8;
-  const dim3 grid((unsigned)(2 * Bc + p.B)), block(512);
+  const dim3 grid((unsigned)((sens ? 4 : 2) * Bc + p.B)), block(512);
   const size_t lds = bwd_lds_bytes(p);
-  if (p.H == 128)
-    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, block, lds, s, a, rc);
-  else
-    hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, block, lds, s, a, rc);
+#define LTC_W128(F, C) \
+  hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<F, C>), grid, block, lds, s, a, rc)
+  if (p.H == 128) {
+    if (p.Dp > 64) LTC_W128(true, 2); else LTC_W128(true, 1);
+  } else {
+    if (p.Dp > 64) LTC_W128(false, 2); else LTC_W128(false, 1);
+  }
+#undef LTC_W128
   return hipGetLastError();
 }
 
@@ -4437,9 +4591,10 @@ int ln_bwd_blocks(const Plan& p) {
 }
 
 hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
-                         const float* dxpart, float* gx, float* lnpart, hipStream_t s) {
+                         const float* dxpart, float* gx, float* lnpart, hipStream_t s, int hb) {
   const dim3 grid(ln_bwd_blocks(p)), block(256);
-  const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = p.Hp / 32;
+  // hb: the dL/dxa partials per row (those of 32-neuron blocks by default)
+  const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = hb > 0 ? hb : p.Hp / 32;
 #define LTC_LNB(C) hipLaunchKernelGGL((ln_bwd_kernel<C>), grid, block, 0, s, lp, ln, dxpart, gx, lnpart, p.T, p.D, p.Dp, BT, HB, rpb)
   if (p.D <= 64) LTC_LNB(1);
   else if (p.D <= 128) LTC_LNB(2);
