@@ -189,8 +189,9 @@ def kernel_times(capi, fn, iters):
 
 def roofline(c, ktimes, plan, traffic=None, counts=None):
     fl = kernel_flops(c, bool(plan["fuse"]), counts)
-    if plan.get("module_row_bwd_fused") and "ltc_sens_bwd" not in ktimes:
-        # the fused row backward: the chain launch also runs the sensory backward
+    if ((plan.get("module_row_bwd_fused") or plan.get("module_row128_rec_fused"))
+            and "ltc_sens_bwd" not in ktimes):
+        # the chain launch also runs the sensory backward (its companions)
         fl["ltc_ode_bwd"] += fl["ltc_sens_bwd"]
     if plan.get("module_row128_rec_fused") and "ltc_rec_grad" not in ktimes:
         # the Hp = 128 chain launch also forms the recurrent parameter-gradient sums
