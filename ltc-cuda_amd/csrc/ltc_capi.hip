@@ -383,7 +383,7 @@ BwdWs carve_bwd(const ltc::Plan& p, Carver& c, bool images = true) {
 // one per batch row when the fused row backward forms them.
 long long module_ln_parts(const ltc::Plan& p) {
   const long long n = ltc::ln_bwd_blocks(p);
-  return ltc::row_bwd_fused(p) && p.B > n ? p.B : n;
+  return (ltc::row_bwd_fused(p) || ltc::row128_sens_fused(p)) && p.B > n ? p.B : n;
 }
 
 // Module-path extras: the normalised input and its row statistics live in the
@@ -1028,14 +1028,15 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   const int* status = nullptr;
   const bool sens_comp = ltc::row128_sens_fused(p);
   if (ltc::row128_rec_fused(p)) {
-    // with D <= 128 the sensory backward runs in that launch too
+    // with D <= 128 the sensory and LayerNorm backward run in that launch too
     unsigned long long* words = row_words;
+    const long long spin = g_spin.load(std::memory_order_relaxed);
+    const ltc::RowCompanion sc{lw.xa, ln, input_w, ln_weight, ln_bias, wb.spart, lnpart,
+                               grad_x, words, spin};
     e = timed(ltc::K_ODE_BWD, s, [&] {
-      return ltc::launch_ode_bwd_row128_rec(
-          p, wb.pp, vsave, densave, grad_out, gs, grad_h_final, wb.dsn, wb.dsd, wb.npart,
-          grad_state, wb.rpart, words, g_spin.load(std::memory_order_relaxed),
-          sens_comp ? lw.xa : nullptr, sens_comp ? wb.spart : nullptr,
-          sens_comp ? wb.dxpart : nullptr, s);
+      return ltc::launch_ode_bwd_row128_rec(p, wb.pp, vsave, densave, grad_out, gs,
+                                            grad_h_final, wb.dsn, wb.dsd, wb.npart, grad_state,
+                                            wb.rpart, words, spin, sens_comp ? &sc : nullptr, s);
     });
     if (e != hipSuccess) return hip_fail("ODE backward launch", e);
     pf.NCH = p.B;
@@ -1060,10 +1061,11 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
     });
     if (e != hipSuccess) return hip_fail("sensory backward launch", e);
   }
-  e = timed(ltc::K_LN_BWD, s, [&] {
-    return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s, sens_comp ? 2 : 0);
-  });
-  if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
+  if (!sens_comp) {
+    e = timed(ltc::K_LN_BWD, s,
+              [&] { return ltc::launch_ln_bwd(p, lp, ln, wb.dxpart, grad_x, lnpart, s); });
+    if (e != hipSuccess) return hip_fail("LayerNorm backward launch", e);
+  }
   e = timed(ltc::K_FINALIZE, s, [&] {
     return ltc::launch_finalize_leaf(pf, lp, wb.rpart, wb.spart, wb.npart, lnpart, wb.ps, lg, s,
                                      status, grad_state);

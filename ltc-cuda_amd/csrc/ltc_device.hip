@@ -1000,14 +1000,21 @@ struct RecC {
   long long spin;
   int* status;  // the status word, after all words
   // Sensory companions (sensB null: none): each step's dL/dsn, dL/dsd as
-  // words [B][T][2][128] from the chain (instead of dsn / dsd), the rows xa,
-  // the backward sensory image, and their outputs: one sensory partial per
-  // row [B][4][Hp][Dp] and dL/dxa partials [2][B*T][Dp] over 64 neurons each.
+  // words [B][T][2][128] from the chain (instead of dsn / dsd), then the
+  // words [B][T][128] that hand the first half's dL/dxa to the second; the
+  // rows xa, the backward sensory image, and their outputs: one sensory
+  // partial per row [B][4][Hp][Dp]; the LayerNorm backward's dL/dx and one
+  // column partial per row [B][4][Dp].
   unsigned long long* sw;
   const float* xa;
   const float4* sensB;
   float* spart;
-  float* dxpart;
+  LnBuf ln;
+  const float* input_w;
+  const float* ln_w;
+  const float* ln_b;
+  float* gx;
+  float* lnpart;
   int D, Dp;
 };
 
@@ -1989,10 +1996,16 @@ __device__ __forceinline__ void rec_companion128(const BwdK& k, const RecC& rc, 
 // gradient sums; the second 64 inputs' operands in LDS). Per step 128
 // threads wait for the step's 128 words while the others stage its row of
 // xa; after the synapses, the 8 per-wave partials of dL/dxa[d] are summed in
-// a fixed order into this half's partial dxpart[jt][row][d], from which the
-// LayerNorm backward launch continues. At the end the companion writes its
-// half of the row's sensory partial and returns its words to tag 0; a wait
-// that runs out sets the status word and no partial is written.
+// a fixed order. The first half (jt = 0) hands its sum to the second as one
+// word per input; wave 0 of the second half waits for it, adds its own sum
+// (dL/dxa = first + second, as the two-partial LayerNorm backward adds them)
+// and finishes the row's LayerNorm backward as ln_bwd_kernel does: dL/dx and
+// the column sums of the LayerNorm and input-affine gradients. The second
+// half is later in the grid than the first, so it never waits on a workgroup
+// dispatched after it. At the end each companion writes its half of the row's
+// sensory partial (the second also its LayerNorm column partial) and returns
+// the words it consumed to tag 0; a wait that runs out sets the status word
+// and no partial is written.
 template <int DC>
 __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc, int b, int jt) {
   constexpr int HP = 128, NX = 64 * DC;
@@ -2005,6 +2018,7 @@ __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc,
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int T = k.T, D = rc.D, Dp = rc.Dp;
   const int h0 = 64 * jt + 8 * w;
+  const bool fin = jt == 1 && w == 0;  // the wave that finishes the LayerNorm backward
   float4 q[8], sa[DC][8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
@@ -2013,12 +2027,35 @@ __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc,
 #pragma unroll
     for (int kk = 0; kk < DC; ++kk) sa[kk][m] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  float iw[DC], lw[DC], lb[DC], cw[DC], cb[DC], cl[DC], cbl[DC];
+#pragma unroll
+  for (int kk = 0; kk < DC; ++kk) {
+    const int d = lane + 64 * kk;
+    const bool in = fin && d < D;
+    iw[kk] = in ? rc.input_w[d] : 0.f;
+    lw[kk] = in ? rc.ln_w[d] : 0.f;
+    lb[kk] = in ? rc.ln_b[d] : 0.f;
+    cw[kk] = cb[kk] = cl[kk] = cbl[kk] = 0.f;
+  }
   if (tid == 0) *flag = 0;
   __syncthreads();
   unsigned long long* words = rc.sw + (long long)b * T * 2 * HP;
-  const long long BT = (long long)k.B * T;
+  // the row's dL/dxa hand-over words, [T][128]
+  unsigned long long* dxw = rc.sw + (long long)k.B * T * 2 * HP + (long long)b * T * HP;
   for (int t = T - 1; t >= 0; --t) {
     const long long row = (long long)b * T + t;
+    // the finishing wave's LayerNorm inputs of the row, requested before the wait
+    float mean = 0.f, rstd = 0.f, xr[DC];
+    if (fin) {
+      mean = rc.ln.stats[2 * row];
+      rstd = rc.ln.stats[2 * row + 1];
+      const float* xrow = rc.ln.x + (long long)b * rc.ln.xs.b + (long long)t * rc.ln.xs.t;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        xr[kk] = d < D ? xrow[(long long)d * rc.ln.xs.c] : 0.f;
+      }
+    }
     if (tid < 128) {
       const int qq = tid >> 6;  // 0: dL/dsn, 1: dL/dsd
       unsigned long long* wd = words + ((long long)t * 2 + qq) * HP + 64 * jt + lane;
@@ -2066,13 +2103,59 @@ __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc,
       __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-    if (tid < NX) {
-      float sxa = 0.f;
+    if (jt == 0) {
+      if (tid < D) {
+        float sxa = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < 8; ++ww) sxa += dxr[ww * NX + tid];
-      if (tid < Dp) rc.dxpart[((long long)jt * BT + row) * Dp + tid] = sxa;
+        for (int ww = 0; ww < 8; ++ww) sxa += dxr[ww * NX + tid];
+        xch_put(dxw + (long long)t * HP + tid, sxa, 1u);
+      }
+    } else if (w == 0) {
+      float xh[DC], gxh[DC];
+      float s1 = 0.f, s2 = 0.f;
+      bool ok = true;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        xh[kk] = gxh[kk] = 0.f;
+        if (d < D) {
+          float own = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < 8; ++ww) own += dxr[ww * NX + d];
+          unsigned long long* wd = dxw + (long long)t * HP + d;
+          unsigned long long v = xch_get(wd);
+          const long long t0 = wall_clock64();
+          while ((unsigned)(v >> 32) != 1u) {
+            if (wall_clock64() - t0 > rc.spin) {
+              ok = false;
+              break;
+            }
+            v = xch_get(wd);
+          }
+          const float gxa = __uint_as_float((unsigned)v) + own;
+          xh[kk] = (xr[kk] - mean) * rstd;
+          const float xn = xh[kk] * lw[kk] + lb[kk];
+          const float gxn = gxa * iw[kk];
+          gxh[kk] = gxn * lw[kk];
+          cw[kk] = fmaf(gxa, xn, cw[kk]);
+          cb[kk] += gxa;
+          cl[kk] = fmaf(gxn, xh[kk], cl[kk]);
+          cbl[kk] += gxn;
+          s1 += gxh[kk];
+          s2 = fmaf(gxh[kk], xh[kk], s2);
+        }
+      }
+      // seen by every wave after the next step's first barrier, or the one below
+      if (!ok) *flag = 1;
+      const float m1 = wave_sum(s1) / (float)D, m2 = wave_sum(s2) / (float)D;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        if (d < D) rc.gx[row * D + d] = rstd * (gxh[kk] - m1 - xh[kk] * m2);
+      }
     }
   }
+  __syncthreads();
   const bool gave_up = *flag != 0;
   if (!gave_up) {
     // this half of the row's sensory partial, layout [4][Hp][Dp] as sens_bwd_kernel's
@@ -2088,11 +2171,26 @@ __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc,
         out[2 * DH + e] = sa[kk][m].z;
         out[3 * DH + e] = sa[kk][m].w;
       }
+    if (fin) {
+      float* lo = rc.lnpart + (long long)b * 4 * Dp;
+#pragma unroll
+      for (int kk = 0; kk < DC; ++kk) {
+        const int d = lane + 64 * kk;
+        if (d < Dp) {
+          lo[d] = cw[kk];
+          lo[Dp + d] = cb[kk];
+          lo[2 * Dp + d] = cl[kk];
+          lo[3 * Dp + d] = cbl[kk];
+        }
+      }
+    }
   }
-  // this companion's words back to tag 0, every step consumed
+  // this companion's words back to tag 0, every step consumed (the second
+  // half also clears the row's hand-over words)
   for (int e = tid; e < T * 128; e += (int)blockDim.x) {
     const int t = e >> 7, r = e & 127;
     xch_put(words + ((long long)t * 2 + (r >> 6)) * HP + 64 * jt + (r & 63), 0.f, 0u);
+    if (jt == 1) xch_put(dxw + e, 0.f, 0u);
   }
   if (gave_up && tid == 0)
     __hip_atomic_store(rc.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -4412,22 +4510,33 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
                                      const float* densave, const float* gout, Strides3 gs,
                                      const float* ghfin, float* dsn, float* dsd, float* npart,
                                      float* gstate, float* rpart, unsigned long long* words,
-                                     long long spin, const float* xa, float* spart,
-                                     float* dxpart, hipStream_t s) {
+                                     long long spin, const RowCompanion* sc, hipStream_t s) {
   if (!row128_rec_fused(p) || pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr ||
       pp.recF == nullptr || words == nullptr)
     return hipErrorInvalidValue;
-  const bool sens = xa != nullptr;
-  if (sens && (!row128_sens_fused(p) || pp.sensB == nullptr || spart == nullptr ||
-               dxpart == nullptr))
+  const bool sens = sc != nullptr;
+  if (sens && (!row128_sens_fused(p) || pp.sensB == nullptr || sc->xa == nullptr ||
+               sc->spart == nullptr || sc->lnpart == nullptr || sc->gx == nullptr ||
+               sc->ln.stats == nullptr || sc->ln.x == nullptr))
     return hipErrorInvalidValue;
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, nullptr, dsn, dsd, npart, gstate,
          rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, words};
   const long long nrec = (long long)p.B * p.T * p.U * 256;
   unsigned long long* sw = sens ? words + nrec : nullptr;
   int* status = reinterpret_cast<int*>(words + row_bwd_words(p) - 1);
-  const RecC rc{pp.recF, spin, status, sw, xa, sens ? pp.sensB : nullptr, spart, dxpart, p.D,
-                p.Dp};
+  RecC rc{pp.recF, spin, status, sw, nullptr, nullptr, nullptr, {}, nullptr, nullptr, nullptr,
+          nullptr, nullptr, p.D, p.Dp};
+  if (sens) {
+    rc.xa = sc->xa;
+    rc.sensB = pp.sensB;
+    rc.spart = sc->spart;
+    rc.ln = sc->ln;
+    rc.input_w = sc->input_w;
+    rc.ln_w = sc->ln_w;
+    rc.ln_b = sc->ln_b;
+    rc.gx = sc->gx;
+    rc.lnpart = sc->lnpart;
+  }
   const int Bc = (p.B + 7) / 8 * 8;
   const dim3 grid((unsigned)((sens ? 4 : 2) * Bc + p.B)), block(512);
   const size_t lds = bwd_lds_bytes(p);
@@ -4591,10 +4700,10 @@ int ln_bwd_blocks(const Plan& p) {
 }
 
 hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
-                         const float* dxpart, float* gx, float* lnpart, hipStream_t s, int hb) {
+                         const float* dxpart, float* gx, float* lnpart, hipStream_t s) {
   const dim3 grid(ln_bwd_blocks(p)), block(256);
-  // hb: the dL/dxa partials per row (those of 32-neuron blocks by default)
-  const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = hb > 0 ? hb : p.Hp / 32;
+  // the dL/dxa partials per row: those of the 32-neuron blocks
+  const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = p.Hp / 32;
 #define LTC_LNB(C) hipLaunchKernelGGL((ln_bwd_kernel<C>), grid, block, 0, s, lp, ln, dxpart, gx, lnpart, p.T, p.D, p.Dp, BT, HB, rpb)
   if (p.D <= 64) LTC_LNB(1);
   else if (p.D <= 128) LTC_LNB(2);
@@ -4612,7 +4721,8 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
   Partials pt;
   hipError_t e = presum(p, rpart, npart, ps, s, pt);
   if (e != hipSuccess) return e;
-  int nln = ln_bwd_blocks(p);
+  // one LayerNorm partial per row when the sensory companions formed them
+  int nln = row128_sens_fused(p) ? p.B : ln_bwd_blocks(p);
   if (presum_parts(nln) > 0) {
     const int parts = presum_parts(nln), rpb = (nln + parts - 1) / parts;
     const long long N = 4LL * p.Dp;

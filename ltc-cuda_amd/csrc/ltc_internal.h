@@ -341,11 +341,12 @@ inline bool row_bwd_fused(const Plan& p) {
 inline bool row128_rec_fused(const Plan& p) {
   return row_wave128_bwd(p) && p.B >= 1 && p.B <= 64;
 }
-// With Dp <= 128 the sensory backward also runs in companion workgroups of
-// that launch, two per row (64 neurons each), taking each step's dL/dsn,
-// dL/dsd as words [B][T][2][128] after the alpha/beta words; they write one
-// sensory partial per row and dL/dxa partials over 64 neurons for the
-// LayerNorm backward.
+// With Dp <= 128 the sensory and LayerNorm backward also run in companion
+// workgroups of that launch, two per row (64 neurons each), taking each
+// step's dL/dsn, dL/dsd as words [B][T][2][128] after the alpha/beta words;
+// the first hands its dL/dxa sums to the second as words [B][T][128], which
+// finishes the LayerNorm backward. They write one sensory partial and one
+// LayerNorm column partial per row, and dL/dx.
 inline bool row128_sens_fused(const Plan& p) { return row128_rec_fused(p) && p.Dp <= 128; }
 // Exchange words of the fused row backward (row_bwd_fused) or of the Hp = 128
 // chain with recurrent-gradient companions (row128_rec_fused); the last one
@@ -353,7 +354,7 @@ inline bool row128_sens_fused(const Plan& p) { return row128_rec_fused(p) && p.D
 inline long long row_bwd_words(const Plan& p) {
   if (row_bwd_fused(p)) return (long long)p.B * p.T * 128 + 1;
   if (row128_rec_fused(p))
-    return (long long)p.B * p.T * p.U * 256 + (row128_sens_fused(p) ? (long long)p.B * p.T * 256 : 0) + 1;
+    return (long long)p.B * p.T * p.U * 256 + (row128_sens_fused(p) ? (long long)p.B * p.T * 384 : 0) + 1;
   return 0;
 }
 inline int cmp_chunks_fwd(const Plan& p) {
@@ -485,7 +486,7 @@ struct LeafGrads {
 // writes dL/dx and per-block column partials lnpart[nblk][4][Dp].
 int ln_bwd_blocks(const Plan& p);
 hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
-                         const float* dxpart, float* gx, float* lnpart, hipStream_t s, int hb = 0);
+                         const float* dxpart, float* gx, float* lnpart, hipStream_t s);
 // With a status word (the companions of a row128_rec_fused chain), every
 // output (also dL/dx and dL/dh0 = gstate) becomes NaN when it is set.
 hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float* rpart,
@@ -513,14 +514,14 @@ struct RowCompanion {
 // The Hp = 128 chain with recurrent-gradient companions (row128_rec_fused):
 // rpart receives one partial per batch row, [B][4][Hp][Hp]; a companion that
 // runs out of its wait budget sets the status word after the words.
-// With xa (row128_sens_fused), also the sensory companions: spart receives one
-// partial per row, dxpart the dL/dxa partials [2][B*T][Dp].
+// With sc (row128_sens_fused), also the sensory companions, which run the
+// sensory and LayerNorm backward as RowCompanion describes (its words and
+// spin unused: those of this call hold).
 hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const float* vsave,
                                      const float* densave, const float* gout, Strides3 gs,
                                      const float* ghfin, float* dsn, float* dsd, float* npart,
                                      float* gstate, float* rpart, unsigned long long* words,
-                                     long long spin, const float* xa, float* spart,
-                                     float* dxpart, hipStream_t s);
+                                     long long spin, const RowCompanion* sc, hipStream_t s);
 hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const float* vsave,
                                     const float* densave, const float* gout, Strides3 gs,
                                     const float* ghfin, float* npart, float* gstate, float* rpart,
