@@ -311,6 +311,7 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     ((24, 8, 129, 64, 6), 0, 0, 0),     # D > 128
     ((24, 8, 128, 62, 6), 0, 1, 0),     # H not a multiple of 4
     ((5, 3, 40, 100, 6), 1, 0, 1),      # H below Hp = 128
+    ((6, 3, 100, 120, 6), 1, 0, 1),     # two ragged 64-input blocks at Hp = 128
     ((65, 2, 40, 128, 6), 0, 0, 0),     # B > 64
     ((4096, 4, 64, 64, 6), 0, 0, 0),    # C5
     ((256, 64, 256, 256, 6), 0, 0, 0),  # C3

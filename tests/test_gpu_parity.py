@@ -381,7 +381,8 @@ def test_full_size_forward_rows_and_backward_linearity(cfg):
 # --------------------------------------------------------------------------- module path
 
 MODULE_SHAPES = [(4, 8, 32, 16), (2, 4, 32, 33), (24, 8, 128, 64), (3, 2, 100, 65),
-                 (2, 3, 1024, 8), (2, 2, 1100, 8), (6, 3, 48, 130)]
+                 (2, 3, 1024, 8), (2, 2, 1100, 8), (6, 3, 48, 130),
+                 (6, 3, 100, 120)]  # Hp = 128 companions over two ragged 64-input blocks
 
 
 @pytest.mark.parametrize("shape", MODULE_SHAPES, ids=lambda s: "B%dT%dD%dH%d" % s)
