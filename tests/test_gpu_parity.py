@@ -566,7 +566,7 @@ def test_hip_graph_capture_replays_match_eager():
 
 
 @pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60), (8, 4, 40, 128), (5, 3, 40, 100),
-                                   (64, 2, 20, 65)],
+                                   (64, 2, 20, 65), (6, 3, 100, 120)],
                          ids=lambda s: "B%dT%dD%dH%d" % s)
 def test_module_backward_twice_over_one_forward(shape):
     """Two backward passes over one forward (retain_graph) with different
