@@ -4539,7 +4539,12 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
   }
   const int Bc = (p.B + 7) / 8 * 8;
   const dim3 grid((unsigned)((sens ? 4 : 2) * Bc + p.B)), block(512);
-  const size_t lds = bwd_lds_bytes(p);
+  // the chain's LDS (its staged rows), or a sensory companion's when larger
+  // (a recurrent-gradient companion needs about 2 KB)
+  const int DC = p.Dp > 64 ? 2 : 1;
+  const size_t comp =
+      sens ? (size_t)((DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9 * 64 * DC * 4 + 16) : 0;
+  const size_t lds = bwd_lds_bytes(p) > comp ? bwd_lds_bytes(p) : comp;
 #define LTC_W128(F, C) \
   hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<F, C>), grid, block, lds, s, a, rc)
   if (p.H == 128) {
