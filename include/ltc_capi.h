@@ -287,7 +287,9 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * Launch plan of one call, for diagnostics and host-side bounds tests. No
  * counterpart in the reference. Writes up to n of: Hp, Dp, NB (batch rows
  * per ODE workgroup), KS (reduction split), RC (= Hp/KS), threads per ODE
- * workgroup, forward LDS bytes, backward LDS bytes, NCH (recurrent gradient
+ * workgroup, forward LDS bytes, backward LDS bytes (the chain launch's
+ * request: with the module path's sensory companions, the larger of the
+ * chain's and a companion's), NCH (recurrent gradient
  * chunks, or one per workgroup when fused), NRC (sensory backward row
  * chunks), ODE workgroups, 1 when the recurrent parameter gradients are
  * accumulated inside the chain kernel, then the chain kernel's own KS, RC
@@ -320,10 +322,16 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
  * needed), the whole cluster leaves early, and the call then overwrites
  * every output it writes (out, h_final and saved for a forward; every
  * gradient for a backward) with NaN and raises a sticky per-device fault flag.
- * The module-path backward at H <= 64 (one batch row per workgroup, D <= 128,
- * B <= 64) runs its sensory and LayerNorm backward in companion workgroups
- * that wait for the chain workgroups the same bounded way, with the same
- * outcome (every gradient NaN, the flag raised) when one runs out.
+ * The module-path backward with one batch row per workgroup and B <= 64 also
+ * runs companion workgroups that wait for the chain workgroups the same
+ * bounded way, with the same outcome (every gradient, dL/dx and dL/dh0 NaN,
+ * the flag raised) when one runs out:
+ *   - at H <= 64 and D <= 128, one companion per row runs the sensory and
+ *     LayerNorm backward from each step's dL/dsn, dL/dsd;
+ *   - at 64 < H <= 128, two companions per row form the recurrent
+ *     parameter-gradient sums from each unfold's alpha and beta, and with
+ *     D <= 128 two more per row run the sensory and LayerNorm backward, the
+ *     second of them also waiting for the first's dL/dxa sums.
  * The call itself has already returned LTC_OK by then (it only queues work);
  * ltc_device_status() waits for the current device, returns LTC_EHIP with a
  * message when the flag is raised, and clears it when `clear` is nonzero.

@@ -1451,7 +1451,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
   const long long v[LTC_PLAN_FIELDS] = {
       p.Hp, p.Dp, p.NB, p.KS, p.RC, cols * p.KS,
       p.CP > 0 ? ltc::cluster_fwd_lds(p) : ltc::fwd_lds(p),
-      p.CP > 0 ? ltc::cluster_bwd_lds(p) : ltc::chain_lds(p),
+      p.CP > 0 ? ltc::cluster_bwd_lds(p) : ltc::chain_launch_lds(p),
       p.NCH, p.NRC, p.CP > 0 ? (long long)p.NCL * p.CP : (B + p.NB - 1) / p.NB,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,

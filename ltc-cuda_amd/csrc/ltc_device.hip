@@ -4540,11 +4540,7 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
   const int Bc = (p.B + 7) / 8 * 8;
   const dim3 grid((unsigned)((sens ? 4 : 2) * Bc + p.B)), block(512);
   // the chain's LDS (its staged rows), or a sensory companion's when larger
-  // (a recurrent-gradient companion needs about 2 KB)
-  const int DC = p.Dp > 64 ? 2 : 1;
-  const size_t comp =
-      sens ? (size_t)((DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9 * 64 * DC * 4 + 16) : 0;
-  const size_t lds = bwd_lds_bytes(p) > comp ? bwd_lds_bytes(p) : comp;
+  const size_t lds = sens ? (size_t)chain_launch_lds(p) : bwd_lds_bytes(p);
 #define LTC_W128(F, C) \
   hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<F, C>), grid, block, lds, s, a, rc)
   if (p.H == 128) {
@@ -4569,8 +4565,7 @@ hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const floa
   const dim3 grid((unsigned)(Bc + p.B)), block(512);
   const int DC = p.Dp / 64;
   // the chain's LDS (its gradient tile), or the companion's when larger
-  const size_t comp = (size_t)((DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9 * 64 * DC * 4 + 16);
-  const size_t lds = bwd_lds_bytes(p) > comp ? bwd_lds_bytes(p) : comp;
+  const size_t lds = (size_t)chain_launch_lds(p);
 #define LTC_RBF(F, C) \
   hipLaunchKernelGGL((ode_bwd_row_fused_kernel<F, C>), grid, block, lds, s, a, rc, pp.sensB, p.D, p.Dp, Bc)
   if (p.H == 64) {

@@ -337,9 +337,15 @@ inline bool row_bwd_fused(const Plan& p) {
 // (64 postsynaptic neurons each) that take each unfold's alpha/beta from the
 // row's chain workgroup as {value, tag} words ([B][T*U][2][128], then a
 // status word), instead of by rec_grad_kernel afterwards: one recurrent
-// partial per row.
+// partial per row. The words live in the module's saved buffer from the
+// forward to the backward, 2 KiB per (row, unfold), so the companions are
+// chosen only while they take at most 64 MiB (B*T*U <= 32768); longer
+// sequences save alpha/beta for rec_grad_kernel instead (8 bytes per neuron
+// and unfold, in the backward's workspace).
+constexpr long long kRow128WordUnfolds = 32768;
 inline bool row128_rec_fused(const Plan& p) {
-  return row_wave128_bwd(p) && p.B >= 1 && p.B <= 64;
+  return row_wave128_bwd(p) && p.B >= 1 && p.B <= 64 &&
+         (long long)p.B * p.T * p.U <= kRow128WordUnfolds;
 }
 // With Dp <= 128 the sensory and LayerNorm backward also run in companion
 // workgroups of that launch, two per row (64 neurons each), taking each
@@ -410,6 +416,24 @@ inline long long chain_lds(const Plan& p) {
   const long long plane =
       p.FUSE ? (row_kernels(p) ? 4LL : 1LL) * p.Hp * (p.Hp + 1) * 4 : 0;
   return base > plane ? base : plane;
+}
+
+// Dynamic LDS of a sensory companion workgroup (the fused row backward at
+// Hp = 64, and the sensory companions of the Hp = 128 chain), over DC
+// 64-input blocks: the operands of every block past the first
+// [8 waves][8][64] float4, one [64] float2 row, the [9][64 * DC] float sums
+// and a flag word.
+inline long long sens_companion_lds(int DC) {
+  return (long long)(DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9LL * 64 * DC * 4 + 16;
+}
+// Dynamic LDS the module backward's chain launch requests: the chain's own,
+// or its sensory companions' when larger (a recurrent-gradient companion of
+// the Hp = 128 chain needs about 2 KB, under the chain's staging).
+inline long long chain_launch_lds(const Plan& p) {
+  const long long c = chain_lds(p);
+  if (!row_bwd_fused(p) && !row128_sens_fused(p)) return c;
+  const long long comp = sens_companion_lds(p.Dp / 64);
+  return c > comp ? c : comp;
 }
 
 hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, const float* sd,

@@ -734,9 +734,12 @@ def require_kernels():
 
 
 def device_status(clear: bool = True) -> None:
-    """Raise RuntimeError if a cluster launch (H > 192) on the current device
-    gave up waiting for its partner workgroups since the last check; the
-    outputs of that call were set to NaN. Synchronises the device."""
+    """Raise RuntimeError if a launch on the current device gave up waiting
+    for its partner workgroups since the last check: a cluster launch
+    (H > 192), or the companion workgroups of a module backward with one batch
+    row per workgroup (the sensory and LayerNorm companions at H <= 64, the
+    recurrent-gradient and sensory companions at 64 < H <= 128). The outputs
+    of that call were set to NaN. Synchronises the device."""
     require_kernels().capi.device_status(clear)
 
 
@@ -813,7 +816,7 @@ class CapturedStep:
     """One training step of a module (forward, loss, backward) as one HIP graph.
 
     At small sizes a step is bound by the host: at B=24 T=8 D=128 H=64 the
-    GPU work is about 0.1 ms (seven library kernels plus the loss and its
+    GPU work is about 0.08 ms (four library kernels plus the loss and its
     gradient), while issuing it eagerly through autograd costs more host time
     than that. Replaying the captured step issues it with one graph launch.
 

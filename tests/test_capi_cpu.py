@@ -239,12 +239,20 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
             assert p["lds_fwd"] == max(Hp * 4 + p["KS"] * Hp * 8, row_f)
         planes = 4 if (NB == 1 and Hp == 64) else 1
         plane = planes * Hp * (Hp + 1) * 4 if p["fuse"] else 0
+        # the module backward's sensory companions in the chain launch (Hp = 64
+        # or 128, one row per workgroup, Dp <= 128, B <= 64): operands of the
+        # second 64-input block in LDS, the step's row, per-wave sums, a flag
+        comp = 0
+        if p["module_row_bwd_fused"] or (p["module_row128_rec_fused"] and p["Dp"] <= 128):
+            DC = p["Dp"] // 64
+            comp = (DC - 1) * 8 * 8 * 64 * 16 + 64 * 8 + 9 * 64 * DC * 4 + 16
         if NB == 1 and Hp == 128 and not p["fuse"] and KSB == 8 and p["RCB"] == 16:
             # the unfused wave-owned single-row chain: alpha/beta by parity and
             # 48 unfolds of staged v, 1/den and dL/dout rows
-            assert p["lds_bwd"] == 2 * Hp * 8 + (3 * 48 + 1) * Hp * 4 <= 159 * 1024
+            chain = 2 * Hp * 8 + (3 * 48 + 1) * Hp * 4
         else:
-            assert p["lds_bwd"] == max(base, plane) <= 159 * 1024
+            chain = max(base, plane)
+        assert p["lds_bwd"] == max(chain, comp) <= 159 * 1024
     assert 1 <= p["NRC"] <= 64
     if p["CP"] > 0:
         # Cluster path: CP members of 64 columns each, the whole grid resident
@@ -303,6 +311,18 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     assert capi.plan(4096, 4, 64, 64, 6)["CP"] == 0     # C5
 
 
+@pytest.mark.parametrize("shape,lds", [
+    # D = 100, H = 120: the Hp = 128 chain's staging (76288 B) beats the
+    # sensory companion's (DC = 2: 70672 B)
+    ((6, 3, 100, 120, 6), 2 * 128 * 8 + (3 * 48 + 1) * 128 * 4),
+    ((32, 16, 128, 128, 6), 2 * 128 * 8 + (3 * 48 + 1) * 128 * 4),  # C2
+    # C1: the companion's (70672 B) beats the chain's four gradient planes (66560 B)
+    ((24, 8, 128, 64, 6), 8 * 8 * 64 * 16 + 64 * 8 + 9 * 128 * 4 + 16),
+])
+def test_chain_launch_lds_covers_the_companions(capi, shape, lds):
+    assert capi.plan(*shape)["lds_bwd"] == lds
+
+
 @pytest.mark.parametrize("shape,sens_in_prep,row_bwd,rec128", [
     ((24, 8, 128, 64, 6), 1, 1, 0),     # C1: 192 row blocks, companions in the chain launch
     ((3, 5, 40, 60, 6), 1, 1, 0),
@@ -313,6 +333,10 @@ def test_cluster_path_is_planned_for_the_large_configurations(capi):
     ((5, 3, 40, 100, 6), 1, 0, 1),      # H below Hp = 128
     ((6, 3, 100, 120, 6), 1, 0, 1),     # two ragged 64-input blocks at Hp = 128
     ((65, 2, 40, 128, 6), 0, 0, 0),     # B > 64
+    ((100, 2, 40, 100, 6), 0, 0, 0),    # B > 64 below Hp = 128: rec_grad after the chain
+    ((4, 3, 200, 100, 6), 0, 0, 1),     # D > 128: recurrent-gradient companions only
+    ((64, 85, 40, 100, 6), 0, 0, 1),    # B*T*U = 32640: the words fit their 64 MiB budget
+    ((64, 86, 40, 100, 6), 0, 0, 0),    # B*T*U = 33024: alpha/beta saved for rec_grad
     ((4096, 4, 64, 64, 6), 0, 0, 0),    # C5
     ((256, 64, 256, 256, 6), 0, 0, 0),  # C3
 ])

@@ -123,7 +123,8 @@ def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi, D1):
 
 
 
-@pytest.mark.parametrize("shape", [(32, 4, 128, 128), (5, 3, 40, 100)], ids=lambda s: "B%dT%dD%dH%d" % s)
+@pytest.mark.parametrize("shape", [(32, 4, 128, 128), (5, 3, 40, 100), (4, 3, 200, 100)],
+                         ids=lambda s: "B%dT%dD%dH%d" % s)
 def test_recurrent_gradient_companions_give_up_sets_every_gradient_to_nan(capi, shape):
     """At Hp = 128 the module backward forms the recurrent parameter-gradient
     sums in companion workgroups that wait for the chain's alpha/beta words:

@@ -382,7 +382,14 @@ def test_full_size_forward_rows_and_backward_linearity(cfg):
 
 MODULE_SHAPES = [(4, 8, 32, 16), (2, 4, 32, 33), (24, 8, 128, 64), (3, 2, 100, 65),
                  (2, 3, 1024, 8), (2, 2, 1100, 8), (6, 3, 48, 130),
-                 (6, 3, 100, 120)]  # Hp = 128 companions over two ragged 64-input blocks
+                 (6, 3, 100, 120),  # Hp = 128 companions over two ragged 64-input blocks
+                 # Hp = 128, D > 128: the recurrent-gradient companions alone; the
+                 # chain writes dL/dsn, dL/dsd, then the sensory and LayerNorm
+                 # backward launches
+                 (4, 3, 200, 100),
+                 # Hp = 128, B > 64: alpha/beta saved, then the recurrent-gradient,
+                 # sensory and LayerNorm backward launches
+                 (100, 2, 40, 100)]
 
 
 @pytest.mark.parametrize("shape", MODULE_SHAPES, ids=lambda s: "B%dT%dD%dH%d" % s)
@@ -566,7 +573,7 @@ def test_hip_graph_capture_replays_match_eager():
 
 
 @pytest.mark.parametrize("shape", [(24, 8, 128, 64), (5, 3, 40, 60), (8, 4, 40, 128), (5, 3, 40, 100),
-                                   (64, 2, 20, 65), (6, 3, 100, 120)],
+                                   (64, 2, 20, 65), (6, 3, 100, 120), (4, 3, 200, 100)],
                          ids=lambda s: "B%dT%dD%dH%d" % s)
 def test_module_backward_twice_over_one_forward(shape):
     """Two backward passes over one forward (retain_graph) with different
