@@ -84,18 +84,18 @@ def kernel_flops(c, fused_chain, counts=None):
     backward 22; per recurrent synapse-unfold, the forward 10 and the chain 14
     (sigmoid recompute 6, sigmoid' 2, delta 4, dv 2), plus the 8 of the four
     parameter-gradient sums, which the fused chain does itself (22) and
-    rec_grad does otherwise. Recurrent synapses count as the kernels evaluate
-    them (counts: syn_counts; the compacted kernels skip masked ones).
+    rec_grad does otherwise. Without `counts` every synapse counts, masked or
+    not (the unit's dense work); with `counts` (syn_counts) synapses count as
+    the kernels evaluate them (the compacted kernels skip masked ones).
     Per-neuron, LayerNorm and finalize work is not counted."""
     counts = counts or syn_counts(c)
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
-    sens = counts["sens"]
     return {
-        "ltc_sens_fwd": 10 * sens,
+        "ltc_sens_fwd": 10 * counts["sens_fwd"],
         "ltc_ode_fwd": 10 * counts["rec_fwd"],
         "ltc_ode_bwd": 22 * counts["rec_bwd"] if fused_chain else 14 * counts.get("rec_dv", rec),
-        "ltc_rec_grad": 8 * rec,
-        "ltc_sens_bwd": 22 * sens,
+        "ltc_rec_grad": 8 * counts["rec_bwd"],
+        "ltc_sens_bwd": 22 * counts["sens_bwd"],
         "ltc_prep": 0,
         "ltc_ln_bwd": 0,
         "ltc_finalize": 0,
@@ -187,7 +187,7 @@ def kernel_times(capi, fn, iters):
     return {k: (ms / n, n // iters) for k, (ms, n) in t.items() if n > 0}
 
 
-def roofline(c, ktimes, plan, traffic=None, counts=None):
+def _kernel_flops_by_launch(c, plan, ktimes, counts=None):
     fl = kernel_flops(c, bool(plan["fuse"]), counts)
     if ((plan.get("module_row_bwd_fused") or plan.get("module_row128_rec_fused"))
             and "ltc_sens_bwd" not in ktimes):
@@ -199,16 +199,30 @@ def roofline(c, ktimes, plan, traffic=None, counts=None):
     if plan.get("module_sens_in_prep") and "ltc_sens_fwd" not in ktimes:
         # the prep launch forms the sensory sums of the module forward
         fl["ltc_prep"] += fl["ltc_sens_fwd"]
+    return fl
+
+
+def roofline(c, ktimes, plan, traffic=None, counts=None):
+    """Dominant kernel of the step against the FP32 peak. `frac` prices the
+    unit's dense work (every synapse, masked or not: SURVEY's FLOP_fwd = 10 and
+    FLOP_bwd = 22 per synapse); `frac_evaluated` the synapses the kernels
+    actually evaluate (the compacted kernels skip masked ones)."""
+    fl = _kernel_flops_by_launch(c, plan, ktimes)
+    fle = _kernel_flops_by_launch(c, plan, ktimes, counts)
     per_step = {k: avg * per for k, (avg, per) in ktimes.items()}
     dom = max(per_step, key=per_step.get)
     avg_ms = ktimes[dom][0]
     achieved = fl[dom] / (avg_ms * 1e-3) / 1e12
+    achieved_e = fle[dom] / (avg_ms * 1e-3) / 1e12
     return {"bound": "valu", "kernel": dom, "achieved": round(achieved, 4),
             "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TFLOPS, 5),
             "traffic": None if traffic is None else traffic.get(dom),
             "avg_launch_ms": round(avg_ms, 5),
-            "flop_per_launch": fl[dom]}
+            "flop_per_launch": fl[dom],
+            "achieved_evaluated": round(achieved_e, 4),
+            "frac_evaluated": round(achieved_e / PEAK_FP32_TFLOPS, 5),
+            "flop_per_launch_evaluated": fle[dom]}
 
 
 # Minimum instruction mix per synapse evaluation: (FMA-class, v_exp_f32, v_rcp_f32).
@@ -225,52 +239,176 @@ def mask_density(m):
 
 
 def syn_counts(c, plan=None, density=(1.0, 1.0)):
-    """Synapse evaluations per step: sensory, recurrent forward and recurrent
-    chain as the kernels run them (the compacted Hp = 256 kernels skip the
-    recurrent synapses with a zero mask entry: plan fields cmp_fwd / cmp_bwd),
-    and the layer's active-only count (both masks' densities)."""
+    """Synapse evaluations per step as the kernels run them, and the layer's
+    active-only count (both masks' densities):
+    - sens_fwd: the compacted sensory launch skips masked sensory synapses
+      (every sensory launch; the dense form only when the module forward forms
+      the sums in its parameter-image launch: plan field module_sens_in_prep);
+    - sens_bwd: the sensory backward evaluates every sensory synapse;
+    - rec_fwd / rec_dv: the compacted forward and chain skip masked recurrent
+      synapses (plan fields cmp_fwd / cmp_bwd);
+    - rec_bwd: the parameter-gradient sums, skipped with the chain only when
+      the chain forms them itself (fuse); an unfused chain's rec_grad pass
+      evaluates every synapse."""
     rho_r, rho_s = density
     sens = c["B"] * c["T"] * c["D"] * c["H"]
     rec = c["B"] * c["T"] * c["U"] * c["H"] ** 2
     plan = plan or {}
-    # an unfused chain skips synapses for dL/dv only; its rec_grad pass still
-    # evaluates every synapse's parameter sums
     skip_bwd = plan.get("cmp_bwd") and plan.get("fuse")
-    return {"sens": sens,
+    sens_cmp = bool(plan) and not plan.get("module_sens_in_prep")
+    return {"sens_fwd": sens * (rho_s if sens_cmp else 1.0),
+            "sens_bwd": sens,
             "rec_fwd": rec * (rho_r if plan.get("cmp_fwd") else 1.0),
             "rec_bwd": rec * (rho_r if skip_bwd else 1.0),
             "rec_dv": rec * (rho_r if plan.get("cmp_bwd") else 1.0),
             "active": sens * rho_s + rec * rho_r}
 
 
-def mix_bound_ms(c, which, counts=None):
+def mix_bound_ms(c, which, counts=None, clock_scale=1.0):
     """Mix-aware VALU bound: the minimum mix of every synapse evaluation, each
     instruction class at the issue rate the probe measured on this GPU
     (lane-ops per CU per clock), issued one after another (the probe's synapse
-    kernel confirms the classes do not overlap). With `counts` (syn_counts) the
-    recurrent synapses are priced as the kernels evaluate them: forward part
-    (4, 1, 1) for each forward evaluation, the backward's (12, 1, 1) for each
-    chain evaluation."""
+    kernel confirms the classes do not overlap). Without `counts` every synapse
+    is priced (the unit's dense work); with `counts` (syn_counts) synapses are
+    priced as the kernels evaluate them: the forward part (4, 1, 1) for each
+    forward evaluation, the backward's (12, 1, 1) for each backward one.
+    `clock_scale` = (engine clock while the probe ran) / (engine clock while
+    the priced kernels ran): the probe's rates hold per clock, so a slower
+    clock during the kernels stretches the bound by that ratio."""
     def clk(mix):
         f, e, r = mix
         return f / RATES["fma"] + e / RATES["exp"] + r / RATES["rcp"]
+    bwd_part = tuple(a - b for a, b in zip(MIX["fwdbwd"], MIX["fwd"]))
     if counts is None:
         work = n_syn(c) * clk(MIX[which])
     elif which == "fwd":
-        work = (counts["sens"] + counts["rec_fwd"]) * clk(MIX["fwd"])
+        work = (counts["sens_fwd"] + counts["rec_fwd"]) * clk(MIX["fwd"])
     else:
-        bwd_part = tuple(a - b for a, b in zip(MIX["fwdbwd"], MIX["fwd"]))
-        work = (counts["sens"] * clk(MIX["fwdbwd"]) + counts["rec_fwd"] * clk(MIX["fwd"]) +
-                counts["rec_bwd"] * clk(bwd_part))
-    return work / (RATES["cus"] * RATES["clk_hz"]) * 1e3
+        work = ((counts["sens_fwd"] + counts["rec_fwd"]) * clk(MIX["fwd"]) +
+                (counts["sens_bwd"] + counts["rec_bwd"]) * clk(bwd_part))
+    return work / (RATES["cus"] * RATES["clk_hz"]) * 1e3 * clock_scale
 
 
 def flop_count(c, which, counts):
     """Algorithmic FLOP per step over the evaluated synapses (10 per forward
     evaluation; sensory backward 22, chain 22 with its parameter sums)."""
+    fwd = 10 * (counts["sens_fwd"] + counts["rec_fwd"])
     if which == "fwd":
-        return 10 * (counts["sens"] + counts["rec_fwd"])
-    return 32 * counts["sens"] + 10 * counts["rec_fwd"] + 22 * counts["rec_bwd"]
+        return fwd
+    return fwd + 22 * (counts["sens_bwd"] + counts["rec_bwd"])
+
+
+# --------------------------------------------------------------------------- clock
+
+class ClockSampler:
+    """Engine clock, board power and temperature while a region runs, read
+    from the amdgpu sysfs files by a thread (as bench_ltc.py:221-234 polls
+    nvidia-smi beside its timings). The clock is the current level of
+    pp_dpm_sclk; reading sysfs does not touch the GPU's queues. Samples at or
+    below the lowest DPM level (500 MHz on MI355X: idle or deep sleep) are
+    counted apart, so that a region with idle gaps reports the clock while
+    busy."""
+
+    def __init__(self, period_s=0.004, floor_mhz=500.0):
+        import glob
+        self.period = period_s
+        self.floor = floor_mhz
+        cards = sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk"))
+        self.reason = None
+        if not cards:
+            self.reason = "no readable pp_dpm_sclk"
+        elif len(cards) > 1:
+            self.reason = f"{len(cards)} cards visible; the bench GPU is ambiguous"
+        self.sclk = cards[0] if len(cards) == 1 else None
+        dev = os.path.dirname(self.sclk) if self.sclk else None
+        self.power = (sorted(glob.glob(os.path.join(dev, "hwmon", "hwmon*", "power1_input")))
+                      if dev else [])
+        self.temps = (sorted(glob.glob(os.path.join(dev, "hwmon", "hwmon*", "temp*_input")))
+                      if dev else [])
+        self.mhz, self.watts, self.celsius = [], [], []
+        self._stop = None
+        self._thread = None
+
+    @staticmethod
+    def _read(path):
+        try:
+            with open(path) as f:
+                return f.read()
+        except OSError:
+            return None
+
+    def _sample(self):
+        txt = self._read(self.sclk)
+        if txt:
+            for line in txt.splitlines():
+                if line.rstrip().endswith("*"):
+                    num = "".join(ch for ch in line.split(":", 1)[-1] if ch.isdigit() or ch == ".")
+                    if num:
+                        self.mhz.append(float(num))
+        if self.power:
+            v = self._read(self.power[0])
+            if v and v.strip().isdigit():
+                self.watts.append(int(v) / 1e6)
+        for tp in self.temps:
+            v = self._read(tp)
+            if v and v.strip().lstrip("-").isdigit():
+                self.celsius.append(int(v) / 1e3)
+
+    def _run(self):
+        while not self._stop.is_set():
+            self._sample()
+            self._stop.wait(self.period)
+
+    def __enter__(self):
+        import threading
+        if self.sclk is not None:
+            self._stop = threading.Event()
+            self._thread = threading.Thread(target=self._run, daemon=True)
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+        return False
+
+    def stats(self):
+        if self.sclk is None:
+            return {"source": None, "reason": self.reason}
+        busy = sorted(m for m in self.mhz if m > self.floor)
+        rec = {"source": self.sclk, "samples": len(self.mhz), "busy_samples": len(busy),
+               "mhz_busy_median": statistics.median(busy) if busy else None,
+               "mhz_busy_min": busy[0] if busy else None,
+               "mhz_busy_max": busy[-1] if busy else None,
+               "power_w_median": round(statistics.median(self.watts), 1) if self.watts else None,
+               "temp_c_max": max(self.celsius) if self.celsius else None}
+        return rec
+
+
+def clock_window(fn, seconds):
+    """Runs fn back to back for about `seconds` under a ClockSampler; returns
+    the clock statistics and the mean ms per call over the window."""
+    torch.cuda.synchronize()
+    n = 0
+    with ClockSampler() as cs:
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            fn()
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / n
+    return {"calls": n, "ms_per_call": round(ms, 5), **cs.stats()}
+
+
+def clock_scale(probe, window):
+    """(engine clock while the issue-rate probe ran) / (engine clock in the
+    window), or None when either is unknown."""
+    pm = (probe or {}).get("clock", {}).get("mhz_busy_median")
+    wm = (window or {}).get("mhz_busy_median")
+    return pm / wm if pm and wm else None
 
 
 # --------------------------------------------------------------------------- probe
@@ -297,10 +435,12 @@ def run_probe():
     if not os.path.isfile(PROBE_BIN):
         return {"source": "defaults (probe not built)", **RATES}
     try:
-        proc = subprocess.run([PROBE_BIN], capture_output=True, text=True, timeout=120)
+        with ClockSampler() as cs:
+            proc = subprocess.run([PROBE_BIN], capture_output=True, text=True, timeout=120)
         rec = json.loads(proc.stdout.strip().splitlines()[-1])
     except (OSError, ValueError, IndexError, subprocess.TimeoutExpired) as exc:
         return {"source": f"defaults (probe failed: {exc})", **RATES}
+    rec["clock"] = cs.stats()
     if "error" in rec:
         return {"source": f"defaults (probe: {rec['error']})", **RATES}
     RATES.update(fma=rec["fma_per_cu_clk"], exp=rec["exp_per_cu_clk"],
@@ -375,6 +515,76 @@ def cpu_baseline(name, c):
                       f"TorchScript oracle, fp32, {threads} threads, {_cpu_model()}"}
 
 
+# Rows of each config whose output and input gradient the oracle checks
+# (every row where the oracle finishes in seconds).
+AGREE_ROWS = {"C1": None, "C2": None, "C3": (0, 255), "C4": (0, 127), "C5": (0, 1, 4095)}
+
+
+def oracle_agreement(name, c):
+    """The GPU path against the float64 oracle on the bench's own inputs, outside
+    every timed region, as bench_ltc.py:137-218 checks its CUDA path against
+    TorchScript before reporting. Rows are independent, so the output and
+    dL/dx of sampled rows are checked in a full-batch run; with every row
+    sampled, so are all parameter gradients. Loss sum(out); the bars are the
+    reference's (forward max-abs 1e-3; gradients allclose rtol 5e-2 /
+    atol 1e-2), plus max error <= 2e-3 of each gradient's largest entry."""
+    from oracle import ltc_oracle as O
+
+    m, x, _ = make_inputs(c, "cuda:0")
+    train = c["loss"] is not None
+    rows = AGREE_ROWS[name]
+    idx = list(range(c["B"])) if rows is None else list(rows)
+    # (C5 reads its strided view in place, as the timed forward does)
+    xg = x.detach().requires_grad_(True) if train else x
+    if train:
+        out, _ = m(xg)
+        out.sum().backward()
+    else:
+        with torch.no_grad():
+            out, _ = m(xg)
+    torch.cuda.synchronize()
+    leaves = {k: v.detach().cpu().double().clone() for k, v in m.state_dict().items()}
+    pnames = [n for n, _ in m.named_parameters()]
+    for k in pnames:
+        leaves[k].requires_grad_(train)
+    xr = x.detach()[idx].cpu().double().requires_grad_(train)
+    if train:
+        r_out, _ = O.module_forward(leaves, xr, None, dt=m.dt, ode_unfolds=m.ode_unfolds,
+                                    epsilon=m.epsilon)
+        r_out.sum().backward()
+    else:
+        with torch.no_grad():
+            r_out, _ = O.module_forward(leaves, xr, None, dt=m.dt, ode_unfolds=m.ode_unfolds,
+                                        epsilon=m.epsilon)
+    got = out.detach()[idx].cpu().double()
+    rec = {"rows": "all" if rows is None else idx,
+           "out_max_abs": (got - r_out.detach()).abs().max().item()}
+    ok = rec["out_max_abs"] <= 1e-3
+
+    def grad_err(a, r):
+        err = (a - r).abs().max().item()
+        passed = (torch.allclose(a, r, rtol=5e-2, atol=1e-2) and
+                  err <= 2e-3 * r.abs().max().item() + 1e-6)
+        return err / max(r.abs().max().item(), 1e-30), passed
+
+    if train:
+        rel, passed = grad_err(xg.grad[idx].cpu().double(), xr.grad)
+        rec["dx_max_rel"] = rel
+        ok = ok and passed
+        if rows is None:
+            worst = 0.0
+            for n, prm in m.named_parameters():
+                rel, passed = grad_err(prm.grad.cpu().double(), leaves[n].grad)
+                worst = max(worst, rel)
+                ok = ok and passed
+            rec["param_grads_max_rel"] = worst
+    rec["pass"] = bool(ok)
+    rec["loss"] = "sum(out)" if train else "none (forward only)"
+    del m, x, xg, out
+    torch.cuda.empty_cache()
+    return rec
+
+
 # --------------------------------------------------------------------------- memory, launches
 
 def peak_memory_mb(m, x, target, train):
@@ -414,7 +624,7 @@ def kernel_launches(fn):
 
 # --------------------------------------------------------------------------- configs
 
-def measure_config(name, c, capi, cpu):
+def measure_config(name, c, capi, cpu, probe=None):
     import ltc_cuda
 
     m, x, target = make_inputs(c, "cuda:0")
@@ -467,6 +677,14 @@ def measure_config(name, c, capi, cpu):
     # synapse evaluated, as the reference does): what skipping buys
     rec["valu_mix_bound_dense_ms"] = round(mix_bound_ms(c, which), 4)
     rec["mix_frac_kernels_dense"] = round(mix_bound_ms(c, which) / ksum, 4)
+    # the engine clock while the config's steps run back to back, and the
+    # bound priced at that clock
+    win = clock_window(fn, 1.0 if name in ("C3", "C4") else 0.5)
+    rec["clock_window"] = win
+    scale = clock_scale(probe, win)
+    if scale is not None:
+        rec["valu_mix_bound_at_clock_ms"] = round(mix_bound_ms(c, which, counts, scale), 4)
+        rec["mix_frac_kernels_at_clock"] = round(mix_bound_ms(c, which, counts, scale) / ksum, 4)
     rec["memory"] = peak_memory_mb(m, x, target, train)
     del m, x, target
     torch.cuda.empty_cache()
@@ -474,6 +692,7 @@ def measure_config(name, c, capi, cpu):
         rec["cpu_baseline"] = cpu_baseline(name, c)
         gpu_ms = rec["fwd_bwd_ms"] if train else rec["fwd_nograd_ms"]
         rec["gpu_vs_cpu"] = round(rec["cpu_baseline"]["ms_per_step"] / gpu_ms, 1)
+        rec["oracle_agreement"] = oracle_agreement(name, c)
     _ = ltc_cuda
     return rec
 
@@ -484,7 +703,8 @@ def sparsity_record(plan, dens, counts):
             "skips_masked_recurrent": {"forward": bool(plan.get("cmp_fwd")),
                                        "chain": bool(plan.get("cmp_bwd"))},
             "n_syn_active": int(round(counts["active"])),
-            "n_syn_evaluated": int(round(counts["sens"] + counts["rec_fwd"]))}
+            "n_syn_evaluated_fwd": int(round(counts["sens_fwd"] + counts["rec_fwd"])),
+            "n_syn_evaluated_bwd": int(round(counts["sens_bwd"] + counts["rec_bwd"]))}
 
 
 def load_traffic(workload):
@@ -608,6 +828,8 @@ def main():
     with torch.no_grad():
         launches_fwd = kernel_launches(lambda: m(x))
     launches_step = kernel_launches(lambda: step(m, x, target))
+    win = clock_window(lambda: step(m, x, target), 0.5)
+    scale = clock_scale(probe, win)
     graph_ms, graph_equal = (None, None)
     if not args.no_graph:
         graph_ms, graph_equal = graphed_c1(m, x, target, args.steps, args.warmup)
@@ -648,6 +870,9 @@ def main():
         "issue_rate": probe,
         "valu_mix_bound_ms": round(mix_bound_ms(c, "fwdbwd", counts), 5),
         "mix_frac_step": round(mix_bound_ms(c, "fwdbwd", counts) / ms, 5),
+        "clock_window": win,
+        "mix_frac_step_at_clock": (None if scale is None else
+                                   round(mix_bound_ms(c, "fwdbwd", counts, scale) / ms, 5)),
         "roofline": roofline(c, kt, plan, load_traffic("C1"), counts),
         "vs_reference_gtx1080_published": round(REF_GTX1080_MS / ms, 3),
     }
@@ -657,9 +882,11 @@ def main():
     if not args.no_large:
         line["large_configs"] = {}
         for name, cfg in LARGE.items():
-            line["large_configs"][name] = measure_config(name, cfg, capi, cpu)
+            line["large_configs"][name] = measure_config(name, cfg, capi, cpu, probe)
             print(f"bench: {name} done", file=sys.stderr, flush=True)
     line["cpu_baseline"] = cpu_baseline("C1", c) if cpu else None
+    if cpu:
+        line["oracle_agreement"] = oracle_agreement("C1", c)
     if rank == 0:
         print(json.dumps(line), flush=True)
 

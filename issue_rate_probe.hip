@@ -50,7 +50,9 @@ __global__ __launch_bounds__(kThreads) void chains(float* out, float seed) {
 template <int OP>
 double rate(float* out, int blocks, int cus, double clk_hz, float seed, hipEvent_t a, hipEvent_t b) {
   double best = 0.0;
-  for (int rep = 0; rep < 4; ++rep) {
+  // enough repetitions (about 0.3 s over the four kernels) for bench.py's
+  // sysfs clock sampler to see the engine clock while they run
+  for (int rep = 0; rep < 12; ++rep) {
     if (hipEventRecord(a, nullptr) != hipSuccess) return -1.0;
     hipLaunchKernelGGL(chains<OP>, dim3(blocks), dim3(kThreads), 0, nullptr, out, seed);
     if (hipGetLastError() != hipSuccess) return -1.0;

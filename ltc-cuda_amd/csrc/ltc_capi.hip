@@ -458,9 +458,10 @@ const char* const kNames[ltc::K_COUNT] = {"ltc_prep",     "ltc_sens_fwd", "ltc_o
 struct Timing {
   std::mutex mu;
   bool on = false;
+  // One timed call: the event pairs of the kernels it launched.
   struct Rec {
     int id;
-    hipEvent_t a, b;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
   };
   std::vector<Rec> pending;
   std::vector<hipEvent_t> pool;
@@ -477,15 +478,25 @@ struct Timing {
     if (hipEventCreate(&e) != hipSuccess) return nullptr;
     return e;
   }
+  // A call's time is the sum of its kernels' durations; calls count once.
   void drain() {
     for (auto& r : pending) {
-      float ms = 0.f;
-      if (hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
-        total_ms[r.id] += ms;
+      double sum = 0.0;
+      bool ok = !r.ev.empty();
+      for (auto& pr : r.ev) {
+        float ms = 0.f;
+        if (hipEventSynchronize(pr.second) == hipSuccess &&
+            hipEventElapsedTime(&ms, pr.first, pr.second) == hipSuccess)
+          sum += ms;
+        else
+          ok = false;
+        pool.push_back(pr.first);
+        pool.push_back(pr.second);
+      }
+      if (ok) {
+        total_ms[r.id] += sum;
         count[r.id] += 1;
       }
-      pool.push_back(r.a);
-      pool.push_back(r.b);
     }
     pending.clear();
   }
@@ -496,23 +507,40 @@ Timing& timing() {
   return *t;
 }
 
-// Runs one launch, bracketed by events when timing is enabled.
+// Hands each kernel of one timed call an event pair from the pool.
+struct CallEvents : ltc::LaunchEvents {
+  Timing& tm;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev;
+  explicit CallEvents(Timing& t) : tm(t) {}
+  bool take(hipEvent_t* a, hipEvent_t* b) override {
+    std::lock_guard<std::mutex> g(tm.mu);
+    *a = tm.get();
+    *b = tm.get();
+    if (*a == nullptr || *b == nullptr) {
+      if (*a) tm.pool.push_back(*a);
+      if (*b) tm.pool.push_back(*b);
+      return false;
+    }
+    ev.emplace_back(*a, *b);
+    return true;
+  }
+};
+
+// Runs one library call's launches; when timing is enabled, each of its
+// kernels is timed by its own execution (hipExtLaunchKernel events).
 template <class F>
 hipError_t timed(int id, hipStream_t s, F&& launch) {
+  (void)s;
   Timing& tm = timing();
   if (!tm.on) return launch();
-  hipEvent_t a = nullptr, b = nullptr;
-  {
-    std::lock_guard<std::mutex> g(tm.mu);
-    a = tm.get();
-    b = tm.get();
-  }
-  if (a) (void)hipEventRecord(a, s);
+  CallEvents ce(tm);
+  ltc::LaunchEvents* prev = ltc::g_launch_events;
+  ltc::g_launch_events = &ce;
   const hipError_t err = launch();
-  if (b) (void)hipEventRecord(b, s);
-  if (a && b) {
+  ltc::g_launch_events = prev;
+  if (!ce.ev.empty()) {
     std::lock_guard<std::mutex> g(tm.mu);
-    tm.pending.push_back({id, a, b});
+    tm.pending.push_back({id, std::move(ce.ev)});
   }
   return err;
 }

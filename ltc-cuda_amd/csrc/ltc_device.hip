@@ -31,6 +31,9 @@
 #include "ltc_internal.h"
 
 namespace ltc {
+
+thread_local LaunchEvents* g_launch_events = nullptr;
+
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -546,7 +549,7 @@ __global__ __launch_bounds__(256) void sens_fwd_cmp_kernel(const float* __restri
                                                            const int* __restrict__ sFi,
                                                            const int* __restrict__ sFn,
                                                            float* __restrict__ sn,
-                                                           float* __restrict__ sd, LnAff la = {}) {
+                                                           float* __restrict__ sd, LnAff la) {
   static_assert(!LN || DS == 1, "the row normalisation runs in the row-group layout");
   constexpr int ROWS = (DS == 1 ? 4 : 1) * RPW;
   constexpr int XLD = ROWS + 4;  // padded staged row, 16-byte aligned
@@ -4216,21 +4219,21 @@ hipError_t fwd_by_rcp(const Plan& p, const FwdK& a, hipStream_t s) {
   const int rcp = (p.RC == 4 || p.RC == 8 || p.RC == 16) ? p.RC : 0;
   if constexpr (NB == 1) {
     if (row_wave128_fwd(p)) {
-      hipLaunchKernelGGL((ode_fwd_row_wave_kernel<128>), grid, dim3(512), lds, s, a);
+      LTC_LAUNCH((ode_fwd_row_wave_kernel<128>), grid, dim3(512), lds, s, a);
       return hipGetLastError();
     }
     if (row_kernels(p)) {
       // the launch plan gives every single-row forward at Hp = 64 RC = 16
       if (rcp != 16) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((ode_fwd_row_wave_kernel<64>), grid, dim3(256), lds, s, a);
+      LTC_LAUNCH((ode_fwd_row_wave_kernel<64>), grid, dim3(256), lds, s, a);
       return hipGetLastError();
     }
   }
   switch (rcp) {
-    case 4: hipLaunchKernelGGL((ode_fwd_kernel<NB, 4>), grid, block, lds, s, a); break;
-    case 8: hipLaunchKernelGGL((ode_fwd_kernel<NB, 8>), grid, block, lds, s, a); break;
-    case 16: hipLaunchKernelGGL((ode_fwd_kernel<NB, 16>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((ode_fwd_kernel<NB, 0>), grid, block, lds, s, a); break;
+    case 4: LTC_LAUNCH((ode_fwd_kernel<NB, 4>), grid, block, lds, s, a); break;
+    case 8: LTC_LAUNCH((ode_fwd_kernel<NB, 8>), grid, block, lds, s, a); break;
+    case 16: LTC_LAUNCH((ode_fwd_kernel<NB, 16>), grid, block, lds, s, a); break;
+    default: LTC_LAUNCH((ode_fwd_kernel<NB, 0>), grid, block, lds, s, a); break;
   }
   return hipGetLastError();
 }
@@ -4240,23 +4243,23 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
   const dim3 grid((p.B + NB - 1) / NB), block(p.Hp * p.KSB);
   const size_t lds = bwd_lds_bytes(p);
   const int rcp = (p.RCB == 4 || p.RCB == 8 || p.RCB == 16) ? p.RCB : 0;
-#define LTC_BWD(R, F) hipLaunchKernelGGL((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
+#define LTC_BWD(R, F) LTC_LAUNCH((ode_bwd_kernel<NB, R, F>), grid, block, lds, s, a)
   if constexpr (NB == 1) {
     if (row_kernels(p)) {
       // the launch plan gives every single-row chain at Hp = 64 FUSE, RCB = 8
       if (!p.FUSE || rcp != 8) return hipErrorInvalidValue;
       if (p.H == 64)
-        hipLaunchKernelGGL((ode_bwd_row_wave_kernel<true>), grid, block, lds, s, a);
+        LTC_LAUNCH((ode_bwd_row_wave_kernel<true>), grid, block, lds, s, a);
       else
-        hipLaunchKernelGGL((ode_bwd_row_wave_kernel<false>), grid, block, lds, s, a);
+        LTC_LAUNCH((ode_bwd_row_wave_kernel<false>), grid, block, lds, s, a);
       return hipGetLastError();
     }
     if (row_wave128_bwd(p)) {
       const RecC none{};
       if (p.H == 128)
-        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a, none);
+        LTC_LAUNCH((ode_bwd_row_wave128_kernel<true>), grid, dim3(512), lds, s, a, none);
       else
-        hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<false>), grid, dim3(512), lds, s, a, none);
+        LTC_LAUNCH((ode_bwd_row_wave128_kernel<false>), grid, dim3(512), lds, s, a, none);
       return hipGetLastError();
     }
   }
@@ -4287,7 +4290,7 @@ size_t bwd_cl_lds_bytes(const Plan& p) { return (size_t)cluster_bwd_lds(p); }
 
 hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s) {
   const long long n = bwd ? cluster_words_bwd(p) : cluster_words(p);
-  hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+  LTC_LAUNCH(clear_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
                      cb.xch, n, cb.status);
   return hipGetLastError();
 }
@@ -4297,9 +4300,9 @@ hipError_t fwd_cl_by_rcp(const Plan& p, const FwdCK& a, hipStream_t s) {
   const dim3 grid(p.NCL * p.CP), block(64 * p.KS);
   const size_t lds = fwd_cl_lds_bytes(p);
   if (p.RC == 16)
-    hipLaunchKernelGGL((ode_fwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
+    LTC_LAUNCH((ode_fwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
   else
-    hipLaunchKernelGGL((ode_fwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
+    LTC_LAUNCH((ode_fwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
   return hipGetLastError();
 }
 
@@ -4312,15 +4315,15 @@ hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
     // (Hp = 256) or 32 streamed ones (Hp = 512).
     if (p.JWB != 32 || p.KSB != 16) return hipErrorInvalidConfiguration;
     if (p.RCB == 16)
-      hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
+      LTC_LAUNCH((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
     else if (p.RCB == 32)
-      hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 32, 0, true, 32>), grid, block, lds, s, a);
+      LTC_LAUNCH((ode_bwd_cl_kernel<NB, 32, 0, true, 32>), grid, block, lds, s, a);
     else
       return hipErrorInvalidConfiguration;
   } else {
     // Streamed operands (a register-resident form spilled at 1024 threads
     // and measured slower).
-    hipLaunchKernelGGL((ode_bwd_cl_kernel<NB, 64, 0, false>), grid, block, lds, s, a);
+    LTC_LAUNCH((ode_bwd_cl_kernel<NB, 64, 0, false>), grid, block, lds, s, a);
   }
   return hipGetLastError();
 }
@@ -4336,7 +4339,7 @@ hipError_t launch_prep(const Plan& p, const RawParams& rp, const Prepped& pp, bo
   const int nflat = (int)((total + 255) / 256);
   const bool rec = (segs & kPrepRec) != 0;
   const int ncmp = (cmp_columns(pp, p.Hp, p.Dp, rec, rec && bwd, (segs & kPrepSens) != 0) + 3) / 4;
-  hipLaunchKernelGGL(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
+  LTC_LAUNCH(prep_kernel, dim3((unsigned)(nflat + ncmp)), dim3(256), 0, s, rp, pp, p.H,
                      p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, segs, nflat, cmp_chunks_fwd(p),
                      cmp_chunks_bwd(p));
   return hipGetLastError();
@@ -4351,7 +4354,7 @@ hipError_t launch_fill(const FillList& fl, hipStream_t s) {
   const long long cap = fl.gate != nullptr ? 256 : 2048;
   long long blocks = (total + 255) / 256;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL(fill_list_kernel, dim3((unsigned)blocks), dim3(256), 0, s, fl);
+  LTC_LAUNCH(fill_list_kernel, dim3((unsigned)blocks), dim3(256), 0, s, fl);
   return hipGetLastError();
 }
 
@@ -4374,7 +4377,7 @@ hipError_t launch_copy_rows(const float* src, long long src_ld, float* dst, long
                             long long rows, int cols, hipStream_t s) {
   const long long n = rows * dst_ld;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
+  LTC_LAUNCH(copy_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src,
                      src_ld, dst, dst_ld, rows, cols);
   return hipGetLastError();
 }
@@ -4391,10 +4394,10 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
 #define LTC_SENS(R, DSV)                                                                        \
   do {                                                                                          \
     if (pp.sF != nullptr)                                                                       \
-      hipLaunchKernelGGL((sens_fwd_cmp_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
-                         p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd);                                  \
+      LTC_LAUNCH((sens_fwd_cmp_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
+                         p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd, LnAff{});                         \
     else                                                                                        \
-      hipLaunchKernelGGL((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT,     \
+      LTC_LAUNCH((sens_fwd_kernel<R, DSV>), grid, block, 0, s, x, xs, p.T, p.D, BT,     \
                          p.Hp, pp.sensF, sn, sd);                                               \
   } while (0)
   if (pp.sF != nullptr && (pp.sFi == nullptr || pp.sFn == nullptr)) return hipErrorInvalidValue;
@@ -4425,7 +4428,7 @@ hipError_t launch_sens_fwd_ln(const Plan& p, const float* x, Strides3 xs, const 
   const SensGeom geo = sens_fwd_geom(p);
   const dim3 grid(p.Hp / 64, (BT + 4 * geo.rpw - 1) / (4 * geo.rpw)), block(256);
 #define LTC_SENSLN(R)                                                                      \
-  hipLaunchKernelGGL((sens_fwd_cmp_kernel<R, 1, true>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
+  LTC_LAUNCH((sens_fwd_cmp_kernel<R, 1, true>), grid, block, 0, s, x, xs, p.T, p.D, BT, \
                      p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd, la)
   switch (geo.rpw) {
     case 8: LTC_SENSLN(8); break;
@@ -4542,7 +4545,7 @@ hipError_t launch_ode_bwd_row128_rec(const Plan& p, const Prepped& pp, const flo
   // the chain's LDS (its staged rows), or a sensory companion's when larger
   const size_t lds = sens ? (size_t)chain_launch_lds(p) : bwd_lds_bytes(p);
 #define LTC_W128(F, C) \
-  hipLaunchKernelGGL((ode_bwd_row_wave128_kernel<F, C>), grid, block, lds, s, a, rc)
+  LTC_LAUNCH((ode_bwd_row_wave128_kernel<F, C>), grid, block, lds, s, a, rc)
   if (p.H == 128) {
     if (p.Dp > 64) LTC_W128(true, 2); else LTC_W128(true, 1);
   } else {
@@ -4567,7 +4570,7 @@ hipError_t launch_ode_bwd_row_fused(const Plan& p, const Prepped& pp, const floa
   // the chain's LDS (its gradient tile), or the companion's when larger
   const size_t lds = (size_t)chain_launch_lds(p);
 #define LTC_RBF(F, C) \
-  hipLaunchKernelGGL((ode_bwd_row_fused_kernel<F, C>), grid, block, lds, s, a, rc, pp.sensB, p.D, p.Dp, Bc)
+  LTC_LAUNCH((ode_bwd_row_fused_kernel<F, C>), grid, block, lds, s, a, rc, pp.sensB, p.D, p.Dp, Bc)
   if (p.H == 64) {
     if (DC == 1) LTC_RBF(true, 1); else LTC_RBF(true, 2);
   } else {
@@ -4581,7 +4584,7 @@ hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
                            const float2* absave, float* rpart, hipStream_t s) {
   const long long nper = (p.N + p.NCH - 1) / p.NCH;
   RecGK a{pp.recF, vsave, absave, rpart, p.Hp, p.N, nper};
-  hipLaunchKernelGGL(rec_grad_kernel, dim3(p.Hp / 64, p.Hp / 32, p.NCH), dim3(256), 0, s, a);
+  LTC_LAUNCH(rec_grad_kernel, dim3(p.Hp / 64, p.Hp / 32, p.NCH), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -4591,7 +4594,7 @@ hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Pre
   const int BT = p.B * p.T;
   const int rows_per = (BT + p.NRC - 1) / p.NRC;
   SensBK a{x, xs, pp.sensB, dsn, dsd, spart, dxpart, p.T, p.D, p.Dp, p.Hp, BT, rows_per};
-  hipLaunchKernelGGL(sens_bwd_kernel, dim3(p.Dp / 64, p.Hp / 32, p.NRC), dim3(256), 0, s, a);
+  LTC_LAUNCH(sens_bwd_kernel, dim3(p.Dp / 64, p.Hp / 32, p.NRC), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -4610,7 +4613,7 @@ hipError_t presum(const Plan& p, const float* rpart, const float* npart, const P
   auto pass = [&](const float* src, int M, long long N, float* dst) {
     const int parts = presum_parts(M);
     const int rpb = (M + parts - 1) / parts;
-    hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
+    LTC_LAUNCH(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
                        dim3(256), 0, s, src, N, M, N, rpb, dst);
     return parts;
   };
@@ -4642,7 +4645,7 @@ hipError_t launch_finalize(const Plan& p, const RawParams& rp, const float* rpar
   FinK a{rp, pt.rpart, spart, dxpart, pt.npart, g, pt.nneuron, p.D, p.H, p.Hp, p.Dp, pt.nrec,
          p.NRC, p.Hp / 32, BT, base, count};
   const unsigned blocks = (unsigned)((count + 255) / 256);
-  hipLaunchKernelGGL(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
+  LTC_LAUNCH(finalize_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -4666,7 +4669,7 @@ hipError_t launch_prep_leaf(const Plan& p, const LeafParams& lp, const Prepped& 
   // reading the compacted image, nothing reads sensF.
   const int sensf = (images & kLeafFwdImages) && !fs && pp.sF == nullptr ? 1 : 0;
 #define LTC_PREPL(C, F)                                                                           \
-  hipLaunchKernelGGL((prep_leaf_kernel<C, F>), dim3(nprep + ncmp + nln), dim3(threads), 0, s, lp, pp, \
+  LTC_LAUNCH((prep_leaf_kernel<C, F>), dim3(nprep + ncmp + nln), dim3(threads), 0, s, lp, pp, \
                      p.H, p.D, p.Hp, p.Dp, bwd ? (p.FUSE ? 1 : 2) : 0, sensf, bwd ? 1 : 0, nprep, \
                      ncmp, cmp_chunks_fwd(p), cmp_chunks_bwd(p), lb, p.T, BT, clear_words,       \
                      nclear, sn, sd)
@@ -4704,7 +4707,7 @@ hipError_t launch_ln_bwd(const Plan& p, const LeafParams& lp, const LnBuf& ln,
   const dim3 grid(ln_bwd_blocks(p)), block(256);
   // the dL/dxa partials per row: those of the 32-neuron blocks
   const int rpb = ln_rows_per_block(p), BT = p.B * p.T, HB = p.Hp / 32;
-#define LTC_LNB(C) hipLaunchKernelGGL((ln_bwd_kernel<C>), grid, block, 0, s, lp, ln, dxpart, gx, lnpart, p.T, p.D, p.Dp, BT, HB, rpb)
+#define LTC_LNB(C) LTC_LAUNCH((ln_bwd_kernel<C>), grid, block, 0, s, lp, ln, dxpart, gx, lnpart, p.T, p.D, p.Dp, BT, HB, rpb)
   if (p.D <= 64) LTC_LNB(1);
   else if (p.D <= 128) LTC_LNB(2);
   else if (p.D <= 256) LTC_LNB(4);
@@ -4726,7 +4729,7 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
   if (presum_parts(nln) > 0) {
     const int parts = presum_parts(nln), rpb = (nln + parts - 1) / parts;
     const long long N = 4LL * p.Dp;
-    hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
+    LTC_LAUNCH(sum_rows_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)parts),
                        dim3(256), 0, s, lnpart, N, nln, N, rpb, ps.ln);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -4742,7 +4745,7 @@ hipError_t launch_finalize_leaf(const Plan& p, const LeafParams& lp, const float
   const long long nel = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
   const long long total = 4 * nel > nel + nx + ns ? 4 * nel : nel + nx + ns;
   const unsigned blocks = (unsigned)((total + 255) / 256);
-  hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
+  LTC_LAUNCH(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -4764,7 +4767,7 @@ hipError_t launch_finalize_leaf_fused(const Plan& p, const LeafParams& lp, const
   const long long nel = (long long)p.H * p.H + (long long)p.D * p.H + p.H + p.D;
   const long long total = 4 * nel > nel + nx + ns ? 4 * nel : nel + nx + ns;
   const unsigned blocks = (unsigned)((total + 255) / 256);
-  hipLaunchKernelGGL(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
+  LTC_LAUNCH(finalize_leaf_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

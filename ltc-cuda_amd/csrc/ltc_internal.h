@@ -3,11 +3,32 @@
 // include/ltc_capi.h.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace ltc {
+
+// Kernel timing (ltc_timing_enable). While a timed call runs on a thread, the
+// hook hands every kernel that call launches a pair of events, and the kernel
+// is launched with hipExtLaunchKernel, which records the pair around the
+// kernel's own execution: the interval is the kernel's duration, with no
+// marker command between the two events and the kernel.
+struct LaunchEvents {
+  virtual bool take(hipEvent_t* start, hipEvent_t* stop) = 0;
+};
+extern thread_local LaunchEvents* g_launch_events;
+
+#define LTC_LAUNCH(K, GRID, BLOCK, LDS, S, ...)                                          \
+  do {                                                                                   \
+    hipEvent_t ltc_ev_a_ = nullptr, ltc_ev_b_ = nullptr;                                 \
+    if (::ltc::g_launch_events != nullptr &&                                             \
+        ::ltc::g_launch_events->take(&ltc_ev_a_, &ltc_ev_b_))                            \
+      hipExtLaunchKernelGGL(K, GRID, BLOCK, LDS, S, ltc_ev_a_, ltc_ev_b_, 0, __VA_ARGS__); \
+    else                                                                                 \
+      hipLaunchKernelGGL(K, GRID, BLOCK, LDS, S, __VA_ARGS__);                           \
+  } while (0)
 
 // Threads per workgroup of the persistent ODE kernels for NB batch rows per
 // workgroup. More rows per thread means more live registers, so fewer
