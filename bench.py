@@ -404,11 +404,14 @@ def clock_window(fn, seconds):
 
 
 def clock_scale(probe, window):
-    """(engine clock while the issue-rate probe ran) / (engine clock in the
-    window), or None when either is unknown."""
-    pm = (probe or {}).get("clock", {}).get("mhz_busy_median")
+    """(the clock the bound is priced at, RATES clk_hz) / (engine clock in the
+    window), or None when the window's clock is unknown. The probe's rates
+    are per engine clock (it measures the clock each kernel ran at), so the
+    bound at the window's clock is the bound at clk_hz times this ratio."""
     wm = (window or {}).get("mhz_busy_median")
-    return pm / wm if pm and wm else None
+    if not wm or not probe or "clock_mhz_measured" not in probe:
+        return None
+    return RATES["clk_hz"] / 1e6 / wm
 
 
 # --------------------------------------------------------------------------- probe
@@ -435,12 +438,10 @@ def run_probe():
     if not os.path.isfile(PROBE_BIN):
         return {"source": "defaults (probe not built)", **RATES}
     try:
-        with ClockSampler() as cs:
-            proc = subprocess.run([PROBE_BIN], capture_output=True, text=True, timeout=120)
+        proc = subprocess.run([PROBE_BIN], capture_output=True, text=True, timeout=120)
         rec = json.loads(proc.stdout.strip().splitlines()[-1])
     except (OSError, ValueError, IndexError, subprocess.TimeoutExpired) as exc:
         return {"source": f"defaults (probe failed: {exc})", **RATES}
-    rec["clock"] = cs.stats()
     if "error" in rec:
         return {"source": f"defaults (probe: {rec['error']})", **RATES}
     RATES.update(fma=rec["fma_per_cu_clk"], exp=rec["exp_per_cu_clk"],

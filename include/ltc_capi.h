@@ -40,8 +40,13 @@ extern "C" {
 #define LTC_EUNSUPPORTED 2
 #define LTC_EHIP 3
 
-/* Largest hidden size one persistent workgroup covers (Hp*KS <= 1024). */
-#define LTC_MAX_HIDDEN 1024
+/* Largest hidden size. Up to H = 1024 a single workgroup can hold a batch
+ * row's neurons; above it the ODE kernels always run as clusters of Hp/64
+ * workgroups (at most one per CU, in as many launches as the batch needs),
+ * which needs Hp/64 <= the device's CU count. The reference has no limit;
+ * 4096 keeps every operand image under 1 GiB and every byte offset inside
+ * the 32-bit buffer range. */
+#define LTC_MAX_HIDDEN 4096
 
 /* ABI version of the loaded library (LTC_ABI_VERSION at build time). */
 int ltc_abi_version(void);
@@ -307,11 +312,13 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * call: no separate sensory launch), 1 when the backward runs the sensory
  * and LayerNorm backward inside the chain launch (Hp = 64), and 1 when it
  * forms the recurrent parameter-gradient sums inside the chain launch
- * (Hp = 128: no separate recurrent-gradient launch). Returns the number of
- * values written, or -1 for invalid sizes. The plan depends on the current
- * device's CU count.
+ * (Hp = 128: no separate recurrent-gradient launch), then the launches of
+ * the forward and of the chain ODE kernel per call: 1, or at Hp > 1024 with
+ * more rows than one launch of at most one workgroup per CU holds, one
+ * launch per NCL * NB rows. Returns the number of values written, or -1 for
+ * invalid sizes. The plan depends on the current device's CU count.
  */
-#define LTC_PLAN_FIELDS 25
+#define LTC_PLAN_FIELDS 27
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

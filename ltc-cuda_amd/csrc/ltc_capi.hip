@@ -108,8 +108,59 @@ void plan_fused_chain(ltc::Plan& p, int ncu) {
   }
 }
 
+// Cluster geometry with NB rows per cluster: the largest KS (16 or 8, RC a
+// multiple of 8, KS >= NB) whose forward and chain LDS fit; 0 if none.
+int cluster_ks(const ltc::Plan& p, int nb) {
+  for (int ks = 16; ks >= nb && ks >= 8; ks >>= 1) {
+    if ((p.Hp / ks) % 8 != 0) continue;  // streamed operands come eight rows at a time
+    const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
+    if (lf > kClusterLds || ltc::cluster_chain_lds(nb, p.Hp, ks, 64, false) > chain_lds_limit())
+      continue;
+    if (p.Hp == 256 && ks == 16 && lf + ltc::cmp_index_lds(64 * ks) > chain_lds_limit()) continue;
+    return ks;
+  }
+  return 0;
+}
+
+// Hp > 1024: one thread per column no longer fits one workgroup, so the
+// cluster form runs every batch size. When the rows do not fit one launch of
+// at most one workgroup per CU, the call makes LCH launches, each taking the
+// next NCL * NB rows (rows are independent): the fewest rows per cluster
+// that fit B in one launch, else the most the LDS allows.
+bool plan_cluster_wide(ltc::Plan& p, int ncu) {
+  if (p.Hp <= 1024 || p.B < 1) return false;
+  const int cp = p.Hp / 64;
+  const int slots = ncu / cp;
+  if (slots < 1) return false;
+  int best_nb = 0, best_ks = 0;
+  for (int nb : {1, 2, 4, 8}) {
+    const int ks = cluster_ks(p, nb);
+    if (ks == 0) continue;
+    best_nb = nb;
+    best_ks = ks;
+    if ((p.B + nb - 1) / nb <= slots) break;
+  }
+  if (best_nb == 0) return false;
+  const int nb = best_nb, ks = best_ks;
+  const int need = (p.B + nb - 1) / nb;
+  const int ncl = need < slots ? need : slots;
+  p.CP = cp;
+  p.NCL = ncl;
+  p.NB = nb;
+  p.KS = p.KSB = ks;
+  p.RC = p.RCB = p.Hp / ks;
+  p.FUSE = false;
+  p.CPB = cp;
+  p.JWB = 64;
+  p.NBB = nb;
+  p.NCLB = ncl;
+  p.LCH = p.LCHB = (p.B + ncl * nb - 1) / (ncl * nb);
+  return true;
+}
+
 bool plan_cluster(ltc::Plan& p, int ncu) {
   if (p.Hp < 256 || p.B < 1) return false;
+  if (p.Hp > 1024) return plan_cluster_wide(p, ncu);
   const int cp = p.Hp / 64;
   const int slots = ncu / cp;
   for (int nb : {1, 2, 4, 8}) {
@@ -223,6 +274,7 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
   p.CP = p.NCL = 0;
   p.CPB = p.NBB = p.NCLB = 0;
   p.JWB = 64;
+  p.LCH = p.LCHB = 1;
   plan_cluster(p, ncu);
   // Recurrent parameter-gradient chunks: about 1024 workgroups, at least 32
   // unfold instances each, at most 64 partials per synapse.
@@ -443,6 +495,12 @@ int check_dims(int B, int T, int D, int H, int U) {
   if (H > LTC_MAX_HIDDEN)
     return fail(LTC_EUNSUPPORTED, "hidden size H = " + std::to_string(H) + " exceeds " +
                                       std::to_string(LTC_MAX_HIDDEN));
+  // above 1024 only the cluster form covers a row: Hp/64 workgroups at once
+  if (H > 1024 && (H + 63) / 64 > device_cus())
+    return fail(LTC_EUNSUPPORTED, "hidden size H = " + std::to_string(H) +
+                                      " needs " + std::to_string((H + 63) / 64) +
+                                      " co-resident workgroups; the device has " +
+                                      std::to_string(device_cus()) + " CUs");
   if ((long long)B * T * (D > H ? D : H) > (1LL << 40))
     return fail(LTC_EUNSUPPORTED, "problem too large");
   return LTC_OK;
@@ -1484,7 +1542,7 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,
       ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0, ltc::prep_sens_fused(p) ? 1 : 0,
-      ltc::row_bwd_fused(p) ? 1 : 0, ltc::row128_rec_fused(p) ? 1 : 0};
+      ltc::row_bwd_fused(p) ? 1 : 0, ltc::row128_rec_fused(p) ? 1 : 0, p.LCH, p.LCHB};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

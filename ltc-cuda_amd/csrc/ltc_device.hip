@@ -3532,6 +3532,7 @@ struct FwdCK {
   const float4* cimg;
   const int* cidx;
   const int* ccnt;
+  int R0;  // first batch row of this launch (launches take NCL * NB rows each)
 };
 
 
@@ -3558,7 +3559,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   int p, cl;
   cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
   const int c = p * kClW + o;  // output column of this thread
-  const int b0 = cl * NB;
+  const int b0 = k.R0 + cl * NB;
   const int r0 = ks * RC;
   const bool owner = ks < NB;  // finishes row ks of column c (the plan keeps KS >= NB)
   const __amdgpu_buffer_rsrc_t rsF = image_rsrc(k.recF, (long long)Hp * Hp * 16);
@@ -3779,6 +3780,7 @@ struct BwdCK {
   const float4* cimg;
   const int* cidx;
   const int* ccnt;
+  int R0;  // first batch row of this launch (launches take NCL * NB rows each)
 };
 
 // One compacted chain synapse for every row of the tile: alpha/beta of its
@@ -3864,7 +3866,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   int p, cl;
   cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
   const int c = p * JW + o;
-  const int b0 = cl * NB;
+  const int b0 = k.R0 + cl * NB;
   const int r0 = ks * RC;
   const bool owner = ks < NB;
   const int bo = ks;
@@ -4150,7 +4152,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
     // (i = c, j = r0 + rr), layout [cluster][4][i][j] as rec_grad_kernel's.
     const long long HH = (long long)Hp * Hp;
     if constexpr (CMP) {
-      float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp;
+      float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)c * Hp;
 #pragma unroll
       for (int rr = 0; rr < NACC; ++rr) {
         if (rr < nmine) {
@@ -4162,7 +4164,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
         }
       }
     } else {
-      float* out = k.rpart + (long long)cl * 4 * HH + (long long)c * Hp + r0;
+      float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)c * Hp + r0;
 #pragma unroll
       for (int rr = 0; rr < NACC; ++rr) {
         out[rr] = gacc[rr].x;
@@ -4288,10 +4290,14 @@ hipError_t bwd_by_rcp(const Plan& p, const BwdK& a, hipStream_t s) {
 size_t fwd_cl_lds_bytes(const Plan& p) { return (size_t)cluster_fwd_lds(p); }
 size_t bwd_cl_lds_bytes(const Plan& p) { return (size_t)cluster_bwd_lds(p); }
 
-hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s) {
+// Clears the exchange words before a cluster launch; the status word only
+// before the first launch of a call, so a give-up in an earlier launch of the
+// call stays reported.
+hipError_t clear_cluster(const Plan& p, const ClusterBuf& cb, bool bwd, hipStream_t s,
+                         bool status = true) {
   const long long n = bwd ? cluster_words_bwd(p) : cluster_words(p);
   LTC_LAUNCH(clear_words_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                     cb.xch, n, cb.status);
+             cb.xch, n, status ? cb.status : nullptr);
   return hipGetLastError();
 }
 
@@ -4444,21 +4450,28 @@ hipError_t launch_ode_fwd(const Plan& p, const Prepped& pp, const float* sn, con
                           const float* state0, float eps, float* out, float* hfin,
                           float* vsave, float* densave, const ClusterBuf& cb, hipStream_t s) {
   if (p.CP > 0) {
-    hipError_t e = clear_cluster(p, cb, false, s);
-    if (e != hipSuccess) return e;
     // Register-resident operands (RC = 16) read no image from L2 in the loop.
     const int xl = (p.RC == 16 && p.NCL % 8 == 0) ? 1 : 0;
     FwdCK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave, cb.xch, cb.status,
             cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, p.CP, xl, eps,
-            pp.cF, pp.cFi, pp.cFn};
+            pp.cF, pp.cFi, pp.cFn, 0};
     if (cmp_fwd(p) && (pp.cF == nullptr || pp.cFi == nullptr || pp.cFn == nullptr))
       return hipErrorInvalidValue;
-    switch (p.NB) {
-      case 8: return fwd_cl_by_rcp<8>(p, a, s);
-      case 4: return fwd_cl_by_rcp<4>(p, a, s);
-      case 2: return fwd_cl_by_rcp<2>(p, a, s);
-      default: return fwd_cl_by_rcp<1>(p, a, s);
+    // One launch per NCL * NB rows (more than one only at Hp > 1024); the
+    // exchange words are cleared before each, in stream order.
+    for (int l = 0; l < p.LCH; ++l) {
+      hipError_t e = clear_cluster(p, cb, false, s, l == 0);
+      if (e != hipSuccess) return e;
+      a.R0 = l * p.NCL * p.NB;
+      switch (p.NB) {
+        case 8: e = fwd_cl_by_rcp<8>(p, a, s); break;
+        case 4: e = fwd_cl_by_rcp<4>(p, a, s); break;
+        case 2: e = fwd_cl_by_rcp<2>(p, a, s); break;
+        default: e = fwd_cl_by_rcp<1>(p, a, s); break;
+      }
+      if (e != hipSuccess) return e;
     }
+    return hipSuccess;
   }
   FwdK a{pp.recF, pp.neuron, sn, sd, state0, out, hfin, vsave, densave,
          p.B, p.T, p.H, p.Hp, p.U, p.KS, p.RC, eps, pp.cF, pp.cFi, pp.cFn};
@@ -4479,22 +4492,27 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           float* npart, float* gstate, float* rpart, const ClusterBuf& cb,
                           hipStream_t s) {
   if (p.CP > 0) {
-    hipError_t e = clear_cluster(p, cb, true, s);
-    if (e != hipSuccess) return e;
     // The register-resident fused chain (Hp = 256) prefetches saved rows that
     // every member of a cluster reads: keep a cluster on one XCD.
     const int xl = (chain_prefetches(p) && p.NCLB % 8 == 0) ? 1 : 0;
     BwdCK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart,
             gstate, rpart, cb.xch, cb.status, cb.spin, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB,
-            p.CPB, xl, pp.cB, pp.cBi, pp.cBn};
+            p.CPB, xl, pp.cB, pp.cBi, pp.cBn, 0};
     if (cmp_bwd(p) && (pp.cB == nullptr || pp.cBi == nullptr || pp.cBn == nullptr))
       return hipErrorInvalidValue;
-    switch (p.NBB) {
-      case 8: return bwd_cl_by_rcp<8>(p, a, s);
-      case 4: return bwd_cl_by_rcp<4>(p, a, s);
-      case 2: return bwd_cl_by_rcp<2>(p, a, s);
-      default: return bwd_cl_by_rcp<1>(p, a, s);
+    for (int l = 0; l < p.LCHB; ++l) {
+      hipError_t e = clear_cluster(p, cb, true, s, l == 0);
+      if (e != hipSuccess) return e;
+      a.R0 = l * p.NCLB * p.NBB;
+      switch (p.NBB) {
+        case 8: e = bwd_cl_by_rcp<8>(p, a, s); break;
+        case 4: e = bwd_cl_by_rcp<4>(p, a, s); break;
+        case 2: e = bwd_cl_by_rcp<2>(p, a, s); break;
+        default: e = bwd_cl_by_rcp<1>(p, a, s); break;
+      }
+      if (e != hipSuccess) return e;
     }
+    return hipSuccess;
   }
   BwdK a{pp.recB, pp.neuron, vsave, densave, gout, gs, ghfin, absave, dsn, dsd, npart, gstate,
          rpart, p.B, p.T, p.H, p.Hp, p.U, p.KSB, p.RCB, pp.cB, pp.cBi, pp.cBn, nullptr};

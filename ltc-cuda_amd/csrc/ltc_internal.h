@@ -81,6 +81,10 @@ struct Plan {
   int NCH;         // partials of the recurrent parameter-gradient reduction
   int NRC;         // row-chunks of the sensory backward reduction
   long long N;     // T * U * B unfold instances
+  // Cluster path, launches per call: 1, or with Hp > 1024 (no single-workgroup
+  // form covers a row) as many as take the B rows NCL * NB at a time, each
+  // launch holding at most one workgroup per CU. Forward and chain.
+  int LCH, LCHB;
 };
 
 // Derived, zero-padded parameter images built once per call by the prep kernel.

@@ -60,7 +60,8 @@ def test_sizes(capi):
     assert 0 < a < b and a % 256 == 0
     assert lib.ltc_bwd_workspace_bytes(24, 8, 128, 64, 6) > 0
     assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 0, 6) == -1
-    assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 2000, 6) == -1
+    assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 5000, 6) == -1
+    assert lib.ltc_fwd_workspace_bytes(1, 1, 1, 2000, 6) > 0  # clusters above H = 1024
     assert lib.ltc_bwd_workspace_bytes(1, 1, 1, 8, 0) == -1
 
 
@@ -78,7 +79,7 @@ def test_forward_rejects_bad_arguments_before_launch(capi):
     # Fake non-NULL addresses: every case must fail validation, so nothing runs.
     assert _fwd_call(capi, H=0) == 1 and "H >= 1" in capi.last_error()
     assert _fwd_call(capi, U=0) == 1 and "ode_unfolds" in capi.last_error()
-    assert _fwd_call(capi, H=1025) == 2 and "exceeds" in capi.last_error()
+    assert _fwd_call(capi, H=4097) == 2 and "exceeds" in capi.last_error()
     assert _fwd_call(capi, params=[1] * 10 + [None]) == 1
     assert _fwd_call(capi, save=1, saved=None) == 1 and "saved" in capi.last_error()
     assert _fwd_call(capi, wsb=16) == 1 and "workspace too small" in capi.last_error()
@@ -107,11 +108,11 @@ def test_step_entry_point_sizes(capi):
         a, b = fn(24, 128, 64), fn(48, 128, 64)
         assert 0 < a < b and a % 256 == 0
         assert fn(1, 0, 8) == -1 and fn(1, 8, 0) == -1 and fn(-1, 8, 8) == -1
-        assert fn(1, 8, 2000) == -1
+        assert fn(1, 8, 5000) == -1 and fn(1, 8, 2000) > 0
     for fn in (lib.ltc_ode_unfold_fwd_workspace_bytes, lib.ltc_ode_unfold_bwd_workspace_bytes):
         a, b = fn(24, 64, 6), fn(48, 64, 6)
         assert 0 < a < b and a % 256 == 0
-        assert fn(1, 8, 0) == -1 and fn(1, 0, 6) == -1 and fn(1, 2000, 6) == -1
+        assert fn(1, 8, 0) == -1 and fn(1, 0, 6) == -1 and fn(1, 5000, 6) == -1
     # the backward also recomputes the forward, so it needs more
     assert lib.ltc_ode_unfold_bwd_workspace_bytes(24, 64, 6) > \
         lib.ltc_ode_unfold_fwd_workspace_bytes(24, 64, 6)
@@ -142,7 +143,7 @@ def test_step_entry_points_reject_bad_arguments_before_launch(capi):
     assert "ode_unfolds" in capi.last_error()
     assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 5, 6, 1e-8, 1, 1, None, 256, big, None) == 1
     assert "v_buffer" in capi.last_error()
-    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 1025, 6, 1e-8, 0, 1, None, 256, big, None) == 2
+    assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 4097, 6, 1e-8, 0, 1, None, 256, big, None) == 2
     assert lib.ltc_ode_unfold_fwd(1, *t9, 2, 5, 6, 1e-8, 0, 1, None, 256, 16, None) == 1
     # ltc_ode_unfold_bwd(vbuf, 9 tensors, grad_out, B, H, U, eps, 10 grads, ws, wsb, s)
     g10 = [1] * 10
@@ -175,7 +176,8 @@ def _max_threads(nb):
 
 SHAPES = [(B, T, D, H, U) for B in (1, 2, 24, 255, 256, 257, 511, 1024, 4096, 5000)
           for (D, H) in ((1, 1), (5, 4), (128, 64), (32, 65), (128, 128), (7, 192), (256, 256),
-                         (512, 512), (64, 1000), (3, 1024), (16, 320), (16, 200))
+                         (512, 512), (64, 1000), (3, 1024), (16, 320), (16, 200), (40, 1100),
+                         (24, 2048), (16, 4096))
           for (T, U) in ((8, 6), (1, 1))]
 
 
@@ -260,13 +262,20 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         # device), and every member finishes at most one row per thread.
         assert p["Hp"] >= 256 and p["CP"] == p["Hp"] // 64
         assert p["NB"] in (1, 2, 4, 8)
-        assert p["NCL"] == -(-B // p["NB"]) and p["ode_workgroups"] == p["NCL"] * p["CP"]
-        assert p["ode_workgroups"] <= 256
+        assert p["ode_workgroups"] == p["NCL"] * p["CP"] <= 256
+        # one launch covers the batch, or (Hp > 1024 only) each launch takes the
+        # next NCL * NB rows
+        L = p["launches_fwd"]
+        assert L == p["launches_bwd"] and L == -(-B // (p["NCL"] * p["NB"]))
+        if p["Hp"] <= 1024:
+            assert L == 1 and p["NCL"] == -(-B // p["NB"])
+        else:
+            assert p["NCL"] == min(-(-B // p["NB"]), 256 // p["CP"]) and not p["fuse"]
         assert p["KS"] in (8, 16) and p["KS"] >= p["NB"]
         assert p["KS"] * p["RC"] == p["Hp"] and p["RC"] % 8 == 0
         assert p["threads"] == 64 * p["KS"] <= 1024
         assert p["ode_workgroups_bwd"] <= 256 and p["NBB"] in (1, 2, 4, 8)
-        assert p["ode_workgroups_bwd"] == p["CPB"] * -(-B // p["NBB"])
+        assert p["ode_workgroups_bwd"] == p["CPB"] * min(-(-B // p["NBB"]), 256 // p["CPB"])
         assert p["KSB"] >= p["NBB"]
         if p["fuse"]:
             # Hp = 256 / 512 chain: Hp/32 members of 32 columns, 512 threads,
