@@ -813,14 +813,17 @@ def main():
     dens = mask_density(m)
     counts = syn_counts(c, plan, dens)
 
-    for _ in range(args.warmup):
+    for _ in range(max(args.warmup, 20)):
         step(m, x, target)
     sync()
+    # the eager step is host-bound at this size: time enough of them (about
+    # 0.1 s) that one host hiccup does not move the mean
+    n_eager = max(args.steps, 800)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(n_eager):
         step(m, x, target)
     sync()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    eager_ms = (time.perf_counter() - t0) * 1e3 / n_eager
 
     split = time_split(m, x, target, max(10, args.steps // 2))
     kt = kernel_times(capi, lambda: step(m, x, target), max(10, args.steps // 2))

@@ -193,7 +193,7 @@ bool plan_cluster(ltc::Plan& p, int ncu) {
 // ---------------------------------------------------------------------------
 // Launch plan
 // ---------------------------------------------------------------------------
-ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
+ltc::Plan make_plan_uncached(int B, int T, int D, int H, int U, int ncu) {
   ltc::Plan p{};
   p.B = B;
   p.T = T;
@@ -307,6 +307,34 @@ ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
     if (p.NRC < 1) p.NRC = 1;
   }
   return p;
+}
+
+// The plans of the last few sizes asked for on this thread: a training step
+// asks for the same sizes several times (saved-buffer and workspace sizes,
+// then the call itself, forward and backward).
+ltc::Plan make_plan(int B, int T, int D, int H, int U, int ncu = device_cus()) {
+  constexpr int kKey = 7;
+  struct Entry {
+    int key[kKey];
+    ltc::Plan p;
+  };
+  constexpr int kEntries = 4;
+  thread_local Entry cache[kEntries];
+  thread_local int used = 0, next = 0;
+  // the plan also depends on the device's per-workgroup LDS limit
+  const int key[kKey] = {B, T, D, H, U, ncu, (int)chain_lds_limit()};
+  for (int i = 0; i < used; ++i) {
+    const Entry& e = cache[i];
+    bool hit = true;
+    for (int k = 0; k < kKey; ++k) hit = hit && e.key[k] == key[k];
+    if (hit) return e.p;
+  }
+  Entry& e = cache[next];
+  for (int i = 0; i < kKey; ++i) e.key[i] = key[i];
+  e.p = make_plan_uncached(B, T, D, H, U, ncu);
+  next = (next + 1) % kEntries;
+  if (used < kEntries) ++used;
+  return e.p;
 }
 
 // Carves 256-byte aligned regions out of one workspace in a fixed order; the

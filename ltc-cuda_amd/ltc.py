@@ -214,30 +214,22 @@ class TrueLiquidTimeConstant(nn.Module):
         h0 is an (h, c) pair for LSTM API compatibility; only h is used.
         """
         B, T, D = x_seq.shape
-        force_ts = getattr(self, "_force_torchscript", False)
+        d = self.__dict__
+        force_ts = d.get("_force_torchscript", False)
         on_hip = x_seq.is_cuda and x_seq.dtype == torch.float32 and not force_ts
-        if on_hip and self.training and self._module_path_ok(D):
-            # Whole layer in two library calls: LayerNorm, affine and the
-            # positivity transforms run inside the fused kernels. Without h0
-            # the library starts from a zero state itself (state None).
-            ltc_cuda.require_kernels()
-            state = None if h0 is None else h0[0]
-            if state is not None and state.dtype != x_seq.dtype:
-                state = state.to(x_seq.dtype)
-            # Straight from the registries (nn.Module attribute access costs a
-            # __getattr__ call per name, ~0.3 us each on this per-step path).
-            P, Bf = self._parameters, self._buffers
-            NP = self._modules["input_norm"]._parameters
-            leaves = [P["w"], P["erev"], Bf["sparsity_mask"], P["mu"], P["sigma"],
-                      P["sensory_w"], P["sensory_erev"], Bf["sensory_sparsity_mask"],
-                      P["sensory_mu"], P["sensory_sigma"], P["gleak"], P["vleak"], P["cm"],
-                      P["input_w"] if "input_w" in P else Bf["input_w"],
-                      P["input_b"] if "input_b" in P else Bf["input_b"],
-                      NP["weight"], NP["bias"]]
-            outputs, state = ltc_cuda.ltc_module_forward(
-                x_seq, state, leaves, self.dt, self.ode_unfolds, self.epsilon,
-                self.input_norm.eps)
-            return outputs, (state, state)
+        if on_hip and d["training"]:
+            leaves = self._module_leaves(D)
+            if leaves is not None:
+                # Whole layer in two library calls: LayerNorm, affine and the
+                # positivity transforms run inside the fused kernels. Without h0
+                # the library starts from a zero state itself (state None).
+                state = None if h0 is None else h0[0]
+                if state is not None and state.dtype != x_seq.dtype:
+                    state = state.to(x_seq.dtype)
+                outputs, state = ltc_cuda.ltc_module_forward(
+                    x_seq, state, leaves, d["dt"], d["ode_unfolds"], d["epsilon"],
+                    d["_modules"]["input_norm"].__dict__["eps"])
+                return outputs, (state, state)
 
         state = torch.zeros(B, self.hidden_dim, device=x_seq.device, dtype=x_seq.dtype)
         if h0 is not None:
@@ -279,11 +271,55 @@ class TrueLiquidTimeConstant(nn.Module):
 
     def _module_path_ok(self, D: int) -> bool:
         """Whether the fused module path applies: standard LayerNorm, fp32 leaves, D in range."""
-        norm = self.input_norm
-        return (D <= ltc_cuda.MODULE_MAX_D and isinstance(norm, nn.LayerNorm)
-                and norm.weight is not None and norm.bias is not None
-                and tuple(norm.normalized_shape) == (D,)
-                and self.w.dtype == torch.float32 and self.w.is_cuda)
+        return self._module_leaves(D) is not None
+
+    def _module_leaves(self, D: int):
+        """The 17 leaves of the fused module path in the library's order, or None
+        when the path does not apply (a LayerNorm other than nn.LayerNorm over D
+        with weight and bias, non-fp32 or host leaves, D out of range). Read
+        straight from the registries: nn.Module attribute access costs a
+        __getattr__ call per name on this per-step path."""
+        d = self.__dict__
+        P, Bf = d["_parameters"], d["_buffers"]
+        norm = d["_modules"].get("input_norm")
+        w = P.get("w")
+        if (D > ltc_cuda.MODULE_MAX_D or not isinstance(norm, nn.LayerNorm) or w is None
+                or w.dtype != torch.float32 or not w.is_cuda):
+            return None
+        nd = norm.__dict__
+        NP = nd["_parameters"]
+        lw, lb = NP.get("weight"), NP.get("bias")
+        if lw is None or lb is None or tuple(nd["normalized_shape"]) != (D,):
+            return None
+        return [w, P["erev"], Bf["sparsity_mask"], P["mu"], P["sigma"],
+                P["sensory_w"], P["sensory_erev"], Bf["sensory_sparsity_mask"],
+                P["sensory_mu"], P["sensory_sigma"], P["gleak"], P["vleak"], P["cm"],
+                P["input_w"] if "input_w" in P else Bf["input_w"],
+                P["input_b"] if "input_b" in P else Bf["input_b"], lw, lb]
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        """nn.Module.zero_grad over the layer's own parameters and its LayerNorm's,
+        read straight from their registries: the generic walk over
+        named_parameters costs more host time than the rest of a small layer's
+        step. Any other module structure takes nn.Module's own walk."""
+        d = self.__dict__
+        mods = d["_modules"]
+        norm = mods.get("input_norm")
+        if (len(mods) != 1 or type(norm) is not nn.LayerNorm or norm._modules
+                or d.get("_is_replica", False)):
+            return super().zero_grad(set_to_none)
+        for reg in (d["_parameters"], norm.__dict__["_parameters"]):
+            for p in reg.values():
+                if p is None or p.grad is None:
+                    continue
+                if set_to_none:
+                    p.grad = None
+                else:
+                    if p.grad.grad_fn is not None:
+                        p.grad.detach_()
+                    else:
+                        p.grad.requires_grad_(False)
+                    p.grad.zero_()
 
     def train(self, mode: bool = True):
         """Switching to train mode drops the eval-mode transform cache (ltc.py:328-332)."""

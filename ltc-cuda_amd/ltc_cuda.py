@@ -582,10 +582,11 @@ def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
     (no Python in the per-step forward or backward), else through
     LTCModuleFunction; both call the same two library entry points.
     """
+    ext = _torch_ext
+    if ext is not None:
+        return tuple(ext.module_apply(x_seq, state, leaves, float(dt), int(ode_unfolds),
+                                      float(epsilon), float(ln_eps)))
     require_kernels()
-    if _torch_ext is not None:
-        return tuple(_torch_ext.module_apply(x_seq, state, list(leaves), float(dt),
-                                             int(ode_unfolds), float(epsilon), float(ln_eps)))
     if state is None:
         state = torch.zeros(x_seq.shape[0], leaves[0].shape[0], device=x_seq.device,
                             dtype=torch.float32)

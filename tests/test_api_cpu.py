@@ -202,3 +202,29 @@ def test_module_apply_takes_absent_state_to_its_own_checks():
     for grad in (False, True):
         with torch.set_grad_enabled(grad), pytest.raises(RuntimeError, match="fp32-only"):
             ext.module_apply(x, None, lv, 0.1, 6, 1e-8, 1e-5)
+
+
+@pytest.mark.parametrize("set_to_none", [True, False])
+def test_zero_grad_matches_nn_module(set_to_none):
+    """The layer's own zero_grad walks its registries directly; it must leave every
+    gradient as nn.Module.zero_grad does, and defer to it for other structures."""
+    torch.manual_seed(0)
+    a = ltc.TrueLiquidTimeConstant(6, 5)
+    b = ltc.TrueLiquidTimeConstant(6, 5)
+    b.load_state_dict(a.state_dict())
+    x = torch.randn(2, 3, 6)
+    for m in (a, b):
+        out, _ = m(x)
+        out.sum().backward()
+    a.zero_grad(set_to_none=set_to_none)
+    torch.nn.Module.zero_grad(b, set_to_none=set_to_none)
+    for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
+        if set_to_none:
+            assert pa.grad is None and pb.grad is None, n
+        else:
+            assert torch.equal(pa.grad, pb.grad) and not pa.grad.any(), n
+    # an extra submodule: nn.Module's own walk reaches its parameters too
+    a.extra = torch.nn.Linear(2, 2)
+    a.extra.weight.grad = torch.ones(2, 2)
+    a.zero_grad()
+    assert a.extra.weight.grad is None
