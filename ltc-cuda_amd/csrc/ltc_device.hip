@@ -2022,11 +2022,13 @@ __device__ __forceinline__ void sens_companion128(const BwdK& k, const RecC& rc,
   const int T = k.T, D = rc.D, Dp = rc.Dp;
   const int h0 = 64 * jt + 8 * w;
   const bool fin = jt == 1 && w == 0;  // the wave that finishes the LayerNorm backward
+  // one 64-bit base, 32-bit offsets: the image rows of this wave's 8 neurons
+  const float4* srow = rc.sensB + (long long)h0 * Dp + lane;
   float4 q[8], sa[DC][8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    q[m] = rc.sensB[(long long)(h0 + m) * Dp + lane];
-    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = rc.sensB[(long long)(h0 + m) * Dp + lane + 64];
+    q[m] = srow[m * Dp];
+    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = srow[m * Dp + 64];
 #pragma unroll
     for (int kk = 0; kk < DC; ++kk) sa[kk][m] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
@@ -2281,11 +2283,13 @@ __device__ __forceinline__ void row_companion(const BwdK& k, const RowCompanion&
   int* flag = reinterpret_cast<int*>(dxr + 8 * NX);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int T = k.T;
+  // one 64-bit base, 32-bit offsets: the image rows of this wave's 8 neurons
+  const float4* srow = sensB + (long long)(8 * w) * Dp + lane;
   float4 q[8], sa[DC][8];
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
-    q[m] = sensB[(long long)(8 * w + m) * Dp + lane];
-    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = sensB[(long long)(8 * w + m) * Dp + lane + 64];
+    q[m] = srow[m * Dp];
+    if constexpr (DC == 2) qsh[(w * 8 + m) * 64 + lane] = srow[m * Dp + 64];
 #pragma unroll
     for (int kk = 0; kk < DC; ++kk) sa[kk][m] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
