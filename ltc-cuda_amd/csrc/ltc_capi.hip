@@ -116,7 +116,9 @@ int cluster_ks(const ltc::Plan& p, int nb) {
     const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
     if (lf > kClusterLds || ltc::cluster_chain_lds(nb, p.Hp, ks, 64, false) > chain_lds_limit())
       continue;
-    if (p.Hp == 256 && ks == 16 && lf + ltc::cmp_index_lds(64 * ks) > chain_lds_limit()) continue;
+    if (p.Hp == 256 && ks == 16 &&
+        lf + ltc::cmp_index_lds(64 * ks) + ltc::balance_lds(64 * ks) > chain_lds_limit())
+      continue;
     return ks;
   }
   return 0;
@@ -171,8 +173,11 @@ bool plan_cluster(ltc::Plan& p, int ncu) {
       const long long lf = (long long)nb * p.Hp * 4 + (long long)ks * nb * 64 * 8;
       if (lf > kClusterLds || ltc::cluster_chain_lds(nb, p.Hp, ks, 64, false) > chain_lds_limit())
         continue;
-      // the compacted forward (Hp = 256, 16 rows per thread) adds its slot table
-      if (p.Hp == 256 && ks == 16 && lf + ltc::cmp_index_lds(64 * ks) > chain_lds_limit()) continue;
+      // the compacted forward (Hp = 256, 16 rows per thread) adds its slot
+      // table and the balanced lane order's scratch
+      if (p.Hp == 256 && ks == 16 &&
+          lf + ltc::cmp_index_lds(64 * ks) + ltc::balance_lds(64 * ks) > chain_lds_limit())
+        continue;
       p.CP = cp;
       p.NCL = ncl;
       p.NB = nb;

@@ -118,6 +118,54 @@ __device__ __forceinline__ int wave_max(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// Balanced lane order of a compacted kernel. Its synapse lanes (one per
+// thread: a column's chunk of entries) hold different entry counts n <= 16,
+// and a wave runs as many slots as its fullest lane. Ranking the lanes by
+// count, largest first (ties by lane index), and giving the r-th ranked lane
+// to thread r puts lanes of nearly equal counts in each wave, so waves run
+// few padding slots, and the long waves and the short ones spread over the
+// SIMDs (the workgroups of a CU place each wave index on different SIMDs).
+// n: the count of this thread's own lane (lane = tid); returns the lane this
+// thread evaluates. Every thread of the workgroup must call it (it holds two
+// workgroup barriers). LDS: perm [nthr] ints, wcnt [nthr / 64][17] ints.
+__device__ __forceinline__ int balanced_lane(int n, int tid, int nthr, int* perm, int* wcnt) {
+  const int lane = tid & 63, w = tid >> 6, nw = nthr >> 6;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int local = 0;
+#pragma unroll
+  for (int v = 0; v <= 16; ++v) {
+    const unsigned long long m = __ballot(n == v);
+    if (n == v) local = __popcll(m & below);
+    if (lane == 0) wcnt[w * 17 + v] = __popcll(m);
+  }
+  __syncthreads();
+  // wave 0, lane v < 17: start[w][v] = (lanes of any wave with count > v)
+  // + (lanes of count v in waves before w), written over wcnt in place
+  if (w == 0) {
+    int tot = 0;
+    if (lane <= 16)
+      for (int x = 0; x < nw; ++x) tot += wcnt[x * 17 + lane];
+    int above = 0;
+#pragma unroll
+    for (int v = 1; v <= 16; ++v) {
+      const int t = __shfl(tot, v, 64);
+      if (v > lane) above += t;
+    }
+    if (lane <= 16) {
+      int run = above;
+      for (int x = 0; x < nw; ++x) {
+        const int c = wcnt[x * 17 + lane];
+        wcnt[x * 17 + lane] = run;
+        run += c;
+      }
+    }
+  }
+  __syncthreads();
+  perm[wcnt[w * 17 + n] + local] = tid;
+  __syncthreads();
+  return perm[tid];
+}
+
 // Sum of the K partials base[0], base[stride], ..., base[(K-1)*stride]: all K
 // LDS reads are issued before the first add, then a fixed pairwise tree.
 template <int K, class V>
@@ -847,13 +895,23 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
 
   float4 preg[RCP > 0 ? RCP : 1];
   int nslot = 0;  // CMP: slots the wave runs
+  // Synapse lane of this thread: (chunk sks, column so). With CMP the lanes
+  // are dealt in balanced order (balanced_lane); the owner role below keeps
+  // (ks, o).
+  int sks = ks, so = o;
   if constexpr (CMP) {
-    const int cnt = k.ccnt[o];
-    nslot = wave_max(cnt > ks ? (cnt - 1 - ks) / KS + 1 : 0);
+    int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);  // [threads]
+    const int cnt0 = k.ccnt[o];
+    const int lane_id = balanced_lane(cnt0 > ks ? (cnt0 - 1 - ks) / KS + 1 : 0, tid, nthr,
+                                      perm, perm + nthr);
+    sks = lane_id / Hp;
+    so = lane_id - sks * Hp;
+    const int cnt = k.ccnt[so];
+    nslot = wave_max(cnt > sks ? (cnt - 1 - sks) / KS + 1 : 0);
     int ix[RCP];
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
-      const long long a = (long long)(ks * RCP + rr) * Hp + o;
+      const long long a = (long long)(sks * RCP + rr) * Hp + so;
       preg[rr] = k.cimg[a];
       ix[rr] = k.cidx[a] * NB * 4;
     }
@@ -914,7 +972,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
         }
       }
 #pragma unroll
-      for (int b = 0; b < NB; ++b) red[(ks * NB + b) * Hp + o] = make_float2(na[b], qa[b]);
+      for (int b = 0; b < NB; ++b) red[(sks * NB + b) * Hp + so] = make_float2(na[b], qa[b]);
       lds_barrier();
 #pragma unroll
       for (int m = 0; m < MO; ++m) {
@@ -3577,13 +3635,23 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
 
   float4 preg[RCP > 0 ? RCP : 1];
   int nslot = 0;  // CMP: slots the wave runs
+  // Synapse lane of this thread (chunk sks, member column so): with CMP in
+  // balanced order (balanced_lane); the owner and exchange roles keep (ks, o).
+  int sks = ks, so = o;
   if constexpr (CMP) {
-    const int cnt = k.ccnt[c];
-    nslot = wave_max(cnt > ks ? (cnt - 1 - ks) / kCmpChunks + 1 : 0);
+    int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);  // [threads]
+    const int cnt0 = k.ccnt[c];
+    const int lane_id = balanced_lane(cnt0 > ks ? (cnt0 - 1 - ks) / kCmpChunks + 1 : 0, tid,
+                                      nthr, perm, perm + nthr);
+    sks = lane_id >> 6;
+    so = lane_id & 63;
+    const int sc = p * kClW + so;
+    const int cnt = k.ccnt[sc];
+    nslot = wave_max(cnt > sks ? (cnt - 1 - sks) / kCmpChunks + 1 : 0);
     int ix[RCP];
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
-      const long long a = (long long)(ks * RCP + rr) * Hp + c;
+      const long long a = (long long)(sks * RCP + rr) * Hp + sc;
       preg[rr] = k.cimg[a];
       ix[rr] = k.cidx[a] * NB * 4;
     }
@@ -3644,7 +3712,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
         }
       }
 #pragma unroll
-      for (int b = 0; b < NB; ++b) red[(ks * NB + b) * kClW + o] = make_float2(na[b], qa[b]);
+      for (int b = 0; b < NB; ++b) red[(sks * NB + b) * kClW + so] = make_float2(na[b], qa[b]);
       lds_barrier();
       const unsigned tag = (unsigned)(t * U + u + 1);
       unsigned long long* slot = xbase + (long long)(tag & 1) * CP * PER;

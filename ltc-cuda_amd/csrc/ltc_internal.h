@@ -131,6 +131,9 @@ struct Prepped {
 constexpr int kCmpChunks = 16;
 // LDS of the compacted kernels' slot table: one int per slot per thread.
 inline long long cmp_index_lds(int threads) { return (long long)threads * kCmpChunks * 4; }
+// LDS scratch of the balanced lane order (balanced_lane in the device code):
+// one int per thread and 17 per wave.
+inline long long balance_lds(long long threads) { return threads * 4 + (threads / 64) * 17 * 4; }
 // The compacted cluster chain pads each alpha/beta row by two pairs.
 inline long long cmp_pad_lds(int hp) { return 16LL * hp; }
 
@@ -404,7 +407,7 @@ inline long long cluster_bwd_lds(const Plan& p) {
 // partials [KS][NB][64] float2, and with the compacted image the slot table.
 inline long long cluster_fwd_lds(const Plan& p) {
   return (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * 64 * 8 +
-         (cmp_fwd(p) ? cmp_index_lds(64 * p.KS) : 0);
+         (cmp_fwd(p) ? cmp_index_lds(64 * p.KS) + balance_lds(64 * p.KS) : 0);
 }
 // Dynamic LDS of the single-workgroup forward: state rows and the KS
 // partials, or the wave-owned single-row forward's state and staged sums.
@@ -413,9 +416,11 @@ inline long long cluster_fwd_lds(const Plan& p) {
 constexpr int kRowSensSteps = 32;
 constexpr int kRowChainUnfolds = 48;
 inline long long fwd_lds(const Plan& p) {
-  // with the compacted image, the slot table: one int per slot per thread
+  // with the compacted image, the slot table (one int per slot per thread)
+  // and the balanced lane order's scratch (one int per thread, 17 per wave)
+  const long long thr = (long long)p.Hp * p.KS;
   const long long base = (long long)p.NB * p.Hp * 4 + (long long)p.KS * p.NB * p.Hp * 8 +
-                         (generic_fwd_cmp(p) ? (long long)p.Hp * p.KS * p.RC * 4 : 0);
+                         (generic_fwd_cmp(p) ? thr * p.RC * 4 + balance_lds(thr) : 0);
   // the wave-owned single-row forms: the double-buffered state and the
   // staged sensory sums
   const long long wave = 2LL * p.Hp * 4 + 2LL * kRowSensSteps * p.Hp * 4;

@@ -196,7 +196,9 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
         Hp, NB, KS = p["Hp"], p["NB"], p["KS"]
         base = NB * Hp * 4 + KS * NB * 64 * 8
         assert base <= 60 * 1024
-        table = 64 * KS * 16 * 4 if (Hp == 256 and KS == 16 and p["RC"] == 16) else 0
+        # plus the balanced lane order's scratch (an int per thread, 17 per wave)
+        table = (64 * KS * 16 * 4 + 64 * KS * 4 + KS * 17 * 4
+                 if (Hp == 256 and KS == 16 and p["RC"] == 16) else 0)
         assert p["lds_fwd"] == base + table <= 159 * 1024
     else:
         # state rows and partials under 64 KiB; with register-resident operands
@@ -210,7 +212,10 @@ def test_launch_plan_fits_the_hardware_limits(capi, shape):
             # 32 staged steps of sensory sums
             assert p["lds_fwd"] == 2 * Hp * 4 + 2 * 32 * Hp * 4
         elif not (NB == 1 and Hp == 64):
-            table = Hp * KS * RC * 4 if RC in (4, 8, 16) else 0
+            # the slot table, and the balanced lane order's scratch (an int per
+            # thread and 17 per wave)
+            thr = Hp * KS
+            table = thr * RC * 4 + thr * 4 + thr // 64 * 17 * 4 if RC in (4, 8, 16) else 0
             assert p["lds_fwd"] == base + table <= 159 * 1024
     # the cluster chain may use up to one CU's LDS (160 KiB on MI355X, less 1 KiB);
     # the single-workgroup chain its partials under 64 KiB, or with FUSE one padded
