@@ -94,7 +94,8 @@ void plan_fused_chain(ltc::Plan& p, int ncu) {
     if (ncl > slots) continue;
     // at Hp = 256 the compacted chain adds its slot table
     if (ltc::cluster_chain_lds(nb, p.Hp, 16, 32, p.Hp == 256) +
-            (p.Hp == 256 ? ltc::cmp_index_lds(512) + ltc::cmp_pad_lds(p.Hp) : 0) >
+            (p.Hp == 256 ? ltc::cmp_index_lds(512) + ltc::cmp_pad_lds(p.Hp) + ltc::balance_lds(512)
+                         : 0) >
         chain_lds_limit())
       continue;
     p.CPB = cp;

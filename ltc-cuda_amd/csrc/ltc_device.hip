@@ -3951,14 +3951,24 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
 
   float4 preg[RCP > 0 ? RCP : 1];
   int nmine = 0, nslot = 0;  // CMP: this lane's entries, slots the wave runs
+  // Synapse lane of this thread (chunk sks, column sc = presynaptic neuron of
+  // its synapses): with CMP in balanced order (balanced_lane); the owner and
+  // exchange roles keep (ks, c).
+  int sks = ks, so = o;
   if constexpr (CMP) {
-    const int cnt = k.ccnt[c];
-    nmine = cnt > ks ? (cnt - 1 - ks) / kCmpChunks + 1 : 0;
+    int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);  // [threads]
+    const int cnt0 = k.ccnt[c];
+    const int lane_id = balanced_lane(cnt0 > ks ? (cnt0 - 1 - ks) / kCmpChunks + 1 : 0, tid,
+                                      nthr, perm, perm + nthr);
+    sks = lane_id / JW;
+    so = lane_id - sks * JW;
+    const int cnt = k.ccnt[p * JW + so];
+    nmine = cnt > sks ? (cnt - 1 - sks) / kCmpChunks + 1 : 0;
     nslot = wave_max(nmine);
     int ix[RCP];
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
-      const long long a = (long long)(ks * RCP + rr) * Hp + c;
+      const long long a = (long long)(sks * RCP + rr) * Hp + p * JW + so;
       preg[rr] = k.cimg[a];
       ix[rr] = k.cidx[a] * ABS * 8;
     }
@@ -3969,6 +3979,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) preg[rr] = k.recB[(long long)(r0 + rr) * Hp + c];
   }
+  const int sc = p * JW + so;  // column of this thread's synapses
   float4 gacc[NACC];
   if constexpr (FUSE) {
 #pragma unroll
@@ -4047,7 +4058,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   float cvi[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
-    cvi[b] = b0 + b < B ? k.vsave[(n_last * B + b0 + b) * Hp + c] : 0.f;
+    cvi[b] = b0 + b < B ? k.vsave[(n_last * B + b0 + b) * Hp + sc] : 0.f;
 
   for (long long n = n_last; n >= 0; --n) {
     const int t = (int)(n / U), u = (int)(n - (long long)t * U);
@@ -4112,7 +4123,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       });
     }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) red[(ks * NB + b) * JW + o] = acc[b];
+    for (int b = 0; b < NB; ++b) red[(sks * NB + b) * JW + so] = acc[b];
     // Without PF: the saved values of unfold n-1, requested now and consumed
     // after the exchange, whose wait covers their latency.
     float nden = 1.f, nvk = 0.f, nvk1 = 0.f;
@@ -4169,7 +4180,7 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
       if (!ok) gave_up = 1;
       if (owner) own_ab(n - 1, pden[bo * Hp + c], vm[bo * Hp + c], vn[bo * Hp + c]);
 #pragma unroll
-      for (int b = 0; b < NB; ++b) cvi[b] = b0 + b < B ? vm[b * Hp + c] : 0.f;
+      for (int b = 0; b < NB; ++b) cvi[b] = b0 + b < B ? vm[b * Hp + sc] : 0.f;
     } else if (n > 0) {
       // Words in flight per thread: 4 for the streamed fused chain (7.5 words
       // per thread at Hp = 512; two poll rounds instead of four), else 2.
@@ -4221,14 +4232,14 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   }
   if constexpr (FUSE) {
     // This cluster's share of the recurrent parameter gradients for synapses
-    // (i = c, j = r0 + rr), layout [cluster][4][i][j] as rec_grad_kernel's.
+    // (i = sc, j = r0 + rr), layout [cluster][4][i][j] as rec_grad_kernel's.
     const long long HH = (long long)Hp * Hp;
     if constexpr (CMP) {
-      float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)c * Hp;
+      float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)sc * Hp;
 #pragma unroll
       for (int rr = 0; rr < NACC; ++rr) {
         if (rr < nmine) {
-          const int j = k.cidx[(long long)(ks * RCP + rr) * Hp + c];
+          const int j = k.cidx[(long long)(sks * RCP + rr) * Hp + sc];
           out[j] = gacc[rr].x;
           out[HH + j] = gacc[rr].y;
           out[2 * HH + j] = gacc[rr].z;

@@ -401,7 +401,9 @@ inline int cmp_chunks_bwd(const Plan& p) {
 // compacted image, its slot table.
 inline long long cluster_bwd_lds(const Plan& p) {
   return cluster_chain_lds(p.NBB, p.Hp, p.KSB, p.JWB, chain_prefetches(p)) +
-         (cmp_bwd(p) ? cmp_index_lds(p.JWB * p.KSB) + cmp_pad_lds(p.Hp) : 0);
+         (cmp_bwd(p) ? cmp_index_lds(p.JWB * p.KSB) + cmp_pad_lds(p.Hp) +
+                           balance_lds(p.JWB * p.KSB)
+                     : 0);
 }
 // Dynamic LDS of a cluster forward member: state rows [NB][Hp], the KS
 // partials [KS][NB][64] float2, and with the compacted image the slot table.
