@@ -1177,7 +1177,8 @@ int ltc_module_backward(const float* x, long long sxb, long long sxt, long long 
   }
   if (!sens_comp) {
     e = timed(ltc::K_SENS_BWD, s, [&] {
-      return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s);
+      return ltc::launch_sens_bwd(p, lw.xa, xas, wb.pp, wb.dsn, wb.dsd, wb.spart, wb.dxpart, s,
+                                  lp.s_mask);
     });
     if (e != hipSuccess) return hip_fail("sensory backward launch", e);
   }

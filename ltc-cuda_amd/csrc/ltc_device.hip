@@ -2728,6 +2728,168 @@ __global__ __launch_bounds__(256) void sens_bwd_kernel(SensBK k) {
 }
 
 // ---------------------------------------------------------------------------
+// Module-path sensory backward over the unmasked synapses only. A synapse
+// whose mask entry is 0 has Ws = 0: its four leaf gradients are zero and it
+// adds nothing to dL/dx, so it can be skipped. Same grid, rows and staging as
+// sens_bwd_kernel (64 inputs x 32 neurons per block), but each thread's lane
+// is one input d and one group of 8 neurons, and holds only that group's
+// unmasked synapses of d, in ascending neuron order (NS = the wave's longest
+// list, the loop instantiated per NS). The block's 256 lanes run in balanced
+// order (balanced_lane), so each wave holds lists of nearly equal length. A
+// slot's dL/dsn, dL/dsd come from its neuron's column of the staged rows (a
+// per-lane LDS read; 32 float2 fill the 64 banks once). Partials of masked
+// synapses stay unwritten: the module finalize writes zero gradients for
+// them without reading their partials.
+// ---------------------------------------------------------------------------
+template <int NS>
+__device__ __forceinline__ void sens_bwd_cmp_rows(const SensBK& k, const float4 (&q)[8],
+                                                  unsigned hsel, int nmine, int ld, int g,
+                                                  int db, int hb, float2 (*absh)[32],
+                                                  float (*xsh)[64], float (*dxr)[SB_RT][64]) {
+  float s1[NS], s2[NS], s3[NS], s4[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) s1[i] = s2[i] = s3[i] = s4[i] = 0.f;
+  const int Dp = k.Dp, Hp = k.Hp;
+  const int rb = blockIdx.z * k.rows_per;
+  const int re = min(k.BT, rb + k.rows_per);
+  constexpr int NA = SB_RT * 32 / 256, NX = SB_RT * 64 / 256;
+  float2 na[NA];
+  float nx[NX];
+  auto fetch = [&](int r0) {
+    const int cnt = min(SB_RT, re - r0);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int e = threadIdx.x + i * 256;
+      const int rr = e >> 5, hh = e & 31;
+      na[i] = make_float2(0.f, 0.f);
+      if (rr < cnt) {
+        const long long ix = (long long)(r0 + rr) * Hp + hb * 32 + hh;
+        na[i] = make_float2(k.dsn[ix], k.dsd[ix]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int e = threadIdx.x + i * 256;
+      const int rr = e >> 6, dd = e & 63;
+      const int row = r0 + rr, dg = db + dd;
+      nx[i] = 0.f;
+      if (rr < cnt && dg < k.D) {
+        const int b = row / k.T, t = row - b * k.T;
+        nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      }
+    }
+  };
+  // the column of each slot's neuron in the staged rows
+  int col[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) col[i] = g * 8 + ((hsel >> (3 * i)) & 7);
+  if (rb < re) fetch(rb);
+  for (int r0 = rb; r0 < re; r0 += SB_RT) {
+    const int cnt = min(SB_RT, re - r0);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int e = threadIdx.x + i * 256;
+      absh[e >> 5][e & 31] = na[i];
+    }
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+      const int e = threadIdx.x + i * 256;
+      xsh[e >> 6][e & 63] = nx[i];
+    }
+    __syncthreads();
+    if (r0 + SB_RT < re) fetch(r0 + SB_RT);
+    for (int rr = 0; rr < cnt; ++rr) {
+      const float xv = xsh[rr][ld];
+      float dxp = 0.f;
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        const float2 c = absh[rr][col[i]];
+        const float a = gate(fmaf(q[i].x, xv, q[i].y));
+        const float a2 = fmaf(-a, a, a);
+        const float gm = fmaf(c.x, q[i].z, c.y);
+        s1[i] = fmaf(gm, a, s1[i]);
+        s2[i] = fmaf(c.x, a, s2[i]);
+        const float ga2 = gm * a2;
+        s3[i] += ga2;
+        s4[i] = fmaf(ga2, xv, s4[i]);
+        dxp = fmaf(ga2, q[i].w, dxp);
+      }
+      dxr[g][rr][ld] = dxp;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < cnt * 64; e += 256) {
+      const int rr = e >> 6, dd = e & 63;
+      const float sum = dxr[0][rr][dd] + dxr[1][rr][dd] + dxr[2][rr][dd] + dxr[3][rr][dd];
+      k.dxpart[((long long)hb * k.BT + r0 + rr) * Dp + db + dd] = sum;
+    }
+    __syncthreads();
+  }
+  const long long DH = (long long)Dp * Hp;
+  float* out = k.spart + (long long)blockIdx.z * 4 * DH;
+  const int d = db + ld, h0 = hb * 32 + g * 8;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    if (i < nmine) {
+      const long long e = (long long)(h0 + ((hsel >> (3 * i)) & 7)) * Dp + d;
+      out[e] = s1[i];
+      out[DH + e] = s2[i];
+      out[2 * DH + e] = s3[i];
+      out[3 * DH + e] = s4[i];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void sens_bwd_cmp_kernel(SensBK k,
+                                                           const float* __restrict__ smask,
+                                                           int H) {
+  __shared__ __align__(16) float2 absh[SB_RT][32];
+  __shared__ float xsh[SB_RT][64];
+  __shared__ float dxr[4][SB_RT][64];
+  __shared__ int perm[256 + 4 * 17];
+  const int tid = threadIdx.x;
+  const int db = blockIdx.x * 64, hb = blockIdx.y;
+  const int D = k.D, Dp = k.Dp;
+  // Unmasked synapses of a lane (input d, neurons h0 .. h0 + 7), as a bit set.
+  auto keep_bits = [&](int d, int h0) {
+    unsigned m = 0;
+    if (d < D) {
+      const float* row = smask + (long long)d * H;
+#pragma unroll
+      for (int hh = 0; hh < 8; ++hh)
+        if (h0 + hh < H && row[h0 + hh] != 0.f) m |= 1u << hh;
+    }
+    return m;
+  };
+  const unsigned m0 = keep_bits(db + (tid & 63), hb * 32 + (tid >> 6) * 8);
+  const int lane_id = balanced_lane(__popc(m0), tid, 256, perm, perm + 256);
+  const int ld = lane_id & 63, g = lane_id >> 6;
+  const int d = db + ld, h0 = hb * 32 + g * 8;
+  unsigned m = keep_bits(d, h0);
+  const int nmine = __popc(m);
+  // The lane's unmasked synapses in ascending neuron order: operands in
+  // q[0 .. nmine), neuron offsets as 3-bit fields of hsel.
+  float4 q[8];
+  unsigned hsel = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    q[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (m != 0) {
+      const int hh = __builtin_ctz(m);
+      m &= m - 1;
+      q[i] = k.sensB[(long long)(h0 + hh) * Dp + d];
+      hsel |= (unsigned)hh << (3 * i);
+    }
+  }
+  switch (wave_max(nmine)) {
+#define LTC_SBC(N) \
+  case N: sens_bwd_cmp_rows<N>(k, q, hsel, nmine, ld, g, db, hb, absh, xsh, dxr); break;
+    LTC_SBC(1) LTC_SBC(2) LTC_SBC(3) LTC_SBC(4) LTC_SBC(5) LTC_SBC(6) LTC_SBC(7)
+    default: sens_bwd_cmp_rows<8>(k, q, hsel, nmine, ld, g, db, hb, absh, xsh, dxr); break;
+#undef LTC_SBC
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Finalize: fixed-order sums of every partial buffer, then the closed forms.
 // Flat index space in four segments: (H*H recurrent) + (H neurons) +
 // (D*H sensory) + (BT*D x). A launch covers [base, base + count) of it, so
@@ -3438,12 +3600,20 @@ __global__ __launch_bounds__(256) void finalize_leaf_kernel(FinLeafK k) {
   e -= nrec;
   if (e < nsens) {
     const int h = (int)(e / D), d = (int)(e - (long long)h * D);
+    const long long o = (long long)d * H + h;
+    const float mk = k.lp.s_mask[o];
+    if (mk == 0.f) {
+      // A masked synapse's four gradients are zero; the compacted sensory
+      // backward leaves its partials unwritten.
+      float* dst = q == 0 ? k.g.s_w : (q == 1 ? k.g.s_erev : (q == 2 ? k.g.s_mu : k.g.s_sigma));
+      dst[o] = 0.f;
+      return;
+    }
     const long long DH = (long long)Dp * Hp;
     const float s = sum_partials_plane(k.spart + q * DH + (long long)h * Dp + d, 4 * DH, k.NRC);
     const float s1 = quad_lane<0>(s), s2 = quad_lane<1>(s);
     const float s3 = quad_lane<2>(s), s4 = quad_lane<3>(s);
-    const long long o = (long long)d * H + h;
-    const float sw = k.lp.s_w[o], mk = k.lp.s_mask[o];
+    const float sw = k.lp.s_w[o];
     const float Ws = softplus_t(sw) * mk;
     if (q == 0) {
       k.g.s_w[o] = s1 * mk * softplus_grad(sw);
@@ -4691,11 +4861,15 @@ hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
 
 hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            const float* dsn, const float* dsd, float* spart, float* dxpart,
-                           hipStream_t s) {
+                           hipStream_t s, const float* smask) {
   const int BT = p.B * p.T;
   const int rows_per = (BT + p.NRC - 1) / p.NRC;
   SensBK a{x, xs, pp.sensB, dsn, dsd, spart, dxpart, p.T, p.D, p.Dp, p.Hp, BT, rows_per};
-  LTC_LAUNCH(sens_bwd_kernel, dim3(p.Dp / 64, p.Hp / 32, p.NRC), dim3(256), 0, s, a);
+  const dim3 grid(p.Dp / 64, p.Hp / 32, p.NRC);
+  if (smask != nullptr)
+    LTC_LAUNCH(sens_bwd_cmp_kernel, grid, dim3(256), 0, s, a, smask, p.H);
+  else
+    LTC_LAUNCH(sens_bwd_kernel, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -478,9 +478,11 @@ hipError_t launch_ode_bwd(const Plan& p, const Prepped& pp, const float* vsave,
                           hipStream_t s);
 hipError_t launch_rec_grad(const Plan& p, const Prepped& pp, const float* vsave,
                            const float2* absave, float* rpart, hipStream_t s);
+// smask (the module path's sensory mask, (D,H)): skip the masked synapses
+// (sens_bwd_cmp_kernel), whose partials stay unwritten.
 hipError_t launch_sens_bwd(const Plan& p, const float* x, Strides3 xs, const Prepped& pp,
                            const float* dsn, const float* dsd, float* spart, float* dxpart,
-                           hipStream_t s);
+                           hipStream_t s, const float* smask = nullptr);
 struct GradOut {
   float* x;        // (B,T,D) contiguous
   float* w_pos;    // (H,H)
