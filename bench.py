@@ -244,7 +244,10 @@ def syn_counts(c, plan=None, density=(1.0, 1.0)):
     - sens_fwd: the compacted sensory launch skips masked sensory synapses
       (every sensory launch; the dense form only when the module forward forms
       the sums in its parameter-image launch: plan field module_sens_in_prep);
-    - sens_bwd: the sensory backward evaluates every sensory synapse;
+    - sens_bwd: the module path's sensory backward launch skips masked
+      sensory synapses; the companions of the fused row backward (plan field
+      module_row_bwd_fused, and module_row128_rec_fused with D <= 128)
+      evaluate every one;
     - rec_fwd / rec_dv: the compacted forward and chain skip masked recurrent
       synapses (plan fields cmp_fwd / cmp_bwd);
     - rec_bwd: the parameter-gradient sums, skipped with the chain only when
@@ -256,8 +259,10 @@ def syn_counts(c, plan=None, density=(1.0, 1.0)):
     plan = plan or {}
     skip_bwd = plan.get("cmp_bwd") and plan.get("fuse")
     sens_cmp = bool(plan) and not plan.get("module_sens_in_prep")
+    sens_bwd_dense = (not plan or plan.get("module_row_bwd_fused")
+                      or (plan.get("module_row128_rec_fused") and plan.get("Dp", 0) <= 128))
     return {"sens_fwd": sens * (rho_s if sens_cmp else 1.0),
-            "sens_bwd": sens,
+            "sens_bwd": sens * (1.0 if sens_bwd_dense else rho_s),
             "rec_fwd": rec * (rho_r if plan.get("cmp_fwd") else 1.0),
             "rec_bwd": rec * (rho_r if skip_bwd else 1.0),
             "rec_dv": rec * (rho_r if plan.get("cmp_bwd") else 1.0),
