@@ -251,10 +251,13 @@ ltc::Plan make_plan_uncached(int B, int T, int D, int H, int U, int ncu) {
     return fits(ks) ? ks : 0;
   };
   // Per-unfold latency is lowest with one wave per SIMD for the forward at
-  // small H (fewer partials, same VALU work per CU); the chain kernel keeps
-  // the widest split, whose register-resident operands carry the fused
-  // gradient accumulators.
-  const int want_f = p.Hp <= 64 ? 4 : 16;
+  // small H with one row per workgroup (fewer partials, same VALU work per
+  // CU). With several rows per workgroup at Hp = 64 (many workgroups per CU)
+  // eight chunks per column measured faster: the compacted forward's waves,
+  // in balanced lane order, then hold 8 entries each at most (C5 forward
+  // 79.2 -> 76.8 us). The chain kernel keeps the widest split, whose
+  // register-resident operands carry the fused gradient accumulators.
+  const int want_f = p.Hp <= 64 ? (p.NB >= 2 ? 8 : 4) : 16;
   for (;;) {
     const int kf = pick_ks(p.NB, want_f, false), kb = pick_ks(p.NB, 16, true);
     if ((kf > 0 && kb > 0) || p.NB == 1) {
