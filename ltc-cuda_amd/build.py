@@ -68,7 +68,7 @@ def ext_path() -> str:
 
 
 def ext_command(out: str) -> list:
-    """Host-only C++ build of the torch glue (the autograd Function of the
+    """Host-only C++ build of the torch glue (the autograd node of the
     fused module path), linked against libltc_hip.so through $ORIGIN."""
     import sysconfig
     import torch

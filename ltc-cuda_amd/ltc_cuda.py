@@ -39,7 +39,7 @@ logger = logging.getLogger(__name__)
 _HAS_CUDA_KERNELS = False
 _cuda_module = None
 _LOAD_ERROR: str | None = None
-# C++ autograd Function of the fused module path (csrc/ltc_torch_ext.cpp), over
+# C++ autograd node of the fused module path (csrc/ltc_torch_ext.cpp), over
 # the same library; None when that extension is not built.
 _torch_ext = None
 
@@ -578,7 +578,7 @@ def ltc_module_forward(x_seq, state, leaves, dt, ode_unfolds, epsilon, ln_eps):
     """Whole-layer fused call; `leaves` in MODULE_LEAVES order, `state` None
     for a zero initial state.
 
-    Runs through the C++ autograd Function when the torch extension is built
+    Runs through the C++ autograd node when the torch extension is built
     (no Python in the per-step forward or backward), else through
     LTCModuleFunction; both call the same two library entry points.
     """

@@ -457,7 +457,7 @@ def test_module_path_strided_input_and_determinism():
 
 
 def test_cpp_and_python_module_functions_agree_bitwise():
-    """The C++ autograd Function (torch extension) and the Python LTCModuleFunction call
+    """The C++ autograd node (torch extension) and the Python LTCModuleFunction call
     the same two library entry points; outputs and every gradient must be identical."""
     assert ltc_cuda._torch_ext is not None, "torch extension (_ltc_torch) not loaded"
     B, T, D, H = 8, 5, 48, 40
