@@ -818,12 +818,12 @@ def main():
     dens = mask_density(m)
     counts = syn_counts(c, plan, dens)
 
-    for _ in range(max(args.warmup, 20)):
+    for _ in range(max(args.warmup, 200)):
         step(m, x, target)
     sync()
     # the eager step is host-bound at this size: time enough of them (about
-    # 0.1 s) that one host hiccup does not move the mean
-    n_eager = max(args.steps, 800)
+    # 0.3 s) that one host hiccup does not move the mean
+    n_eager = max(args.steps, 2000)
     t0 = time.perf_counter()
     for _ in range(n_eager):
         step(m, x, target)

@@ -3527,20 +3527,28 @@ __device__ __forceinline__ void finalize_leaf_poison(const FinLeafK& k, long lon
 }
 
 // One plane's sum over n partials at stride `stride`, in partial order, up to
-// 32 loads in flight at once. Indices past n reload the last partial and add
-// zero, which leaves the sum bitwise unchanged (it starts at +0 and a
-// round-to-nearest sum is never -0 unless both terms are).
+// 32 loads in flight at once. Loads past the n-th reload the last partial and
+// add zero instead, which leaves the sum bitwise unchanged (it starts at +0,
+// and a round-to-nearest sum is never -0 unless both terms are). The address
+// advances by one stride per load (up to the last partial), and the adds take
+// their bound from a copy of the count that the compiler cannot see through:
+// 32 separately formed 64-bit offsets, or the loads' 32 bound conditions kept
+// for the adds, would be live in scalar registers at once and spill them.
 __device__ __forceinline__ float sum_partials_plane(const float* p, long long stride, int n) {
   float acc = 0.f;
   for (int z = 0; z < n; z += 32) {
     float v[32];
+    const float* q = p + (long long)z * stride;
+    const int m = n - z;  // partials left from z on, >= 1
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      const int zi = z + i < n ? z + i : n - 1;
-      v[i] = p[(long long)zi * stride];
+      v[i] = *q;
+      if (i + 1 < m) q += stride;
     }
+    int ma = m;
+    asm volatile("" : "+s"(ma));
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc += z + i < n ? v[i] : 0.f;
+    for (int i = 0; i < 32; ++i) acc += i < ma ? v[i] : 0.f;
   }
   return acc;
 }
