@@ -114,3 +114,17 @@ def test_output_gradient_of_another_dtype(use_ext):
     for a, b in zip(ref, [p.grad for p in m.parameters()]):
         assert a.dtype == b.dtype == torch.float32
         assert torch.allclose(a, b, rtol=1e-6, atol=1e-7)
+
+
+def test_inference_mode_matches_no_grad(use_ext):
+    """Under torch.inference_mode the layer records nothing and returns the
+    no-grad forward's outputs bitwise (inference tensors)."""
+    m = _module()
+    x = torch.randn(B, T, D, device=DEV)
+    with torch.no_grad():
+        ref, (rh, _) = m(x)
+    with torch.inference_mode():
+        out, (h, _) = m(x)
+    assert out.is_inference() and h.is_inference()
+    assert out.grad_fn is None
+    assert torch.equal(out, ref) and torch.equal(h, rh)
