@@ -405,3 +405,17 @@ def test_cluster_wait_budget_and_status_without_gpu(capi):
         lib.ltc_set_cluster_spin_ticks(prev)
     if lib.ltc_device_count() == 0:
         assert lib.ltc_device_status(0) == 3 and capi.last_error()
+
+
+@pytest.mark.parametrize("shape,nrc", [((256, 64, 256, 256, 6), 48), ((128, 32, 512, 512, 6), 12),
+                                       ((4, 3, 40, 100, 6), 2), ((600, 2, 8, 16, 6), 64)],
+                         ids=["C3", "C4", "few-rows", "cap"])
+def test_sensory_backward_row_chunks(capi, shape, nrc):
+    """Row chunks of the sensory backward: two rounds of three resident blocks
+    per CU (256 CUs without a device), at most 64 chunks and at least 8 rows
+    each."""
+    B, T, D, H, U = shape
+    p = capi.plan(B, T, D, H, U)
+    assert p["NRC"] == nrc
+    bpc = (p["Dp"] // 64) * (p["Hp"] // 32)
+    assert p["NRC"] * bpc >= min(6 * 256, bpc * min(64, (B * T + 7) // 8))
