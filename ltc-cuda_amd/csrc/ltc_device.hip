@@ -3935,6 +3935,199 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl_kernel(FwdCK k) {
   }
 }
 
+// The compacted cluster forward (register-resident operands, RC = 16) with
+// its NB >= 2 rows in two groups of NB/2 that take turns, so that each
+// group's exchange travels while the other group's synapses are evaluated.
+// Phase (g, n) evaluates group g's rows at unfold n. After the phase's one
+// barrier, the owners of group g (waves 0 .. NB-1, which the SIMDs issue
+// first) finish v_g^{n+1} of the member's columns and publish it, tag n + 1,
+// at the start of the next phase, ahead of their own synapses, while the
+// other waves go straight on. A phase also gathers the partners' columns of
+// the other group's newest state: each gathering thread issues its word's
+// load halfway through its synapse slots and writes the value into LDS before
+// the barrier. Two barriers per unfold, as in the one-group form, but the
+// owners' reduction and the exchange no longer sit between the unfolds.
+// Exchange words as in ode_fwd_cl_kernel: [cluster][2 slots][CP][NB][64], a
+// group's rows at [g*NB/2, (g+1)*NB/2); each group's tags rise by one per
+// unfold and alternate the two slots, so a slot is overwritten only after
+// every partner has published the group's following state, which it does
+// after it has gathered the slot's words. Waits are bounded as there.
+template <int NB>
+__global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
+  static_assert(NB == 2 || NB == 4 || NB == 8, "two groups of rows");
+  constexpr int HB = NB / 2, RCP = 16, PER = NB * kClW, PERG = HB * kClW;
+  extern __shared__ float4 lds4[];
+  __shared__ int gave_up;
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
+  float* vs = reinterpret_cast<float*>(lds4);                          // [Hp][NB]
+  float2* red = reinterpret_cast<float2*>(vs + NB * Hp);               // [2][KS][HB][64]
+  int4* slot_tab = reinterpret_cast<int4*>(red + 2 * KS * HB * kClW);  // [4][threads]
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int ks = __builtin_amdgcn_readfirstlane(tid >> 6), o = tid & 63;
+  int p, cl;
+  cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
+  const int c = p * kClW + o;
+  const int b0 = k.R0 + cl * NB;
+  const bool owner = ks < NB;  // finishes row bo = ks of column c (the plan keeps KS >= NB)
+  const int bo = ks, og = ks / HB;
+  const bool live = owner && b0 + bo < B;
+  unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
+  const float C = k.neuron[c], G = k.neuron[Hp + c], L = k.neuron[2 * Hp + c];
+  const float GL = G * L, CG = C + G;
+
+  // Synapse lane in balanced order, as in ode_fwd_cl_kernel.
+  float4 preg[RCP];
+  int nslot, sks, so;
+  {
+    int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);
+    const int cnt0 = k.ccnt[c];
+    const int lane_id = balanced_lane(cnt0 > ks ? (cnt0 - 1 - ks) / kCmpChunks + 1 : 0, tid,
+                                      nthr, perm, perm + nthr);
+    sks = lane_id >> 6;
+    so = lane_id & 63;
+    const int sc = p * kClW + so;
+    const int cnt = k.ccnt[sc];
+    nslot = wave_max(cnt > sks ? (cnt - 1 - sks) / kCmpChunks + 1 : 0);
+    int ix[RCP];
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(sks * RCP + rr) * Hp + sc;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * NB * 4;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
+  }
+  if (tid == 0) gave_up = 0;
+  for (int e = tid; e < NB * Hp; e += nthr) {
+    const int b = e / Hp, j = e - b * Hp;
+    vs[j * NB + b] = (k.state0 != nullptr && b0 + b < B && j < H)
+                         ? k.state0[(long long)(b0 + b) * H + j]
+                         : 0.f;
+  }
+  lds_barrier();
+
+  // This thread's word of a group gather (threads below (CP - 1) * PERG):
+  // partner member gm, row gr of the group, column gc.
+  const bool gth = tid < (CP - 1) * PERG;
+  int gm = 0, gr = 0, gc = 0;
+  if (gth) {
+    const int q = tid / PERG, r = tid - q * PERG;
+    gm = q + (q >= p ? 1 : 0);
+    gr = r / kClW;
+    gc = r - gr * kClW;
+  }
+  const long long N = (long long)T * U;
+  float snr = 0.f, sdr = 0.f;  // owners: their row's sensory sums at the current step
+  float vlast = 0.f;           // owners: their column's newest state
+  bool pend = false;           // owners: a finish of their group is due
+  float2 pnq = make_float2(0.f, 0.f);
+  long long pn = 0;
+  auto load_sens = [&](int t) {
+    snr = sdr = 0.f;
+    if (live) {
+      const long long e = ((long long)(b0 + bo) * T + t) * Hp + c;
+      snr = k.sn[e];
+      sdr = k.sd[e];
+    }
+  };
+  // The owners' finish of unfold pn: v^{pn+1} of (row bo, column c) from the
+  // reduced sums pnq; publish (when a partner needs it), saved state, output.
+  auto finish = [&](bool publish) {
+    const int t = (int)(pn / U), u = (int)(pn - (long long)t * U);
+    const float vold = vs[c * NB + bo];
+    const float den = CG + (pnq.y + sdr) + k.eps;
+    const float num = C * vold + GL + (pnq.x + snr);
+    const float rden = __builtin_amdgcn_rcpf(den);
+    const float vnew = c < H ? num * rden : 0.f;
+    if (publish) {
+      const unsigned tag = (unsigned)(pn + 1);
+      xch_put(xbase + (long long)(tag & 1) * CP * PER + p * PER + bo * kClW + o, vnew, tag);
+    }
+    if (k.vsave != nullptr && live) {
+      const long long e = (pn * B + b0 + bo) * Hp + c;
+      k.vsave[e] = vold;
+      k.densave[e] = rden;
+    }
+    vs[c * NB + bo] = vnew;
+    vlast = vnew;
+    if (u == U - 1) {
+      if (live && c < H) k.out[((long long)(b0 + bo) * T + t) * H + c] = vnew;
+      if (t + 1 < T) load_sens(t + 1);
+    }
+  };
+  if (owner && T > 0) load_sens(0);
+  for (long long n = 0; n < N; ++n) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      if (pend) {
+        pend = false;
+        finish(true);
+      }
+      // The other group's newest state: v_0^{n+1} (published at the start
+      // of this phase) while evaluating group 1, v_1^n while evaluating
+      // group 0; not needed past the last unfold or before the first.
+      const int gg = 1 - g;
+      const long long gtag = g == 1 ? n + 1 : n;
+      const bool need = g == 1 ? n + 1 < N : n > 0;
+      unsigned long long* gw = xbase + (long long)(gtag & 1) * CP * PER + gm * PER +
+                               (gg * HB + gr) * kClW + gc;
+      unsigned long long w = 0;
+      float na[HB], qa[HB];
+#pragma unroll
+      for (int b = 0; b < HB; ++b) na[b] = qa[b] = 0.f;
+#pragma unroll
+      for (int q = 0; q < RCP / 4; ++q) {
+        if (q == RCP / 8 && need && gth) w = xch_get(gw);
+        if (4 * q < nslot) {
+          const int4 of = slot_tab[q * nthr + tid];
+          fwd_synapses_cmp<HB>(preg + 4 * q, vs + g * HB, of.x, of.y, na, qa);
+          if (4 * q + 2 < nslot)
+            fwd_synapses_cmp<HB>(preg + 4 * q + 2, vs + g * HB, of.z, of.w, na, qa);
+        }
+      }
+      float2* rg = red + g * KS * HB * kClW;
+#pragma unroll
+      for (int b = 0; b < HB; ++b) rg[(sks * HB + b) * kClW + so] = make_float2(na[b], qa[b]);
+      if (k.spin <= 0) {
+        gave_up = 1;  // a budget of 0: give up at the first wait, as xch_gather does
+      } else if (need && gth) {
+        const long long t0 = wall_clock64();
+        bool ok = true;
+        while ((unsigned)(w >> 32) != (unsigned)gtag) {
+          if (wall_clock64() - t0 > k.spin) {
+            ok = false;
+            break;
+          }
+          w = xch_get(gw);
+        }
+        if (ok)
+          vs[(gm * kClW + gc) * NB + gg * HB + gr] = __uint_as_float((unsigned)w);
+        else
+          gave_up = 1;
+      }
+      lds_barrier();
+      if (gave_up) {
+        if (live && c < H) k.hfin[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
+        if (tid == 0) __hip_atomic_store(k.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      if (owner && og == g) {
+        pnq = ks_sum_wide(rg + (bo - g * HB) * kClW + o, HB * kClW, KS);
+        pn = n;
+        pend = true;
+      }
+    }
+  }
+  // group 1's last finish: nothing gathers v_1^N
+  if (pend) finish(false);
+  if (live) {
+    if (c < H) k.hfin[(long long)(b0 + bo) * H + c] = vlast;
+    if (k.vsave != nullptr) k.vsave[((long long)T * U * B + b0 + bo) * Hp + c] = vlast;
+  }
+}
+
 // Fused chain synapse phase with streamed operands (RCS rows per thread,
 // fully unrolled so that each row's four gradient sums stay in registers).
 // Members are 32 columns wide, so a wave holds two reduction chunks: its
@@ -4566,7 +4759,9 @@ template <int NB>
 hipError_t fwd_cl_by_rcp(const Plan& p, const FwdCK& a, hipStream_t s) {
   const dim3 grid(p.NCL * p.CP), block(64 * p.KS);
   const size_t lds = fwd_cl_lds_bytes(p);
-  if (p.RC == 16)
+  if (p.RC == 16 && NB >= 2)
+    LTC_LAUNCH((ode_fwd_cl2_kernel<(NB >= 2 ? NB : 2)>), grid, block, lds, s, a);
+  else if (p.RC == 16)
     LTC_LAUNCH((ode_fwd_cl_kernel<NB, 16>), grid, block, lds, s, a);
   else
     LTC_LAUNCH((ode_fwd_cl_kernel<NB, 0>), grid, block, lds, s, a);
