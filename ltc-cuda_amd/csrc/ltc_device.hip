@@ -4630,6 +4630,321 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
   }
 }
 
+// The compacted fused cluster chain (register-resident operands, Hp = 256,
+// 32-column members of 512 threads) with its NB >= 2 rows in two groups of
+// NB/2 that take turns, as ode_fwd_cl2_kernel does for the forward. Phase
+// (g, n) runs group g's synapses at unfold n (reverse time). After the
+// phase's one barrier the owners of group g (waves of ks < NB, which the SIMDs
+// issue first) reduce dL/dv^n of their columns and publish it (tag n) at the
+// start of the next phase, and that next phase, which gathers the partners'
+// words of group g halfway through its slots, rebuilds group g's alpha/beta
+// of unfold n-1 before its barrier. The saved 1/den and v of the cluster's
+// rows come through LDS prefetches issued in group 1's phases two phases
+// ahead of use (after that phase's word loads, so the word waits do not wait
+// for them): 1/den of two unfolds and v of three slots. The four gradient
+// sums of each synapse take the rows in the same order as the one-group
+// kernel, so they are bitwise the same.
+template <int NB>
+__global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
+  static_assert(NB == 2 || NB == 4 || NB == 8, "two groups of rows");
+  constexpr int JW = 32, RCP = 16, HB = NB / 2, PER = NB * JW, PERG = HB * JW;
+  constexpr int ABS = NB + 2;  // padded alpha/beta rows, as in ode_bwd_cl_kernel
+  constexpr int HPC = 16 * RCP;  // Hp = 256
+  constexpr int XW = 2;          // gather words per thread and group: (CP-1)*PERG <= 2*512
+  extern __shared__ float4 lds4[];
+  __shared__ int gave_up;
+  const int Hp = k.Hp, H = k.H, KS = k.KS, B = k.B, T = k.T, U = k.U, CP = k.CP;
+  float2* ab = reinterpret_cast<float2*>(lds4);                  // [Hp][ABS]
+  float* red = reinterpret_cast<float*>(ab + ABS * Hp);         // [2][KS][HB][JW]
+  float* pden = red + 2 * KS * HB * JW;                         // [2][NB][Hp] by unfold parity
+  float* pv = pden + 2 * NB * Hp;                               // [3][NB][Hp] by slot mod 3
+  int4* slot_tab = reinterpret_cast<int4*>(pv + 3 * NB * Hp);   // [4][threads]
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int ks = tid / JW, o = tid % JW;
+  int p, cl;
+  cluster_coords(blockIdx.x, CP, k.xcd_local != 0, p, cl);
+  const int c = p * JW + o;
+  const int b0 = k.R0 + cl * NB;
+  const bool owner = ks < NB;
+  const int bo = ks, og = ks / HB;
+  const bool live = owner && b0 + bo < B;
+  unsigned long long* xbase = k.xch + (long long)cl * 2 * CP * PER;
+  const long long BHp = (long long)B * Hp;
+  const float C = k.neuron[c];
+  if (T == 0) return;
+  auto pden_at = [&](long long m) { return pden + (m & 1) * NB * Hp; };
+  auto pv_at = [&](long long m) { return pv + (m % 3) * NB * Hp; };
+
+  float4 preg[RCP];
+  int nmine, nslot, sks, so;
+  {
+    int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);
+    const int cnt0 = k.ccnt[c];
+    const int lane_id = balanced_lane(cnt0 > ks ? (cnt0 - 1 - ks) / kCmpChunks + 1 : 0, tid,
+                                      nthr, perm, perm + nthr);
+    sks = lane_id / JW;
+    so = lane_id - sks * JW;
+    const int cnt = k.ccnt[p * JW + so];
+    nmine = cnt > sks ? (cnt - 1 - sks) / kCmpChunks + 1 : 0;
+    nslot = wave_max(nmine);
+    int ix[RCP];
+#pragma unroll
+    for (int rr = 0; rr < RCP; ++rr) {
+      const long long a = (long long)(sks * RCP + rr) * Hp + p * JW + so;
+      preg[rr] = k.cimg[a];
+      ix[rr] = k.cidx[a] * ABS * 8;
+    }
+#pragma unroll
+    for (int q = 0; q < RCP / 4; ++q)
+      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
+  }
+  const int sc = p * JW + so;
+  float4 gacc[RCP];
+#pragma unroll
+  for (int rr = 0; rr < RCP; ++rr) gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tid == 0) gave_up = 0;
+
+  // Owner state, as in ode_bwd_cl_kernel.
+  float g = 0.f, gdir = 0.f, accA = 0.f, accB = 0.f, pC = 0.f, pGv = 0.f, pA = 0.f;
+  auto own_ab = [&](float den, float vk, float vk1) {
+    float al = 0.f, be = 0.f;
+    gdir = 0.f;
+    if (live && c < H) {
+      al = g * den;  // saved 1/den
+      be = -g * vk1 * den;
+      accA += al;
+      accB += be;
+      pC += al * (vk - vk1);
+      pGv += al * vk1;
+      pA += al;
+      gdir = al * C;
+    }
+    ab[c * ABS + bo] = make_float2(al, be);
+  };
+  auto gout_at = [&](int b, int t, int col) {
+    return k.gout[(long long)(b0 + b) * k.gs.b + (long long)t * k.gs.t + (long long)col * k.gs.c];
+  };
+  auto prefetch = [&](long long m) {  // 1/den of unfold m, v of slot m
+    rows_to_lds_fixed<NB, HPC, 512>(k.densave + m * BHp, b0, B, pden_at(m), tid);
+    rows_to_lds_fixed<NB, HPC, 512>(k.vsave + m * BHp, b0, B, pv_at(m), tid);
+  };
+
+  const long long n_last = (long long)T * U - 1;
+  // Unfold n_last's alpha/beta of every column from the output gradients.
+  if (owner) {
+    if (live && c < H) {
+      g = gout_at(bo, T - 1, c);
+      if (k.ghfin != nullptr) g += k.ghfin[(long long)(b0 + bo) * H + c];
+    }
+    float den = 1.f, vk = 0.f, vk1 = 0.f;
+    if (live) {
+      const long long e = (n_last * B + b0 + bo) * Hp + c;
+      den = k.densave[e];
+      vk = k.vsave[e];
+      vk1 = k.vsave[e + BHp];
+    }
+    own_ab(den, vk, vk1);
+  }
+  for (int e = tid; e < (CP - 1) * PER; e += nthr) {
+    const int q = e / PER, r = e - q * PER, b = r / JW;
+    const int col = (q + (q >= p ? 1 : 0)) * JW + (r - b * JW);
+    float al = 0.f, be = 0.f;
+    if (b0 + b < B && col < H) {
+      float gg = gout_at(b, T - 1, col);
+      if (k.ghfin != nullptr) gg += k.ghfin[(long long)(b0 + b) * H + col];
+      const long long ee = (n_last * B + b0 + b) * Hp + col;
+      const float rden = k.densave[ee];
+      al = gg * rden;
+      be = -gg * k.vsave[ee + BHp] * rden;
+    }
+    ab[col * ABS + b] = make_float2(al, be);
+  }
+  // The prefetched rows the first three phases read: v of slots n_last and
+  // n_last - 1, 1/den of unfold n_last - 1.
+  rows_to_lds_fixed<NB, HPC, 512>(k.vsave + n_last * BHp, b0, B, pv_at(n_last), tid);
+  if (n_last > 0) prefetch(n_last - 1);
+  wait_vm();
+  lds_barrier();
+
+  // This thread's gather words (x < XW): partner member, row of the group, column.
+  int gm[XW], gr[XW], gcl[XW];
+  bool gth[XW];
+#pragma unroll
+  for (int x = 0; x < XW; ++x) {
+    const int e = tid + x * nthr;
+    gth[x] = e < (CP - 1) * PERG;
+    const int q = e / PERG, r = e - q * PERG;
+    gm[x] = q + (q >= p ? 1 : 0);
+    gr[x] = r / JW;
+    gcl[x] = gm[x] * JW + (r - gr[x] * JW);
+  }
+  bool pend = false;  // owners: their group's finish is due
+  long long pn = 0;
+  float gnext = 0.f;
+  for (long long n = n_last; n >= 0; --n) {
+    const int t = (int)(n / U), u = (int)(n - (long long)t * U);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      // (e) the owners of the previous phase's group: dL/dv^{pn}, published
+      // for the partners' alpha/beta of unfold pn - 1.
+      bool own_next = false;
+      if (pend) {
+        pend = false;
+        const int pt = (int)(pn / U), pu = (int)(pn - (long long)pt * U);
+        const float* rg = red + og * KS * HB * JW;
+        const float s = ks_sum_wide(rg + (bo - og * HB) * JW + o, HB * JW, KS);
+        g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
+        if (pn > 0) {
+          g += gnext;
+          const unsigned tag = (unsigned)pn;
+          xch_put(xbase + (long long)(tag & 1) * CP * PER + p * PER + bo * JW + o, g, tag);
+          own_next = true;
+        }
+        if (pu == 0 && live) {
+          const long long e = ((long long)(b0 + bo) * T + pt) * Hp + c;
+          k.dsn[e] = accA;
+          k.dsd[e] = accB;
+        }
+        if (pu == 0) accA = accB = 0.f;
+      }
+      // The output gradient entering at this unfold's step boundary.
+      if (owner && og == gi) gnext = (n > 0 && u == 0 && live && c < H) ? gout_at(bo, t - 1, c) : 0.f;
+      // (a) group gi's synapses at unfold n; the other group's newest words
+      // are loaded halfway: group 0's dL/dv^n while running group 1, group
+      // 1's dL/dv^{n+1} while running group 0.
+      const int gg = 1 - gi;
+      const long long gtag = gi == 1 ? n : n + 1;
+      const bool need = gi == 1 ? n > 0 : n < n_last;
+      const long long am = gtag - 1;  // the unfold whose alpha/beta the words rebuild
+      unsigned long long* gslot = xbase + (long long)(gtag & 1) * CP * PER;
+      unsigned long long w[XW];
+      float cvi[HB], acc[HB];
+      const float* vn = pv_at(n);
+#pragma unroll
+      for (int b = 0; b < HB; ++b) {
+        cvi[b] = b0 + gi * HB + b < B ? vn[(gi * HB + b) * Hp + sc] : 0.f;
+        acc[b] = 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < RCP / 4; ++q) {
+        if (q == RCP / 8) {
+#pragma unroll
+          for (int x = 0; x < XW; ++x)
+            if (need && gth[x])
+              w[x] = xch_get(gslot + gm[x] * PER + (gg * HB + gr[x]) * JW + (gcl[x] - gm[x] * JW));
+          // group 1's phases issue the prefetch of unfold n - 2, after the
+          // word loads
+          if (gi == 1 && n >= 2) prefetch(n - 2);
+        }
+        if (4 * q < nslot) {
+          const int4 of = slot_tab[q * nthr + tid];
+          const int off[4] = {of.x, of.y, of.z, of.w};
+#pragma unroll
+          for (int h = 0; h < 4; h += 2) {
+            if (4 * q + h < nslot) {
+#pragma unroll
+              for (int i = 0; i < 2; ++i) {
+                const int rr = 4 * q + h + i;
+                bwd_synapse_cmp<HB>(preg[rr], ab + gi * HB, off[h + i], cvi, acc, gacc[rr]);
+                asm volatile("" : "+v"(gacc[rr].x), "+v"(gacc[rr].y), "+v"(gacc[rr].z),
+                             "+v"(gacc[rr].w));
+              }
+            }
+          }
+        }
+      }
+      // (b) the group's partials
+      float* rgi = red + gi * KS * HB * JW;
+#pragma unroll
+      for (int b = 0; b < HB; ++b) rgi[(sks * HB + b) * JW + so] = acc[b];
+      // (c) the other group's alpha/beta of unfold am from the partners'
+      // words, and the owners' own entry of the group they just finished
+      if (k.spin <= 0) {
+        gave_up = 1;  // a budget of 0: give up at the first wait, as xch_gather does
+      } else if (need) {
+        const float* dn = pden_at(am);
+        const float* vk1 = pv_at(am + 1);
+#pragma unroll
+        for (int x = 0; x < XW; ++x) {
+          if (!gth[x]) continue;
+          const long long t0 = wall_clock64();
+          bool ok = true;
+          unsigned long long* wa =
+              gslot + gm[x] * PER + (gg * HB + gr[x]) * JW + (gcl[x] - gm[x] * JW);
+          while ((unsigned)(w[x] >> 32) != (unsigned)gtag) {
+            if (wall_clock64() - t0 > k.spin) {
+              ok = false;
+              break;
+            }
+            w[x] = xch_get(wa);
+          }
+          if (!ok) {
+            gave_up = 1;
+            continue;
+          }
+          const int b = gg * HB + gr[x], col = gcl[x];
+          float al = 0.f, be = 0.f;
+          if (b0 + b < B && col < H) {
+            const float gv = __uint_as_float((unsigned)w[x]);
+            const float rden = dn[b * Hp + col];
+            al = gv * rden;
+            be = -gv * vk1[b * Hp + col] * rden;
+          }
+          ab[col * ABS + b] = make_float2(al, be);
+        }
+      }
+      if (own_next) own_ab(pden_at(pn - 1)[bo * Hp + c], pv_at(pn - 1)[bo * Hp + c],
+                           pv_at(pn)[bo * Hp + c]);
+      // the prefetch issued in the previous (group 1) phase, visible to
+      // every wave after this barrier
+      if (gi == 0) wait_vm();
+      lds_barrier();
+      if (gave_up) {
+        if (k.gstate != nullptr && live && c < H)
+          k.gstate[(long long)(b0 + bo) * H + c] = __builtin_nanf("");
+        if (tid == 0) __hip_atomic_store(k.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      if (owner && og == gi) {
+        pn = n;
+        pend = true;
+      }
+    }
+  }
+  // group 1's finish of unfold 0 (nothing is published at unfold 0)
+  if (pend) {
+    const float* rg = red + og * KS * HB * JW;
+    const float s = ks_sum_wide(rg + (bo - og * HB) * JW + o, HB * JW, KS);
+    g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
+    if (live) {
+      const long long e = ((long long)(b0 + bo) * T) * Hp + c;
+      k.dsn[e] = accA;
+      k.dsd[e] = accB;
+    }
+  }
+  if (live) {
+    if (k.gstate != nullptr && c < H) k.gstate[(long long)(b0 + bo) * H + c] = g;
+    float* np = k.npart + (long long)(b0 + bo) * 3 * Hp + c;
+    np[0] = pC;
+    np[Hp] = pGv;
+    np[2 * Hp] = pA;
+  }
+  // This cluster's share of the recurrent parameter gradients, layout
+  // [cluster][4][i][j], as ode_bwd_cl_kernel writes it.
+  const long long HH = (long long)Hp * Hp;
+  float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)sc * Hp;
+#pragma unroll
+  for (int rr = 0; rr < RCP; ++rr) {
+    if (rr < nmine) {
+      const int j = k.cidx[(long long)(sks * RCP + rr) * Hp + sc];
+      out[j] = gacc[rr].x;
+      out[HH + j] = gacc[rr].y;
+      out[2 * HH + j] = gacc[rr].z;
+      out[3 * HH + j] = gacc[rr].w;
+    }
+  }
+}
+
 // Clears the cluster exchange words (tag 0) and the status word before a
 // cluster launch; a kernel rather than a memset so that graph capture
 // records a kernel node.
@@ -4776,7 +5091,9 @@ hipError_t bwd_cl_by_rcp(const Plan& p, const BwdCK& a, hipStream_t s) {
     // 32-column members, 512 threads: 16 register-resident synapses each
     // (Hp = 256) or 32 streamed ones (Hp = 512).
     if (p.JWB != 32 || p.KSB != 16) return hipErrorInvalidConfiguration;
-    if (p.RCB == 16)
+    if (p.RCB == 16 && NB >= 2)
+      LTC_LAUNCH((ode_bwd_cl2_kernel<(NB >= 2 ? NB : 2)>), grid, block, lds, s, a);
+    else if (p.RCB == 16)
       LTC_LAUNCH((ode_bwd_cl_kernel<NB, 32, 16, true>), grid, block, lds, s, a);
     else if (p.RCB == 32)
       LTC_LAUNCH((ode_bwd_cl_kernel<NB, 32, 0, true, 32>), grid, block, lds, s, a);

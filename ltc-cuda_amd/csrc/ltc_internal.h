@@ -309,8 +309,13 @@ constexpr int kImageSlackRows = 8;
 // reduction partials [KS][NB][JW], and with `pf` three [NB][Hp] blocks of
 // saved forward values (1/den of one unfold, v of two slots) prefetched ahead
 // of use.
+// Saved values the prefetching chain keeps per (row, column): 1/den of one
+// unfold and v of two slots (12 bytes), or in the two-group form
+// (ode_bwd_cl2_kernel, NB >= 2) 1/den of two unfolds and v of three slots.
+inline long long chain_pf_bytes(int nb) { return nb >= 2 ? 20 : 12; }
 inline long long cluster_chain_lds(int nb, int hp, int ks, int jw, bool pf) {
-  return (long long)nb * hp * 8 + (long long)ks * nb * jw * 4 + (pf ? 12LL * nb * hp : 0);
+  return (long long)nb * hp * 8 + (long long)ks * nb * jw * 4 +
+         (pf ? chain_pf_bytes(nb) * nb * hp : 0);
 }
 // The cluster chain prefetches saved values when its operands are
 // register-resident: the fused form at Hp = 256.

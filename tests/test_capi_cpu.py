@@ -419,3 +419,19 @@ def test_sensory_backward_row_chunks(capi, shape, nrc):
     assert p["NRC"] == nrc
     bpc = (p["Dp"] // 64) * (p["Hp"] // 32)
     assert p["NRC"] * bpc >= min(6 * 256, bpc * min(64, (B * T + 7) // 8))
+
+
+@pytest.mark.parametrize("B,nb,nbb", [(16, 1, 1), (48, 1, 2), (100, 2, 4), (200, 4, 8)])
+def test_two_group_cluster_plans(capi, B, nb, nbb):
+    """Rows per cluster at H = 256 (forward NB, chain NBB; the two-group kernels
+    run from two rows on), and the chain's LDS: alpha/beta rows padded to NBB + 2
+    pairs, the KS partials, the prefetched saved values (1/den and v: 12 bytes per
+    row and column, 20 in the two-group form, which keeps 1/den of two unfolds and
+    v of three slots), the slot table and the balanced-order scratch."""
+    p = capi.plan(B, 2, 8, 256, 6)
+    assert (p["CP"], p["NB"], p["NBB"]) == (4, nb, nbb)
+    Hp, ks, jw, thr = 256, 16, 32, 512
+    pf = 20 if nbb >= 2 else 12
+    lds = ((nbb + 2) * Hp * 8 + ks * nbb * jw * 4 + pf * nbb * Hp + thr * 16 * 4
+           + thr * 4 + (thr // 64) * 17 * 4)
+    assert p["lds_bwd"] == lds <= 159 * 1024

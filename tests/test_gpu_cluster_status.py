@@ -17,15 +17,36 @@ from _gpu_common import DEV, _native, _perturbed_module, boundary, gpu_backward,
 
 pytestmark = pytest.mark.gpu
 
-B, T, D, H = 16, 2, 8, 256
+T, D, H = 2, 8, 256
 DEFAULT_TICKS = 20000000
+# Batch sizes at H = 256: one row per cluster in the forward and the chain
+# (the one-group kernels), one-row forward and two-row chain clusters, and
+# four-row forward and eight-row chain clusters (the two-group kernels).
+BATCHES = [16, 48, 200]
+
+
+@pytest.fixture(params=BATCHES, ids=lambda b: f"B{b}")
+def B(request):
+    return request.param
 
 
 @pytest.fixture()
-def capi():
+def capi(B):
     c = ltc_cuda._cuda_module.capi
-    assert c.plan(B, T, D, H, 6)["CP"] > 0
+    plan = c.plan(B, T, D, H, 6)
+    assert plan["CP"] > 0
+    print(f"B={B}: forward rows per cluster {plan['NB']}, chain {plan['NBB']}", flush=True)
     c.device_status(clear=True)  # start clean
+    yield c
+    assert c.lib.ltc_set_cluster_spin_ticks(DEFAULT_TICKS) >= 0
+    c.lib.ltc_device_status(1)
+
+
+@pytest.fixture()
+def capi_row():
+    """The library, for the single-workgroup give-up tests (no cluster plan)."""
+    c = ltc_cuda._cuda_module.capi
+    c.device_status(clear=True)
     yield c
     assert c.lib.ltc_set_cluster_spin_ticks(DEFAULT_TICKS) >= 0
     c.lib.ltc_device_status(1)
@@ -50,7 +71,7 @@ def _expect_fault(capi):
     assert capi.lib.ltc_device_status(0) == 0  # the first read cleared it
 
 
-def test_forward_give_up_sets_every_output_to_nan(capi):
+def test_forward_give_up_sets_every_output_to_nan(capi, B):
     args = boundary(B, T, D, H, seed=31)
     with _NoWait(capi):
         _, (out, h, saved) = gpu_forward(args, save=True)
@@ -62,7 +83,7 @@ def test_forward_give_up_sets_every_output_to_nan(capi):
     capi.device_status()
 
 
-def test_backward_give_up_sets_every_gradient_to_nan(capi):
+def test_backward_give_up_sets_every_gradient_to_nan(capi, B):
     args = boundary(B, T, D, H, seed=32)
     dev_args, (out, h, saved) = gpu_forward(args, save=True)
     assert torch.isfinite(out).all()
@@ -79,7 +100,7 @@ def test_backward_give_up_sets_every_gradient_to_nan(capi):
     capi.device_status()
 
 
-def test_module_path_give_up_is_reported_through_python(capi):
+def test_module_path_give_up_is_reported_through_python(capi, B):
     m = _perturbed_module(D, H, seed=33).to(DEV)
     x = torch.randn(B, T, D, device=DEV)
     with _NoWait(capi):
@@ -94,7 +115,8 @@ def test_module_path_give_up_is_reported_through_python(capi):
 
 
 @pytest.mark.parametrize("D1", [128, 48])
-def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi, D1):
+def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi_row, D1):
+    capi = capi_row
     """At H = 64 the module backward's sensory and LayerNorm part runs in
     companion workgroups that wait for the chain's words: with a budget of 0
     they leave at once, and the finalize writes NaN into every gradient."""
@@ -125,7 +147,8 @@ def test_fused_row_backward_give_up_sets_every_gradient_to_nan(capi, D1):
 
 @pytest.mark.parametrize("shape", [(32, 4, 128, 128), (5, 3, 40, 100), (4, 3, 200, 100)],
                          ids=lambda s: "B%dT%dD%dH%d" % s)
-def test_recurrent_gradient_companions_give_up_sets_every_gradient_to_nan(capi, shape):
+def test_recurrent_gradient_companions_give_up_sets_every_gradient_to_nan(capi_row, shape):
+    capi = capi_row
     """At Hp = 128 the module backward forms the recurrent parameter-gradient
     sums in companion workgroups that wait for the chain's alpha/beta words:
     with a budget of 0 they leave at once, and the finalize writes NaN into
