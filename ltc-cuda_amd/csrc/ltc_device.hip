@@ -2662,15 +2662,19 @@ __global__ __launch_bounds__(256) void sens_bwd_kernel(SensBK k) {
         na[i] = make_float2(k.dsn[ix], k.dsd[ix]);
       }
     }
+    // x rows r0 + wv + 4i, wave-uniform: one division per chunk, then steps
+    // of four rows
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int dg = db + (int)(threadIdx.x & 63);
+    int b = (r0 + wv) / k.T, t = r0 + wv - b * k.T;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int e = threadIdx.x + i * 256;
-      const int rr = e >> 6, dd = e & 63;
-      const int row = r0 + rr, dg = db + dd;
       nx[i] = 0.f;
-      if (rr < cnt && dg < k.D) {
-        const int b = row / k.T, t = row - b * k.T;
-        nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      if (wv + 4 * i < cnt && dg < k.D) nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      t += 4;
+      while (t >= k.T) {
+        t -= k.T;
+        ++b;
       }
     }
   };
@@ -2767,15 +2771,19 @@ __device__ __forceinline__ void sens_bwd_cmp_rows(const SensBK& k, const float4 
         na[i] = make_float2(k.dsn[ix], k.dsd[ix]);
       }
     }
+    // x rows r0 + wv + 4i, wave-uniform: one division per chunk, then steps
+    // of four rows
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int dg = db + (int)(threadIdx.x & 63);
+    int b = (r0 + wv) / k.T, t = r0 + wv - b * k.T;
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      const int e = threadIdx.x + i * 256;
-      const int rr = e >> 6, dd = e & 63;
-      const int row = r0 + rr, dg = db + dd;
       nx[i] = 0.f;
-      if (rr < cnt && dg < k.D) {
-        const int b = row / k.T, t = row - b * k.T;
-        nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      if (wv + 4 * i < cnt && dg < k.D) nx[i] = k.x[b * k.xs.b + t * k.xs.t + dg * k.xs.c];
+      t += 4;
+      while (t >= k.T) {
+        t -= k.T;
+        ++b;
       }
     }
   };
