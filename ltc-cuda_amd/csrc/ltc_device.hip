@@ -1385,7 +1385,8 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 // g = lane >> 4 holds the compacted entries g, g + 4, ... of column j (the
 // rows i whose synapse (i -> j) has a nonzero weight, ascending), with their
 // operands and LDS row offsets in registers. The wave runs NS slots, its
-// fullest lane's count rounded up to even, in a loop unrolled for that NS.
+// fullest lane's count (at Hp = 128 as row128_slots rounds it), in a loop
+// unrolled for that NS.
 // A column's sums over its four row groups finish inside the wave
 // (group_sum4), so an unfold has one LDS round trip: the new state goes to a
 // double-buffered LDS row and, after the unfold's one barrier, every lane
@@ -1396,6 +1397,16 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
 // groups per column (group_sum4); HP = 64 runs 4 waves of 16 slots per lane,
 // HP = 128 8 waves of 32 (two waves per SIMD, so each wave has 256
 // registers for its slots' operands).
+// Slot count a single-row Hp = 128 wave runs for its fullest lane's nslot:
+// multiples of four up to 12 and from 28, even counts between (where the
+// counts of half-dense masks fall), so a wave runs at most one padding slot
+// there.
+__device__ __forceinline__ int row128_slots(int nslot) {
+  if (nslot <= 12) return nslot <= 4 ? 4 : (nslot <= 8 ? 8 : 12);
+  if (nslot <= 28) return (nslot + 1) & ~1;
+  return 32;
+}
+
 template <int HP>
 struct RowWave {
   static_assert(HP == 64 || HP == 128, "single-row wave layouts");
@@ -1553,29 +1564,24 @@ __global__ __launch_bounds__(RowWave<HP>::kThreads) void ode_fwd_row_wave_kernel
   const float v = (k.state0 != nullptr && col) ? k.state0[(long long)blockIdx.x * H + j] : 0.f;
   if (lead) vsh[j] = v;
   if constexpr (HP == 64) {
-    switch ((nslot + 1) >> 1) {
-      case 0:
-      case 1: fwd_row_wave_loop<2, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 2: fwd_row_wave_loop<4, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 3: fwd_row_wave_loop<6, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 4: fwd_row_wave_loop<8, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 5: fwd_row_wave_loop<10, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 6: fwd_row_wave_loop<12, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 7: fwd_row_wave_loop<14, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+    switch (nslot) {
+#define LTC_FRW(N) \
+  case N: fwd_row_wave_loop<N, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      case 0: LTC_FRW(1) LTC_FRW(2) LTC_FRW(3) LTC_FRW(4) LTC_FRW(5) LTC_FRW(6) LTC_FRW(7)
+      LTC_FRW(8) LTC_FRW(9) LTC_FRW(10) LTC_FRW(11) LTC_FRW(12) LTC_FRW(13) LTC_FRW(14)
+      LTC_FRW(15)
       default: fwd_row_wave_loop<16, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+#undef LTC_FRW
     }
   } else {
-    // slots rounded up to a multiple of four (padding slots add zeros)
-    switch ((nslot + 3) >> 2) {
-      case 0:
-      case 1: fwd_row_wave_loop<4, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 2: fwd_row_wave_loop<8, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 3: fwd_row_wave_loop<12, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 4: fwd_row_wave_loop<16, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 5: fwd_row_wave_loop<20, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 6: fwd_row_wave_loop<24, HP>(k, preg, ix, vsh, j, lead, col, v); break;
-      case 7: fwd_row_wave_loop<28, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+    // padding slots add zeros
+    switch (row128_slots(nslot)) {
+#define LTC_FRW(N) \
+  case N: fwd_row_wave_loop<N, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+      LTC_FRW(4) LTC_FRW(8) LTC_FRW(12) LTC_FRW(14) LTC_FRW(16) LTC_FRW(18) LTC_FRW(20)
+      LTC_FRW(22) LTC_FRW(24) LTC_FRW(26) LTC_FRW(28)
       default: fwd_row_wave_loop<32, HP>(k, preg, ix, vsh, j, lead, col, v); break;
+#undef LTC_FRW
     }
   }
 }
@@ -1635,8 +1641,8 @@ __device__ __forceinline__ void chain_stage(const BwdK& k, int b0, long long nhi
 // holds the compacted entries jg, jg + 8, ... of column i (its postsynaptic
 // j: every real synapse on the boundary, those with a nonzero mask entry on
 // the module path), with their operands, four gradient sums and LDS offsets
-// in registers. The wave runs NS slots, its fullest lane's count rounded up
-// to even, in a loop unrolled for that NS. dL/dv_i finishes inside the wave
+// in registers. The wave runs NS slots, its fullest lane's count, in a loop
+// unrolled for that NS. dL/dv_i finishes inside the wave
 // (group_sum8), so an unfold has one LDS round trip: alpha/beta of every
 // column go to a double-buffered LDS row and, after the unfold's one barrier,
 // every lane reads its slots' pairs back. The unfold loop runs in pairs so
@@ -1785,11 +1791,15 @@ __device__ __forceinline__ void bwd_row_wave_body(const BwdK& k) {
     gacc[rr] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (k.T == 0) return;
-  switch ((nslot + 1) >> 1) {
+  switch (nslot) {
     case 0:
-    case 1: bwd_row_wave_loop<2, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
-    case 2: bwd_row_wave_loop<4, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
-    case 3: bwd_row_wave_loop<6, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 1: bwd_row_wave_loop<1, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 2: bwd_row_wave_loop<2, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 3: bwd_row_wave_loop<3, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 4: bwd_row_wave_loop<4, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 5: bwd_row_wave_loop<5, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 6: bwd_row_wave_loop<6, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
+    case 7: bwd_row_wave_loop<7, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
     default: bwd_row_wave_loop<8, FULL>(k, preg, jx, gacc, abs_, i, lead); break;
   }
   // Recurrent-gradient partials through four padded [64][65] LDS planes at
@@ -2299,17 +2309,14 @@ __global__ __launch_bounds__(512) void ode_bwd_row_wave128_kernel(BwdK k, RecC r
     jx[rr / 2] = (unsigned)(k.cidx[a] * 8) | ((unsigned)(k.cidx[a + HP] * 8) << 16);
   }
   if (k.T == 0) return;
-  // slots rounded up to a multiple of four (padding slots add zeros)
-  switch ((nslot + 3) >> 2) {
-    case 0:
-    case 1: bwd_row_wave128_loop<4, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 2: bwd_row_wave128_loop<8, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 3: bwd_row_wave128_loop<12, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 4: bwd_row_wave128_loop<16, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 5: bwd_row_wave128_loop<20, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 6: bwd_row_wave128_loop<24, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
-    case 7: bwd_row_wave128_loop<28, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+  // padding slots add zeros
+  switch (row128_slots(nslot)) {
+#define LTC_BRW(N) \
+  case N: bwd_row_wave128_loop<N, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+    LTC_BRW(4) LTC_BRW(8) LTC_BRW(12) LTC_BRW(14) LTC_BRW(16) LTC_BRW(18) LTC_BRW(20)
+    LTC_BRW(22) LTC_BRW(24) LTC_BRW(26) LTC_BRW(28)
     default: bwd_row_wave128_loop<32, FULL>(k, preg, jx, abs_, i, lead, rc.sw); break;
+#undef LTC_BRW
   }
 }
 
