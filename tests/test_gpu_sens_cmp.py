@@ -1,10 +1,14 @@
-"""The sensory launch over the compacted sensory image.
+"""The sensory launches over the unmasked sensory synapses only.
 
 When the sensory sums are not formed in the prep launch, the forward
 (ltc_module_forward, and ltc_full_forward behind the eval-mode module) builds,
 per 64-input chunk and neuron, the list of inputs whose sensory weight is
-nonzero (in the prep launch) and the sensory launch walks only those. These
-tests set the sensory mask so that the lists take every edge the layout has:
+nonzero (in the prep launch) and the sensory launch walks only those. The
+module backward of these shapes runs the compacted sensory backward
+(sens_bwd_cmp_kernel: each lane holds one input's unmasked synapses of an
+8-neuron group; the plan asserts that neither fused row backward takes it
+over). These tests set the sensory mask so that the lists take every edge
+the layout has:
 a neuron with no input at all, a neuron with every input, a chunk that is
 full for one neuron and empty for the next, a ragged last chunk (D not a
 multiple of 64) and a single input, on both thread layouts of the launch (four
@@ -30,6 +34,7 @@ CASES = [
     (40, 8, 130, 72, True),
     (2, 3, 200, 40, False),   # few rows: the inputs split over the waves
     (300, 2, 1, 8, False),    # one input
+    (300, 7, 130, 72, False), # 33 rows per backward block: a full 32-row chunk, then one
 ]
 
 
@@ -50,6 +55,10 @@ def test_compacted_sensory_forward_matches_oracle(case):
     B, T, D, H, strided = case
     plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
     assert plan["module_sens_in_prep"] == 0, plan
+    # the backward's sensory gradients come from sens_bwd_cmp_kernel: no fused
+    # row backward, and no Hp = 128 sensory companions (those need Dp <= 128)
+    assert plan["module_row_bwd_fused"] == 0, plan
+    assert plan["module_row128_rec_fused"] == 0 or plan["Dp"] > 128, plan
     m = _perturbed_module(D, H, seed=5 * D + H).to(DEV)
     with torch.no_grad():
         m.sensory_sparsity_mask.copy_(_edge_mask(D, H, seed=D + H).to(DEV))
