@@ -4689,6 +4689,10 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   if (T == 0) return;
   auto pden_at = [&](long long m) { return pden + (m & 1) * NB * Hp; };
   auto pv_at = [&](long long m) { return pv + (m % 3) * NB * Hp; };
+  // v slot r (an unfold index mod 3, kept by the loop instead of divided)
+  auto pv_slot = [&](int r) { return pv + r * NB * Hp; };
+  auto mod3_next = [](int r) { return r == 2 ? 0 : r + 1; };
+  auto mod3_prev = [](int r) { return r == 0 ? 2 : r - 1; };
 
   float4 preg[RCP];
   int nmine, nslot, sks, so;
@@ -4795,9 +4799,11 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   }
   bool pend = false;  // owners: their group's finish is due
   long long pn = 0;
+  int pn3 = 0, pt = 0, pu = 0;  // pn mod 3, its step and unfold within the step
   float gnext = 0.f;
+  // step t, unfold u within it and n mod 3, stepped with n
+  int t = T - 1, u = U - 1, n3 = (int)(n_last % 3);
   for (long long n = n_last; n >= 0; --n) {
-    const int t = (int)(n / U), u = (int)(n - (long long)t * U);
 #pragma unroll
     for (int gi = 0; gi < 2; ++gi) {
       // (e) the owners of the previous phase's group: dL/dv^{pn}, published
@@ -4805,7 +4811,6 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       bool own_next = false;
       if (pend) {
         pend = false;
-        const int pt = (int)(pn / U), pu = (int)(pn - (long long)pt * U);
         const float* rg = red + og * KS * HB * JW;
         const float s = ks_sum_wide(rg + (bo - og * HB) * JW + o, HB * JW, KS);
         g = c < H ? fmaf(kNegLn2, s, gdir) : 0.f;
@@ -4834,7 +4839,7 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       unsigned long long* gslot = xbase + (long long)(gtag & 1) * CP * PER;
       unsigned long long w[XW];
       float cvi[HB], acc[HB];
-      const float* vn = pv_at(n);
+      const float* vn = pv_slot(n3);
 #pragma unroll
       for (int b = 0; b < HB; ++b) {
         cvi[b] = b0 + gi * HB + b < B ? vn[(gi * HB + b) * Hp + sc] : 0.f;
@@ -4849,7 +4854,12 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
               w[x] = xch_get(gslot + gm[x] * PER + (gg * HB + gr[x]) * JW + (gcl[x] - gm[x] * JW));
           // group 1's phases issue the prefetch of unfold n - 2, after the
           // word loads
-          if (gi == 1 && n >= 2) prefetch(n - 2);
+          if (gi == 1 && n >= 2) {
+            // 1/den of unfold n - 2, v of slot n - 2 (n - 2 = n + 1 mod 3)
+            rows_to_lds_fixed<NB, HPC, 512>(k.densave + (n - 2) * BHp, b0, B, pden_at(n), tid);
+            rows_to_lds_fixed<NB, HPC, 512>(k.vsave + (n - 2) * BHp, b0, B,
+                                            pv_slot(mod3_next(n3)), tid);
+          }
         }
         if (4 * q < nslot) {
           const int4 of = slot_tab[q * nthr + tid];
@@ -4878,7 +4888,7 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
         gave_up = 1;  // a budget of 0: give up at the first wait, as xch_gather does
       } else if (need) {
         const float* dn = pden_at(am);
-        const float* vk1 = pv_at(am + 1);
+        const float* vk1 = pv_slot(gi == 1 ? n3 : mod3_next(n3));  // slot am + 1 = gtag
 #pragma unroll
         for (int x = 0; x < XW; ++x) {
           if (!gth[x]) continue;
@@ -4908,8 +4918,8 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
           ab[col * ABS + b] = make_float2(al, be);
         }
       }
-      if (own_next) own_ab(pden_at(pn - 1)[bo * Hp + c], pv_at(pn - 1)[bo * Hp + c],
-                           pv_at(pn)[bo * Hp + c]);
+      if (own_next) own_ab(pden_at(pn - 1)[bo * Hp + c], pv_slot(mod3_prev(pn3))[bo * Hp + c],
+                           pv_slot(pn3)[bo * Hp + c]);
       // the prefetch issued in the previous (group 1) phase, visible to
       // every wave after this barrier
       if (gi == 0) wait_vm();
@@ -4922,8 +4932,16 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       }
       if (owner && og == gi) {
         pn = n;
+        pn3 = n3;
+        pt = t;
+        pu = u;
         pend = true;
       }
+    }
+    n3 = mod3_prev(n3);
+    if (--u < 0) {
+      u = U - 1;
+      --t;
     }
   }
   // group 1's finish of unfold 0 (nothing is published at unfold 0)
