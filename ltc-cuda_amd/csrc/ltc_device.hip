@@ -4039,6 +4039,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
   bool pend = false;           // owners: a finish of their group is due
   float2 pnq = make_float2(0.f, 0.f);
   long long pn = 0;
+  int pt = 0, pu = 0;  // pn's step and unfold within the step
   auto load_sens = [&](int t) {
     snr = sdr = 0.f;
     if (live) {
@@ -4050,7 +4051,7 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
   // The owners' finish of unfold pn: v^{pn+1} of (row bo, column c) from the
   // reduced sums pnq; publish (when a partner needs it), saved state, output.
   auto finish = [&](bool publish) {
-    const int t = (int)(pn / U), u = (int)(pn - (long long)t * U);
+    const int t = pt, u = pu;
     const float vold = vs[c * NB + bo];
     const float den = CG + (pnq.y + sdr) + k.eps;
     const float num = C * vold + GL + (pnq.x + snr);
@@ -4073,7 +4074,15 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
     }
   };
   if (owner && T > 0) load_sens(0);
-  for (long long n = 0; n < N; ++n) {
+  // step t and unfold u within it, stepped with n
+  int t = 0, u = 0;
+  auto step = [&] {
+    if (++u == U) {
+      u = 0;
+      ++t;
+    }
+  };
+  for (long long n = 0; n < N; ++n, step()) {
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       if (pend) {
@@ -4131,6 +4140,8 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
       if (owner && og == g) {
         pnq = ks_sum_wide(rg + (bo - g * HB) * kClW + o, HB * kClW, KS);
         pn = n;
+        pt = t;
+        pu = u;
         pend = true;
       }
     }
