@@ -4850,6 +4850,11 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       unsigned long long* gslot = xbase + (long long)(gtag & 1) * CP * PER;
       unsigned long long w[XW];
       float cvi[HB], acc[HB];
+      // The slot count, opaque to the compiler here: otherwise it keeps the
+      // slot branches' conditions as lane masks across the loop, which spill
+      // and are reloaded every phase.
+      int nsl = nslot;
+      asm volatile("" : "+s"(nsl));
       const float* vn = pv_slot(n3);
 #pragma unroll
       for (int b = 0; b < HB; ++b) {
@@ -4872,12 +4877,12 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
                                             pv_slot(mod3_next(n3)), tid);
           }
         }
-        if (4 * q < nslot) {
+        if (4 * q < nsl) {
           const int4 of = slot_tab[q * nthr + tid];
           const int off[4] = {of.x, of.y, of.z, of.w};
 #pragma unroll
           for (int h = 0; h < 4; h += 2) {
-            if (4 * q + h < nslot) {
+            if (4 * q + h < nsl) {
 #pragma unroll
               for (int i = 0; i < 2; ++i) {
                 const int rr = 4 * q + h + i;
