@@ -4802,7 +4802,13 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
 #pragma unroll
   for (int x = 0; x < XW; ++x) {
     const int e = tid + x * nthr;
-    gth[x] = e < (CP - 1) * PERG;
+    // With two or more rows per group the word count (CP - 1) * PERG is a
+    // multiple of 64, so a wave gathers all its words or none: a scalar
+    // branch instead of a lane mask.
+    if constexpr (HB >= 2)
+      gth[x] = __builtin_amdgcn_readfirstlane(e) < (CP - 1) * PERG;
+    else
+      gth[x] = e < (CP - 1) * PERG;
     const int q = e / PERG, r = e - q * PERG;
     gm[x] = q + (q >= p ? 1 : 0);
     gr[x] = r / JW;
