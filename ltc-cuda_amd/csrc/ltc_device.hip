@@ -4101,13 +4101,17 @@ __global__ __launch_bounds__(1024) void ode_fwd_cl2_kernel(FwdCK k) {
       float na[HB], qa[HB];
 #pragma unroll
       for (int b = 0; b < HB; ++b) na[b] = qa[b] = 0.f;
+      // the slot count, opaque here so that the slot branches' conditions are
+      // not held as lane masks across the loop
+      int nsl = nslot;
+      asm volatile("" : "+s"(nsl));
 #pragma unroll
       for (int q = 0; q < RCP / 4; ++q) {
         if (q == RCP / 8 && need && gth) w = xch_get(gw);
-        if (4 * q < nslot) {
+        if (4 * q < nsl) {
           const int4 of = slot_tab[q * nthr + tid];
           fwd_synapses_cmp<HB>(preg + 4 * q, vs + g * HB, of.x, of.y, na, qa);
-          if (4 * q + 2 < nslot)
+          if (4 * q + 2 < nsl)
             fwd_synapses_cmp<HB>(preg + 4 * q + 2, vs + g * HB, of.z, of.w, na, qa);
         }
       }
