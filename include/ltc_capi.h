@@ -315,10 +315,12 @@ int ltc_ode_unfold_bwd(const float* v_buffer, const float* w_pos, const float* w
  * (Hp = 128: no separate recurrent-gradient launch), then the launches of
  * the forward and of the chain ODE kernel per call: 1, or at Hp > 1024 with
  * more rows than one launch of at most one workgroup per CU holds, one
- * launch per NCL * NB rows. Returns the number of values written, or -1 for
- * invalid sizes. The plan depends on the current device's CU count.
+ * launch per NCL * NB rows, then 1 when the module forward's sensory launch
+ * walks one list per neuron over all of D (64 < D <= 256 with many rows)
+ * instead of per 64-input chunk. Returns the number of values written, or
+ * -1 for invalid sizes. The plan depends on the current device's CU count.
  */
-#define LTC_PLAN_FIELDS 27
+#define LTC_PLAN_FIELDS 28
 int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out, int n);
 
 /*

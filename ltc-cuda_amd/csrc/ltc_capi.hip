@@ -409,6 +409,7 @@ void carve_sens_cmp(const ltc::Plan& p, Carver& c, ltc::Prepped& pp) {
   pp.sF = c.take<float4>(n);
   pp.sFi = c.take<int>(n);
   pp.sFn = c.take<int>((long long)(p.Dp / 64) * p.Hp);
+  pp.sFfull = ltc::sens_full_list(p) ? 1 : 0;
 }
 
 // sens: with the compacted sensory image (every forward that runs the
@@ -1023,6 +1024,7 @@ int ltc_module_forward(const float* x, long long sxb, long long sxt, long long s
   pp.sF = sens_in_prep ? nullptr : wfw.pp.sF;
   pp.sFi = sens_in_prep ? nullptr : wfw.pp.sFi;
   pp.sFn = sens_in_prep ? nullptr : wfw.pp.sFn;
+  pp.sFfull = wfw.pp.sFfull;
   // Without saving, nothing but the sensory launch reads the normalised rows:
   // when they fit one 64-input chunk, it normalises them itself.
   const bool ln_in_sens = !save_intermediates && !sens_in_prep && ltc::sens_fwd_ln_fusable(p);
@@ -1584,7 +1586,8 @@ int ltc_launch_plan(int B, int T, int D, int H, int ode_unfolds, long long* out,
       p.FUSE ? 1 : 0, p.KSB, p.RCB, colsb * p.KSB, p.CP, p.NCL, p.CPB, nbb,
       p.CP > 0 ? (long long)p.NCLB * p.CPB : (B + p.NB - 1) / p.NB,
       ltc::cmp_fwd(p) ? 1 : 0, ltc::cmp_bwd(p) ? 1 : 0, ltc::prep_sens_fused(p) ? 1 : 0,
-      ltc::row_bwd_fused(p) ? 1 : 0, ltc::row128_rec_fused(p) ? 1 : 0, p.LCH, p.LCHB};
+      ltc::row_bwd_fused(p) ? 1 : 0, ltc::row128_rec_fused(p) ? 1 : 0, p.LCH, p.LCHB,
+      ltc::sens_full_list(p) ? 1 : 0};
   const int m = n < LTC_PLAN_FIELDS ? n : LTC_PLAN_FIELDS;
   for (int i = 0; i < m; ++i) out[i] = v[i];
   return m;

@@ -318,7 +318,7 @@ __device__ __forceinline__ void compact_column(int col, int nrows, int stride, i
 __host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, int Dp, bool fwd, bool bwd,
                                             bool sens) {
   return ((fwd && pp.cF != nullptr) ? Hp : 0) + ((bwd && pp.cB != nullptr) ? Hp : 0) +
-         ((sens && pp.sF != nullptr) ? (Dp / 64) * Hp : 0);
+         ((sens && pp.sF != nullptr) ? (pp.sFfull ? Hp : (Dp / 64) * Hp) : 0);
 }
 
 // Compacted sensory forward column (one wave per 64-input chunk c and neuron
@@ -327,6 +327,17 @@ __host__ __device__ inline int cmp_columns(const Prepped& pp, int Hp, int Dp, bo
 template <class Op>
 __device__ __forceinline__ void compact_sens_column(const Prepped& pp, int col, int Hp, int D,
                                                     int H, int lane, Op op) {
+  if (pp.sFfull) {
+    // one list per neuron h = col over all of D (Dp rows)
+    const int Dp = (D + 63) & ~63;
+    compact_column(col, Dp, Hp, 1, lane, pp.sF, pp.sFi, pp.sFn, [&](int d, float4& v, bool& act) {
+      if (d < D && col < H) {
+        v = op((long long)d * H + col);
+        act = v.w != 0.f;
+      }
+    });
+    return;
+  }
   const int c = col / Hp, h = col - c * Hp;
   const long long cb = (long long)c * 64 * Hp;
   compact_column(h, 64, Hp, 1, lane, pp.sF + cb, pp.sFi + cb, pp.sFn + (long long)c * Hp,
@@ -389,7 +400,7 @@ __global__ __launch_bounds__(256) void prep_kernel(RawParams rp, Prepped pp, int
       }
       col -= Hp;
     }
-    if ((segs & kPrepSens) && pp.sF != nullptr && col < (Dp / 64) * Hp) {
+    if ((segs & kPrepSens) && pp.sF != nullptr && col < (pp.sFfull ? Hp : (Dp / 64) * Hp)) {
       compact_sens_column(pp, col, Hp, D, H, lane, [&](long long e) {
         const float Ss = rp.s_sigma[e], Ms = rp.s_mu[e], Ws = rp.s_wpos[e];
         return make_float4(-Ss * kLog2e, Ss * Ms * kLog2e, Ws * rp.s_erev[e], Ws);
@@ -2613,6 +2624,115 @@ __global__ __launch_bounds__(256) void rec_grad_kernel(RecGK k) {
 }
 
 // ---------------------------------------------------------------------------
+// Sensory forward over the compacted image as one list per neuron over all of
+// D (sFfull; sens_full_list). sens_fwd_cmp_kernel's layout with four row
+// groups (lane -> neuron h, wave w -> rows w*RPW ...), but the block's rows of
+// x are staged whole (Dp inputs, one barrier) and each lane walks its neuron's
+// entries over all of D. A wave then runs its fullest neuron's total count,
+// rounded up to four, instead of the fullest count of every 64-input chunk
+// rounded up to four: at half-dense masks about 148 slots against 4 x 44.
+// The entries come in ascending input order, as over the chunks in turn, so
+// the sums take the same terms in the same order as in sens_fwd_cmp_kernel
+// (padding slots add exact zeros there between chunks, here at the end).
+// ---------------------------------------------------------------------------
+template <int RPW>
+__global__ __launch_bounds__(256) void sens_fwd_full_kernel(const float* __restrict__ x,
+                                                            Strides3 xs, int T, int D, int Dp,
+                                                            int BT, int Hp,
+                                                            const float4* __restrict__ sF,
+                                                            const int* __restrict__ sFi,
+                                                            const int* __restrict__ sFn,
+                                                            float* __restrict__ sn,
+                                                            float* __restrict__ sd) {
+  constexpr int ROWS = 4 * RPW;
+  constexpr int XLD = ROWS + 4;  // padded staged row, 16-byte aligned
+  extern __shared__ float4 lds4[];
+  float* xsh = reinterpret_cast<float*>(lds4);  // [Dp][XLD]
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = blockIdx.x * 64 + lane;
+  const int row0 = blockIdx.y * ROWS;
+  const int rw = w * RPW;
+  // Stage x: lane l of wave w loads input d0 + l of rows w, w + 4, ...
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = wu + 4 * i, row = row0 + r;
+    const float* xr = nullptr;
+    if (row < BT) {
+      const int b = row / T, t = row - b * T;
+      xr = x + b * xs.b + t * xs.t;
+    }
+    for (int d0 = 0; d0 < Dp; d0 += 64) {
+      const int d = d0 + lane;
+      xsh[d * XLD + r] = (xr != nullptr && d < D) ? xr[(long long)d * xs.c] : 0.f;
+    }
+  }
+  float an[RPW], ad[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) an[r] = ad[r] = 0.f;
+  const int nsw = (wave_max(sFn[h]) + 3) & ~3;
+  __syncthreads();
+  if (nsw > 0) {
+    const float4* pcol = sF + h;
+    const int* icol = sFi + h;
+    float4 pc[4], pn[4];
+    int dc[4], dn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pc[i] = pcol[(long long)i * Hp];
+      dc[i] = icol[(long long)i * Hp];
+    }
+    for (int s = 0; s < nsw; s += 4) {
+      // the next group's operands travel while this one is evaluated (the
+      // last group reloads itself)
+      const int sn4 = s + 4 < nsw ? s + 4 : s;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pn[i] = pcol[(long long)(sn4 + i) * Hp];
+        dn[i] = icol[(long long)(sn4 + i) * Hp];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float* xr = xsh + dc[i] * XLD + rw;
+        float xq[RPW];
+        if constexpr (RPW % 4 == 0) {
+#pragma unroll
+          for (int r = 0; r < RPW; r += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(xr + r);
+            xq[r] = q4.x;
+            xq[r + 1] = q4.y;
+            xq[r + 2] = q4.z;
+            xq[r + 3] = q4.w;
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < RPW; ++r) xq[r] = xr[r];
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const float a = gate(fmaf(pc[i].x, xq[r], pc[i].y));
+          an[r] = fmaf(a, pc[i].z, an[r]);
+          ad[r] = fmaf(a, pc[i].w, ad[r]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pc[i] = pn[i];
+        dc[i] = dn[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int row = row0 + rw + r;
+    if (row < BT) {
+      sn[(long long)row * Hp + h] = an[r];
+      sd[(long long)row * Hp + h] = ad[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Sensory backward over all (b,t) rows.
 // grid (Dp/64, Hp/32, NRC), block 256: lane -> d, wave w -> 8 neurons h.
 // With A = dL/dsn, Bq = dL/dsd, gamma = A*Es + Bq, a2 = a(1-a):
@@ -3304,7 +3424,7 @@ __global__ __launch_bounds__(FS ? kPrepSensThreads : 256) void prep_leaf_kernel(
       }
       col -= Hp;
     }
-    if (pp.sF != nullptr && col < (Dp / 64) * Hp) {
+    if (pp.sF != nullptr && col < (pp.sFfull ? Hp : (Dp / 64) * Hp)) {
       compact_sens_column(pp, col, Hp, D, H, lane, [&](long long e) {
         const float Ss = lp.s_sigma[e], Ms = lp.s_mu[e];
         const float Ws = softplus_t(lp.s_w[e]) * lp.s_mask[e];
@@ -5239,6 +5359,21 @@ hipError_t launch_sens_fwd(const Plan& p, const float* x, Strides3 xs, const Pre
                          p.Hp, pp.sensF, sn, sd);                                               \
   } while (0)
   if (pp.sF != nullptr && (pp.sFi == nullptr || pp.sFn == nullptr)) return hipErrorInvalidValue;
+  if (pp.sF != nullptr && pp.sFfull) {
+    // one list per neuron over all of D; the block's rows of x staged whole
+    if (split_d || p.Dp > 256) return hipErrorInvalidValue;
+#define LTC_SENSF(R)                                                                          \
+  LTC_LAUNCH((sens_fwd_full_kernel<R>), grid, block, (size_t)p.Dp * (4 * R + 4) * 4, s, x, xs, \
+             p.T, p.D, p.Dp, BT, p.Hp, pp.sF, pp.sFi, pp.sFn, sn, sd)
+    switch (rpw) {
+      case 8: LTC_SENSF(8); break;
+      case 4: LTC_SENSF(4); break;
+      case 2: LTC_SENSF(2); break;
+      default: LTC_SENSF(1); break;
+    }
+#undef LTC_SENSF
+    return hipGetLastError();
+  }
   if (split_d) {
     switch (rpw) {
       case 8: LTC_SENS(8, 4); break;

@@ -126,6 +126,9 @@ struct Prepped {
   float4* sF;
   int* sFi;
   int* sFn;
+  // 1: the same image as one list per neuron over all of D instead
+  // ([slot][Hp] operands and input indices, [Hp] counts; sens_full_list)
+  int sFfull;
 };
 // Chunks (and slots per chunk) of a compacted image column at Hp = 256.
 constexpr int kCmpChunks = 16;
@@ -233,6 +236,13 @@ inline SensGeom sens_fwd_geom(const Plan& p) {
   int rpw = 8;
   while (rpw > 1 && hb * ((BT + rows_of * rpw - 1) / (rows_of * rpw)) < 1024) rpw >>= 1;
   return {rpw, split_d};
+}
+// The compacted sensory image as one list per neuron over all of D (for
+// sens_fwd_full_kernel, which stages the block's rows of x whole): with four
+// row groups per workgroup and 64 < Dp <= 256. With Dp = 64 the per-chunk
+// image is already one list per neuron.
+inline bool sens_full_list(const Plan& p) {
+  return p.Dp > 64 && p.Dp <= 256 && !sens_fwd_geom(p).split_d;
 }
 // The module forward's sensory sums inside the prep launch: when a block
 // per (row, 64 neurons) fits the chip at once (at most 256 of them) and a

@@ -75,7 +75,7 @@ class CApi:
                    "NRC", "ode_workgroups", "fuse", "KSB", "RCB",
                    "threads_bwd", "CP", "NCL", "CPB", "NBB", "ode_workgroups_bwd",
                    "cmp_fwd", "cmp_bwd", "module_sens_in_prep", "module_row_bwd_fused",
-                   "module_row128_rec_fused", "launches_fwd", "launches_bwd")
+                   "module_row128_rec_fused", "launches_fwd", "launches_bwd", "sens_full_list")
 
     def __init__(self, path: str = LIB_PATH):
         self.path = path

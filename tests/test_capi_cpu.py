@@ -421,6 +421,24 @@ def test_sensory_backward_row_chunks(capi, shape, nrc):
     assert p["NRC"] * bpc >= min(6 * 256, bpc * min(64, (B * T + 7) // 8))
 
 
+@pytest.mark.parametrize("shape,full", [
+    ((256, 64, 256, 256, 6), 1),  # C3: four 64-input chunks, many rows
+    ((300, 7, 130, 72, 6), 1),    # three chunks, ragged
+    ((40, 8, 130, 72, 6), 0),     # few rows: the waves split D instead
+    ((4096, 4, 64, 64, 6), 0),    # C5: one chunk is already one list per neuron
+    ((128, 32, 512, 512, 6), 0),  # C4: D past the staged rows' LDS
+])
+def test_sensory_forward_full_lists(capi, shape, full):
+    """The module forward's sensory launch walks one list per neuron over all
+    of D (the block's rows of x staged whole) when 64 < Dp <= 256 and the
+    plan has four row groups per workgroup; otherwise the per-chunk lists."""
+    B, T, D, H, U = shape
+    p = capi.plan(B, T, D, H, U)
+    assert p["sens_full_list"] == full
+    if full:
+        assert 64 < p["Dp"] <= 256
+
+
 @pytest.mark.parametrize("B,nb,nbb", [(16, 1, 1), (48, 1, 2), (100, 2, 4), (200, 4, 8)])
 def test_two_group_cluster_plans(capi, B, nb, nbb):
     """Rows per cluster at H = 256 (forward NB, chain NBB; the two-group kernels

@@ -34,7 +34,8 @@ CASES = [
     (40, 8, 130, 72, True),
     (2, 3, 200, 40, False),   # few rows: the inputs split over the waves
     (300, 2, 1, 8, False),    # one input
-    (300, 7, 130, 72, False), # 33 rows per backward block: a full 32-row chunk, then one
+    (300, 7, 130, 72, False), # 33 rows per backward block: a full 32-row chunk, then one;
+                              # the forward walks one list per neuron over all of D
 ]
 
 
@@ -55,6 +56,7 @@ def test_compacted_sensory_forward_matches_oracle(case):
     B, T, D, H, strided = case
     plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
     assert plan["module_sens_in_prep"] == 0, plan
+    assert plan["sens_full_list"] == (1 if (B, T) == (300, 7) else 0), plan
     # the backward's sensory gradients come from sens_bwd_cmp_kernel: no fused
     # row backward, and no Hp = 128 sensory companions (those need Dp <= 128)
     assert plan["module_row_bwd_fused"] == 0, plan
