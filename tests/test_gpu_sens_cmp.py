@@ -24,7 +24,7 @@ import pytest
 import torch
 
 import ltc_cuda
-from _gpu_common import DEV, _native, _oracle_module_grads, _perturbed_module  # noqa: F401
+from _gpu_common import DEV, O, _native, _oracle_module_grads, _perturbed_module  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -128,6 +128,47 @@ def test_compacted_sensory_forward_boundary_path_matches_oracle(shape):
     e_out = (out.cpu().double() - r_out).abs().max().item()
     e_h = (h.cpu().double() - r_h).abs().max().item()
     print(f"compacted sensory, boundary {shape}: out err {e_out:.2e} h err {e_h:.2e}", flush=True)
+    assert e_out <= 1e-3 and e_h <= 1e-3
+
+
+def _sens_rows_per_wave(B, T, Hp):
+    """Rows per wave of the sensory forward with four row groups per
+    workgroup: halved from 8 until the grid has at least 1024 workgroups."""
+    BT, hb, rpw = B * T, Hp // 64, 8
+    while rpw > 1 and hb * ((BT + 4 * rpw - 1) // (4 * rpw)) < 1024:
+        rpw //= 2
+    return rpw
+
+
+@pytest.mark.parametrize("shape,rpw", [((512, 8, 130, 72), 2), ((1024, 8, 130, 72), 4)],
+                         ids=lambda v: "B%dT%dD%dH%d" % v if isinstance(v, tuple) else "rpw%d" % v)
+def test_full_list_sensory_forward_rows_per_wave(shape, rpw):
+    """The per-neuron sensory forward (one list over all of D, the block's rows
+    of x staged whole in LDS) at 2 and 4 rows per wave; C3 runs 8 and the
+    (300, 7) case above 1. The no-grad forward and the training forward agree
+    bit for bit, and both match the float64 oracle (max-abs 1e-3)."""
+    B, T, D, H = shape
+    plan = ltc_cuda._cuda_module.capi.plan(B, T, D, H, 6)
+    assert plan["sens_full_list"] == 1 and plan["module_sens_in_prep"] == 0, plan
+    assert _sens_rows_per_wave(B, T, plan["Hp"]) == rpw
+    m = _perturbed_module(D, H, seed=7 * D + B).to(DEV)
+    with torch.no_grad():
+        m.sensory_sparsity_mask.copy_(_edge_mask(D, H, seed=D + B).to(DEV))
+    g = torch.Generator().manual_seed(B + D)
+    x = torch.randn(B, T, D, generator=g)
+    h0 = torch.randn(B, H, generator=g) * 0.2
+    xd, hd = x.to(DEV), h0.to(DEV)
+    with torch.no_grad():
+        a, (ha, _) = m(xd, (hd, hd))
+    b, (hb, _) = m(xd.clone().requires_grad_(True), (hd, hd))
+    assert torch.equal(a, b.detach()) and torch.equal(ha, hb.detach())
+    p = {k: v.detach().cpu().double() for k, v in m.state_dict().items()}
+    with torch.no_grad():
+        r_out, (r_h, _) = O.module_forward(p, x.double(), (h0.double(), h0.double()), dt=m.dt,
+                                           ode_unfolds=m.ode_unfolds, epsilon=m.epsilon)
+    e_out = (a.cpu().double() - r_out).abs().max().item()
+    e_h = (ha.cpu().double() - r_h).abs().max().item()
+    print(f"full-list sensory forward {shape} rpw {rpw}: out err {e_out:.2e} h err {e_h:.2e}", flush=True)
     assert e_out <= 1e-3 and e_h <= 1e-3
 
 
