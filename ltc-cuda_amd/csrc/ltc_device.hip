@@ -4407,6 +4407,35 @@ __device__ __forceinline__ void bwd_synapse_cmp(const float4 p, const float2* ab
   }
 }
 
+// bwd_synapse_cmp over operands (x, y, E, w x), w factored out of dL/darg:
+// dl = (alpha E + beta) a (1 - a) is dL/darg / w, so dL/dv_i takes dl (w x)
+// and the last two gradient sums (of dL/darg and dL/darg v_i) come out
+// divided by w, which the caller multiplies back once at the end. One
+// multiply per synapse-row fewer.
+template <int NB>
+__device__ __forceinline__ void bwd_synapse_cmpe(const float4 p, const float2* ab, int off,
+                                                 const float* vi, float* acc, float4& gacc) {
+  float2 c[NB];
+  const char* at = reinterpret_cast<const char*>(ab) + off;
+#pragma unroll
+  for (int b = 0; b < NB; b += 2) {
+    const float4 w = *reinterpret_cast<const float4*>(at + b * 8);
+    c[b] = make_float2(w.x, w.y);
+    c[b + 1] = make_float2(w.z, w.w);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float a = gate(fmaf(p.x, vi[b], p.y));
+    const float a2 = fmaf(-a, a, a);
+    const float dl = fmaf(c[b].x, p.z, c[b].y) * a2;
+    acc[b] = fmaf(dl, p.w, acc[b]);
+    gacc.x = fmaf(c[b].x, a, gacc.x);
+    gacc.y = fmaf(c[b].y, a, gacc.y);
+    gacc.z += dl;
+    gacc.w = fmaf(dl, vi[b], gacc.w);
+  }
+}
+
 // Cluster chain: member p forms dL/dv_i for its JW columns i (reduction over
 // every postsynaptic j) and publishes them; alpha_j/beta_j of the other
 // members' columns are then rebuilt from the published dL/dv_j and the saved
@@ -4845,7 +4874,10 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
       const long long a = (long long)(sks * RCP + rr) * Hp + p * JW + so;
-      preg[rr] = k.cimg[a];
+      // image operands (x, y, w E, w) -> (x, y, E, w x); an entry with
+      // w = 0 (a padding slot) contributes nothing either way
+      const float4 q = k.cimg[a];
+      preg[rr] = make_float4(q.x, q.y, q.w != 0.f ? q.z / q.w : 0.f, q.w * q.x);
       ix[rr] = k.cidx[a] * ABS * 8;
     }
 #pragma unroll
@@ -5016,7 +5048,7 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
 #pragma unroll
               for (int i = 0; i < 2; ++i) {
                 const int rr = 4 * q + h + i;
-                bwd_synapse_cmp<HB>(preg[rr], ab + gi * HB, off[h + i], cvi, acc, gacc[rr]);
+                bwd_synapse_cmpe<HB>(preg[rr], ab + gi * HB, off[h + i], cvi, acc, gacc[rr]);
                 asm volatile("" : "+v"(gacc[rr].x), "+v"(gacc[rr].y), "+v"(gacc[rr].z),
                              "+v"(gacc[rr].w));
               }
@@ -5112,14 +5144,21 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   // [cluster][4][i][j], as ode_bwd_cl_kernel writes it.
   const long long HH = (long long)Hp * Hp;
   float* out = k.rpart + (long long)(k.R0 / NB + cl) * 4 * HH + (long long)sc * Hp;
+  // The image entries are indexed again from a copy of sks the compiler
+  // cannot match with the preload's, so that it does not keep the preload's
+  // addresses (or every w) live across the loop.
+  int sks_end = sks;
+  asm volatile("" : "+v"(sks_end));
 #pragma unroll
   for (int rr = 0; rr < RCP; ++rr) {
     if (rr < nmine) {
-      const int j = k.cidx[(long long)(sks * RCP + rr) * Hp + sc];
+      const long long a = (long long)(sks_end * RCP + rr) * Hp + sc;
+      const int j = k.cidx[a];
+      const float w = k.cimg[a].w;  // the factor the last two sums left out
       out[j] = gacc[rr].x;
       out[HH + j] = gacc[rr].y;
-      out[2 * HH + j] = gacc[rr].z;
-      out[3 * HH + j] = gacc[rr].w;
+      out[2 * HH + j] = gacc[rr].z * w;
+      out[3 * HH + j] = gacc[rr].w * w;
     }
   }
 }
