@@ -4417,11 +4417,15 @@ __device__ __forceinline__ void bwd_synapse_cmpe(const float4 p, const float2* a
                                                  const float* vi, float* acc, float4& gacc) {
   float2 c[NB];
   const char* at = reinterpret_cast<const char*>(ab) + off;
+  if constexpr (NB % 2 == 0) {
 #pragma unroll
-  for (int b = 0; b < NB; b += 2) {
-    const float4 w = *reinterpret_cast<const float4*>(at + b * 8);
-    c[b] = make_float2(w.x, w.y);
-    c[b + 1] = make_float2(w.z, w.w);
+    for (int b = 0; b < NB; b += 2) {
+      const float4 w = *reinterpret_cast<const float4*>(at + b * 8);
+      c[b] = make_float2(w.x, w.y);
+      c[b + 1] = make_float2(w.z, w.w);
+    }
+  } else {
+    c[0] = *reinterpret_cast<const float2*>(at);
   }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -4822,7 +4826,8 @@ __global__ __launch_bounds__(FUSE ? 512 : 1024) void ode_bwd_cl_kernel(BwdCK k) 
 // ahead of use (after that phase's word loads, so the word waits do not wait
 // for them): 1/den of two unfolds and v of three slots. The four gradient
 // sums of each synapse take the rows in the same order as the one-group
-// kernel, so they are bitwise the same.
+// kernel; a slot's operands are (x, y, E, w x), w factored out of dL/darg
+// (bwd_synapse_cmpe), and its alpha/beta row offset stays in a register.
 template <int NB>
 __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   static_assert(NB == 2 || NB == 4 || NB == 8, "two groups of rows");
@@ -4837,7 +4842,9 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   float* red = reinterpret_cast<float*>(ab + ABS * Hp);         // [2][KS][HB][JW]
   float* pden = red + 2 * KS * HB * JW;                         // [2][NB][Hp] by unfold parity
   float* pv = pden + 2 * NB * Hp;                               // [3][NB][Hp] by slot mod 3
-  int4* slot_tab = reinterpret_cast<int4*>(pv + 3 * NB * Hp);   // [4][threads]
+  // [4][threads] int4 of the compacted kernels' slot table, of which this
+  // kernel only uses the space after it (balanced_lane's scratch)
+  int4* slot_tab = reinterpret_cast<int4*>(pv + 3 * NB * Hp);
   const int tid = threadIdx.x, nthr = blockDim.x;
   const int ks = tid / JW, o = tid % JW;
   int p, cl;
@@ -4859,6 +4866,7 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
   auto mod3_prev = [](int r) { return r == 0 ? 2 : r - 1; };
 
   float4 preg[RCP];
+  int ix[RCP];  // slot row offsets, in registers
   int nmine, nslot, sks, so;
   {
     int* perm = reinterpret_cast<int*>(slot_tab + (RCP / 4) * nthr);
@@ -4870,7 +4878,6 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
     const int cnt = k.ccnt[p * JW + so];
     nmine = cnt > sks ? (cnt - 1 - sks) / kCmpChunks + 1 : 0;
     nslot = wave_max(nmine);
-    int ix[RCP];
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
       const long long a = (long long)(sks * RCP + rr) * Hp + p * JW + so;
@@ -4880,9 +4887,6 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       preg[rr] = make_float4(q.x, q.y, q.w != 0.f ? q.z / q.w : 0.f, q.w * q.x);
       ix[rr] = k.cidx[a] * ABS * 8;
     }
-#pragma unroll
-    for (int q = 0; q < RCP / 4; ++q)
-      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
   }
   const int sc = p * JW + so;
   float4 gacc[RCP];
@@ -5040,8 +5044,7 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
           }
         }
         if (4 * q < nsl) {
-          const int4 of = slot_tab[q * nthr + tid];
-          const int off[4] = {of.x, of.y, of.z, of.w};
+          const int off[4] = {ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]};
 #pragma unroll
           for (int h = 0; h < 4; h += 2) {
             if (4 * q + h < nsl) {
