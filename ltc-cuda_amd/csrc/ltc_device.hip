@@ -5015,6 +5015,12 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       const long long am = gtag - 1;  // the unfold whose alpha/beta the words rebuild
       unsigned long long* gslot = xbase + (long long)(gtag & 1) * CP * PER;
       unsigned long long w[XW];
+      // 1/den and v^{am+1} of the gathered words' rows and columns, read
+      // from LDS when the word loads are issued, so that the rebuild after
+      // the poll does not wait for LDS
+      float rdn[XW], rvk[XW], odn = 0.f, ovk = 0.f, ovk1 = 0.f;
+      const float* dn = pden_at(am);
+      const float* vk1 = pv_slot(gi == 1 ? n3 : mod3_next(n3));  // slot am + 1 = gtag
       float cvi[HB], acc[HB];
       // The slot count, opaque to the compiler here: otherwise it keeps the
       // slot branches' conditions as lane masks across the loop, which spill
@@ -5034,6 +5040,21 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
           for (int x = 0; x < XW; ++x)
             if (need && gth[x])
               w[x] = xch_get(gslot + gm[x] * PER + (gg * HB + gr[x]) * JW + (gcl[x] - gm[x] * JW));
+#pragma unroll
+          for (int x = 0; x < XW; ++x) {
+            rdn[x] = rvk[x] = 0.f;
+            if (need && gth[x]) {
+              const int e = (gg * HB + gr[x]) * Hp + gcl[x];
+              rdn[x] = dn[e];
+              rvk[x] = vk1[e];
+            }
+          }
+          // the owners' own entry likewise
+          if (own_next) {
+            odn = pden_at(pn - 1)[bo * Hp + c];
+            ovk = pv_slot(mod3_prev(pn3))[bo * Hp + c];
+            ovk1 = pv_slot(pn3)[bo * Hp + c];
+          }
           // group 1's phases issue the prefetch of unfold n - 2, after the
           // word loads
           if (gi == 1 && n >= 2) {
@@ -5068,8 +5089,6 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
       if (k.spin <= 0) {
         gave_up = 1;  // a budget of 0: give up at the first wait, as xch_gather does
       } else if (need) {
-        const float* dn = pden_at(am);
-        const float* vk1 = pv_slot(gi == 1 ? n3 : mod3_next(n3));  // slot am + 1 = gtag
 #pragma unroll
         for (int x = 0; x < XW; ++x) {
           if (!gth[x]) continue;
@@ -5092,15 +5111,14 @@ __global__ __launch_bounds__(512) void ode_bwd_cl2_kernel(BwdCK k) {
           float al = 0.f, be = 0.f;
           if (b0 + b < B && col < H) {
             const float gv = __uint_as_float((unsigned)w[x]);
-            const float rden = dn[b * Hp + col];
+            const float rden = rdn[x];
             al = gv * rden;
-            be = -gv * vk1[b * Hp + col] * rden;
+            be = -gv * rvk[x] * rden;
           }
           ab[col * ABS + b] = make_float2(al, be);
         }
       }
-      if (own_next) own_ab(pden_at(pn - 1)[bo * Hp + c], pv_slot(mod3_prev(pn3))[bo * Hp + c],
-                           pv_slot(pn3)[bo * Hp + c]);
+      if (own_next) own_ab(odn, ovk, ovk1);
       // the prefetch issued in the previous (group 1) phase, visible to
       // every wave after this barrier
       if (gi == 0) wait_vm();
