@@ -881,8 +881,8 @@ __device__ __forceinline__ void fwd_synapses_cmp(const float4* p, const float* v
 // image (CMP): thread (o, ks) holds the entries ks, ks + KS, ... of column o,
 // the wave runs as many slots as its fullest lane (wave-uniform branches
 // around unused pairs), the state sits in LDS as [Hp][NB] so that a slot's NB
-// values are one read at a per-lane row, and the slot row offsets come from an
-// LDS table [RCP/4][threads] of int4.
+// values are one read at a per-lane row, and the slot row offsets stay in
+// registers (no table read before a slot pair's state reads).
 template <int NB, int RCP>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   constexpr int MO = ode_owned_rows(NB);
@@ -892,7 +892,9 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   const int RC = RCP > 0 ? RCP : k.RC;
   float* vs = reinterpret_cast<float*>(lds4);            // [NB][Hp] ([Hp][NB] with CMP)
   float2* red = reinterpret_cast<float2*>(vs + NB * Hp);  // [KS][NB][Hp]
-  int4* slot_tab = reinterpret_cast<int4*>(red + KS * NB * Hp);  // CMP: [RCP/4][threads]
+  // CMP: the compacted kernels' slot-table space [RCP/4][threads] (int4); this
+  // kernel keeps its offsets in registers and uses only the space after it
+  int4* slot_tab = reinterpret_cast<int4*>(red + KS * NB * Hp);
   auto vat = [&](int b, int j) { return CMP ? j * NB + b : b * Hp + j; };
   const int tid = threadIdx.x, nthr = blockDim.x;
   // Hp is a multiple of 64, so ks is uniform across each wave.
@@ -905,6 +907,7 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
   const float GL = G * L, CG = C + G;
 
   float4 preg[RCP > 0 ? RCP : 1];
+  int ix[RCP > 0 ? RCP : 1];  // CMP: slot row offsets, in registers
   int nslot = 0;  // CMP: slots the wave runs
   // Synapse lane of this thread: (chunk sks, column so). With CMP the lanes
   // are dealt in balanced order (balanced_lane); the owner role below keeps
@@ -919,16 +922,12 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
     so = lane_id - sks * Hp;
     const int cnt = k.ccnt[so];
     nslot = wave_max(cnt > sks ? (cnt - 1 - sks) / KS + 1 : 0);
-    int ix[RCP];
 #pragma unroll
     for (int rr = 0; rr < RCP; ++rr) {
       const long long a = (long long)(sks * RCP + rr) * Hp + so;
       preg[rr] = k.cimg[a];
       ix[rr] = k.cidx[a] * NB * 4;
     }
-#pragma unroll
-    for (int q = 0; q < RCP / 4; ++q)
-      slot_tab[q * nthr + tid] = make_int4(ix[4 * q], ix[4 * q + 1], ix[4 * q + 2], ix[4 * q + 3]);
   }
 
   for (int e = tid; e < NB * Hp; e += blockDim.x) {
@@ -965,9 +964,9 @@ __global__ __launch_bounds__(ode_max_threads(NB)) void ode_fwd_kernel(FwdK k) {
 #pragma unroll
         for (int q = 0; q < RCP / 4; ++q) {
           if (4 * q < nslot) {
-            const int4 of = slot_tab[q * nthr + tid];
-            fwd_synapses_cmp<NB>(preg + 4 * q, vs, of.x, of.y, na, qa);
-            if (4 * q + 2 < nslot) fwd_synapses_cmp<NB>(preg + 4 * q + 2, vs, of.z, of.w, na, qa);
+            fwd_synapses_cmp<NB>(preg + 4 * q, vs, ix[4 * q], ix[4 * q + 1], na, qa);
+            if (4 * q + 2 < nslot)
+              fwd_synapses_cmp<NB>(preg + 4 * q + 2, vs, ix[4 * q + 2], ix[4 * q + 3], na, qa);
           }
         }
       } else {
@@ -1193,7 +1192,7 @@ __device__ __forceinline__ void bwd_load_gout(const BwdK& k, int t, int b0, int 
 // to dL/dv (the parameter gradients come from rec_grad_kernel over every
 // synapse). Thread (o, ks) holds the entries ks, ks + KS, ... of column o,
 // alpha/beta sit in LDS as [Hp][NB], and the slot row offsets come from an
-// LDS table [RCP/4][threads] of int4, as in the forward.
+// LDS table [RCP/4][threads] of int4.
 template <int NB, int RCP, bool FUSE>
 __global__ __launch_bounds__(ode_max_threads(NB)) void ode_bwd_kernel(BwdK k) {
   static_assert(!FUSE || RCP > 0, "fused gradients need register-resident operands");
